@@ -1,0 +1,143 @@
+/*
+ * pi05_w4a4.h -- C ABI of the MI355X (gfx950) W4A4 prefix-LM GEMM library
+ * (libpi05_w4a4.so, built by hipcc --offload-arch=gfx950).
+ *
+ * The library replaces the pybind module that the reference JIT-builds from
+ * pi05_fast/w4a4/csrc/int4_gemm.cu (PYBIND11_MODULE at int4_gemm.cu:644-650).  The
+ * host mirror of the reference's op surface (pi05_fast.w4a4.extension) binds these
+ * symbols through ctypes.  Signatures carry plain device pointers, sizes and a HIP
+ * stream (as void*), never torch types.  The library allocates no device memory:
+ * outputs, quantized activations and workspaces are allocated by the caller.
+ *
+ * Every entry point returns a status code (PI05W4A4_OK on success).  A non-zero code
+ * comes with a message retrievable through pi05w4a4_last_error() (thread-local).
+ * Kernels are launched asynchronously on `stream`; nothing synchronises the host.
+ *
+ * Data formats
+ *   x      fp16 [M, K] row-major activations (K % 64 == 0).
+ *   q      int32 [M, K/8] nibble-packed activation codes: element k of a row is
+ *          nibble (k & 7) of word k >> 3, two's complement, values in [-7, 7].
+ *   sa     fp32 [M] per-token activation scales.
+ *   w_mfma weights in the gfx950 MFMA-fragment-major layout (see
+ *          pi05w4a4_repack_weight).  N % 16 == 0.  Word count pi05w4a4_mfma_words().
+ *   y      fp16 [M, N] row-major outputs.
+ */
+#ifndef PI05_W4A4_H_
+#define PI05_W4A4_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PI05W4A4_OK 0
+#define PI05W4A4_EINVAL 1     /* invalid argument (shape, alignment, null pointer) */
+#define PI05W4A4_EHIP 2       /* HIP runtime / launch error */
+#define PI05W4A4_EWORKSPACE 3 /* workspace too small */
+
+/* Source layouts accepted by pi05w4a4_repack_weight. */
+#define PI05W4A4_LAYOUT_ROW_MAJOR 0 /* L1 [N, K/8+1] / L2 [N, K/8+P]: row stride = src_stride */
+#define PI05W4A4_LAYOUT_WMMA_TILED 1 /* L3 [N, K/8+9] read flat: flat[(t*N+n)*2+h] = L1[n,2t+h] */
+
+/* Extra words per row of the persistent MFMA tensor [N, K/8 + 16] ("MFMA marker stride"). */
+#define PI05W4A4_MFMA_MARKER_WORDS 16
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pi05w4a4_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* pi05w4a4_last_error(void);
+
+/*
+ * Fused Walsh-Hadamard rotation + per-token symmetric INT4 quantization + nibble pack.
+ * Replaces quantize_x / quant_rot_rb / quant_rows (int4_gemm.cu:396-477, 496-531).
+ * Rotation iff K in {1024, 2048, 16384} (unnormalised Sylvester FWHT, staged in fp32);
+ * sdiv = amax/7 + 1e-12; q = clamp(rint(x'/sdiv), -7, 7);
+ * sa = sdiv * fp32(1/sqrt(K)) when rotated, else sdiv.
+ */
+int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                      void* stream);
+
+/*
+ * Words of the MFMA-fragment-major weight buffer for an [N, K] weight: payload
+ * N*K/8 words followed by N fp32 scale words.  Equals N * (K/8 + 1).  The persistent
+ * tensor form is int32 [N, K/8 + PI05W4A4_MFMA_MARKER_WORDS] (the extra words are zero).
+ */
+size_t pi05w4a4_mfma_words(int32_t n, int32_t k);
+
+/*
+ * One-time weight repack into the MFMA-fragment-major layout.
+ * Replaces the reference's load-time layout handling: row padding (apply.py:68-69),
+ * preshuffle_wmma_weight (pack.py:45-68) and the kernel-side addressing
+ * weight_word_offset / weight_scale_offset (int4_gemm.cu:44-61).
+ *   src        device int32 weights in `src_layout`;
+ *   src_stride row stride in words for PI05W4A4_LAYOUT_ROW_MAJOR (>= K/8 + 1), ignored
+ *              for PI05W4A4_LAYOUT_WMMA_TILED;
+ *   dst        device buffer of at least pi05w4a4_mfma_words(n, k) int32 words.
+ * Layout of dst, for 16-column block nb, 64-deep k block kb, lane L in [0, 64), word j
+ * in {0, 1}: dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j];
+ * then dst[N*K/8 + n] = scale bits of column n.
+ */
+int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
+                           int64_t src_stride, int32_t* dst, void* stream);
+
+/*
+ * Exact workspace bytes that pi05w4a4_gemm / _gemm_multi (gelu = 0) or
+ * pi05w4a4_gemm_gelu_up (gelu = 1, ngroups = 2, n = {N, N}) need for an (M, K)
+ * activation against weights of n[0..ngroups-1] columns.  0 means no workspace.
+ * The workspace holds split-K int32 partial sums; it is fully overwritten by each call
+ * (no zeroing needed), so calls that share one workspace must be stream-ordered.
+ */
+size_t pi05w4a4_gemm_workspace_bytes(int64_t m, int32_t k, int32_t ngroups, const int32_t* n,
+                                     int32_t gelu);
+
+/*
+ * y = fp16((float(acc) * sa[m]) * sw[n]), acc[m,n] = sum_k q[m,k] * w[n,k] in int32.
+ * Replaces gemm_from_q + gemm_iu4 / gemm_iu4_shape (int4_gemm.cu:63-394, 566-616).
+ */
+int pi05w4a4_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                  const int32_t* w_mfma, int32_t n, void* y_fp16, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/*
+ * Shared-activation GEMM against 1..3 weights of equal K in one launch
+ * (the fan-out of int4_gemm2 / int4_gemm3, int4_gemm.cu:626-642).
+ * w_mfma[g], n[g], y_fp16[g] for g < ngroups.
+ */
+int pi05w4a4_gemm_multi(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                        int32_t ngroups, const int32_t* const* w_mfma, const int32_t* n,
+                        void* const* y_fp16, void* workspace, size_t workspace_bytes,
+                        void* stream);
+
+/*
+ * Fused gate/up GEMM with a GELU-tanh(gate) * up epilogue: h = fp16(gelu_tanh(g) * u)
+ * where g, u are the fp16-rounded gate/up outputs.  Replaces the int4_gemm2 call plus
+ * the elementwise `act_fn(gate) * up` of apply.py:135-138 (one rounding fewer).
+ */
+int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                          const int32_t* w_gate_mfma, const int32_t* w_up_mfma, int32_t n,
+                          void* h_fp16, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Raw int32 accumulators acc[m, n] (row-major [M, N]) for bit-exact checks; no dequant.
+ * Debug counterpart of the int32 accumulation inside gemm_iu4 (int4_gemm.cu:114-178).
+ */
+int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_mfma,
+                      int32_t n, int32_t* acc, void* stream);
+
+/*
+ * Convenience: quantize + GEMM(s), mirroring the reference's host entry points
+ * int4_gemm / int4_gemm2 / int4_gemm3 (int4_gemm.cu:618-642) for MFMA-layout weights.
+ * `qbuf` must hold M*K/8 int32 words and `sabuf` M floats.
+ */
+int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
+                       int32_t n, void* y_fp16, int32_t* qbuf, float* sabuf, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PI05_W4A4_H_ */

@@ -1,0 +1,71 @@
+#!/usr/bin/env python3
+"""Build ``pi05_fast/w4a4/_lib/libpi05_w4a4.so`` with hipcc for gfx950 (in-tree).
+
+    python pi05-pytorch-fast_amd/build_lib.py [--arch gfx950] [--verbose]
+
+One hipcc invocation compiles the HIP translation units under ``csrc/`` into a
+position-independent shared library exporting the C ABI of ``include/pi05_w4a4.h``.
+The library links only the HIP runtime (no torch headers or libraries).
+"""
+
+from __future__ import annotations
+
+import argparse
+import os
+import shlex
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_ROOT = Path(__file__).resolve().parent
+CSRC = PKG_ROOT / "csrc"
+SOURCES = ["quant_rot.hip", "repack.hip", "gemm.hip", "capi.hip"]
+OUT = PKG_ROOT / "pi05_fast" / "w4a4" / "_lib" / "libpi05_w4a4.so"
+
+
+def hipcc() -> str:
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    return str(Path(rocm) / "bin" / "hipcc")
+
+
+def build(arch: str = "gfx950", verbose: bool = False) -> Path:
+    OUT.parent.mkdir(parents=True, exist_ok=True)
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [
+        hipcc(),
+        f"--offload-arch={arch}",
+        "-O3",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        # Packed-fp32 instructions are kept out of the generated code on purpose.
+        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+        "-Wall",
+        "-o", str(tmp),
+    ] + [str(CSRC / s) for s in SOURCES]
+    extra = shlex.split(os.environ.get("PI05_W4A4_EXTRA_CFLAGS", ""))
+    cmd[1:1] = extra
+    if verbose:
+        print(" ".join(shlex.quote(c) for c in cmd), flush=True)
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    diag = "\n".join(l for l in (proc.stdout + proc.stderr).splitlines() if noise not in l)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{diag}")
+    if diag.strip() and verbose:
+        print(diag, flush=True)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--arch", default=os.environ.get("PYTORCH_ROCM_ARCH", "gfx950"))
+    ap.add_argument("--verbose", action="store_true")
+    args = ap.parse_args()
+    out = build(args.arch, args.verbose)
+    print(f"built {out}")
+
+
+if __name__ == "__main__":
+    sys.exit(main())

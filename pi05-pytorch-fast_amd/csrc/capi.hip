@@ -1,0 +1,300 @@
+// extern "C" entry points of libpi05_w4a4.so (declared in include/pi05_w4a4.h).
+//
+// Host-side responsibilities mirror the reference's host glue
+// (pi05_fast/w4a4/csrc/int4_gemm.cu:479-642): argument validation, the
+// quantize-once / GEMM-many fan-out and shape-based kernel dispatch.  Unlike the
+// reference, nothing here allocates device memory: the caller passes the outputs,
+// the quantized-activation buffers and the split-K workspace.
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/pi05_w4a4.h"
+#include "w4a4_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return PI05W4A4_OK;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess)
+    return fail(PI05W4A4_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+constexpr int kNumCUs = 256;  // MI355X: 8 XCDs x 32 CUs
+
+struct TileCfg {
+  int id, mi, ni;
+};
+constexpr TileCfg kCfgs[] = {{0, 7, 4}, {1, 7, 2}, {2, 4, 2}, {3, 2, 2}, {4, 1, 2}};
+
+struct Plan {
+  TileCfg cfg;
+  int64_t mtiles;
+  int64_t ntiles;
+  int ksplit;
+  int kstages;
+};
+
+// Tile configuration, tile counts and K split for one call.
+Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
+  Plan pl{};
+  if (m <= 16)
+    pl.cfg = kCfgs[4];
+  else if (m <= 32)
+    pl.cfg = kCfgs[3];
+  else if (m <= 64)
+    pl.cfg = kCfgs[2];
+  else
+    pl.cfg = kCfgs[0];
+  auto count_tiles = [&](const TileCfg& c) {
+    int64_t t = 0;
+    if (gelu) {
+      t = cdiv(n[0], 32 * c.ni);
+    } else {
+      for (int g = 0; g < ngroups; ++g) t += cdiv(n[g], 64 * c.ni);
+    }
+    return t;
+  };
+  pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
+  pl.ntiles = count_tiles(pl.cfg);
+  if (pl.cfg.id == 0 && pl.mtiles * pl.ntiles < 2 * kNumCUs) {
+    pl.cfg = kCfgs[1];
+    pl.ntiles = count_tiles(pl.cfg);
+  }
+  const int nst = static_cast<int>(cdiv(k, 128));
+  // |256 * acc| < 2^31 needs <= 65536 k per slice: at most 512 stages per slice.
+  int ks = 1;
+  if (allow_split) {
+    const int64_t base = pl.mtiles * pl.ntiles;
+    if (base < kNumCUs) ks = static_cast<int>(cdiv(kNumCUs, base));
+    if (ks > w4a4::kMaxKSplit) ks = w4a4::kMaxKSplit;
+  }
+  if (ks > nst) ks = nst;
+  if (ks < 1) ks = 1;
+  int stages = static_cast<int>(cdiv(nst, ks));
+  if (stages > 512) stages = 512;
+  pl.kstages = stages;
+  pl.ksplit = static_cast<int>(cdiv(nst, stages));
+  return pl;
+}
+
+int validate_gemm_common(const int32_t* q, const float* sa, int64_t m, int32_t k) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  if (m > 0 && (q == nullptr || sa == nullptr))
+    return fail(PI05W4A4_EINVAL, "null activation codes or scales");
+  if (!aligned(q, 16)) return fail(PI05W4A4_EINVAL, "activation codes must be 16-byte aligned");
+  if (!aligned(sa, 4)) return fail(PI05W4A4_EINVAL, "activation scales must be 4-byte aligned");
+  return PI05W4A4_OK;
+}
+
+int validate_weight(const int32_t* w, int32_t n, const char* name) {
+  if (w == nullptr) return fail(PI05W4A4_EINVAL, "%s is null", name);
+  if (n <= 0 || n % 16 != 0)
+    return fail(PI05W4A4_EINVAL, "%s: N must be a positive multiple of 16, got %d", name, n);
+  if (!aligned(w, 8)) return fail(PI05W4A4_EINVAL, "%s must be 8-byte aligned", name);
+  return PI05W4A4_OK;
+}
+
+int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroups,
+             const int32_t* const* w, const int32_t* n, void* const* y, int mode,
+             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const bool gelu = mode == w4a4::kEpiGeluUp;
+  const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc);
+  if (pl.mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
+  w4a4::GemmParams p{};
+  p.q = q;
+  p.sa = sa;
+  p.m = m;
+  p.k = k;
+  p.ngroups = ngroups;
+  int64_t n_total = 0;
+  int tile_begin = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    p.g[g].w = w[g];
+    p.g[g].y = y[g];
+    p.g[g].n = n[g];
+    p.g[g].tile_begin = tile_begin;
+    tile_begin += static_cast<int>(cdiv(n[g], 64 * pl.cfg.ni));
+    n_total += n[g];
+  }
+  p.ntiles = static_cast<int32_t>(pl.ntiles);
+  p.mtiles = static_cast<int32_t>(pl.mtiles);
+  p.ksplit = pl.ksplit;
+  p.kstages_per_split = pl.kstages;
+  p.n_total = static_cast<int32_t>(n_total);
+  p.gelu_pair_n = gelu ? n[0] : 0;
+  if (pl.ksplit > 1) {
+    const size_t need = static_cast<size_t>(pl.ksplit) * static_cast<size_t>(m) *
+                        static_cast<size_t>(n_total) * sizeof(int32_t);
+    if (workspace == nullptr || workspace_bytes < need)
+      return fail(PI05W4A4_EWORKSPACE, "workspace too small: need %zu bytes, got %zu", need,
+                  workspace_bytes);
+    if (!aligned(workspace, 16)) return fail(PI05W4A4_EINVAL, "workspace must be 16-byte aligned");
+    p.partial = static_cast<int32_t*>(workspace);
+    p.mode = w4a4::kEpiPartial;
+    hipError_t e = w4a4::launch_gemm(p, pl.cfg.id, stream);
+    if (e != hipSuccess) return hip_status(e, "gemm launch");
+    p.mode = gelu ? w4a4::kEpiGeluUp : w4a4::kEpiFp16;
+    return hip_status(w4a4::launch_splitk_reduce(p, stream), "split-K reduce launch");
+  }
+  p.mode = mode;
+  return hip_status(w4a4::launch_gemm(p, pl.cfg.id, stream), "gemm launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int pi05w4a4_version(void) { return 100; }
+
+const char* pi05w4a4_last_error(void) { return g_last_error.c_str(); }
+
+int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                      void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  if (m == 0) return ok();
+  if (x_fp16 == nullptr || q == nullptr || sa == nullptr)
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!aligned(x_fp16, 16) || !aligned(q, 16) || !aligned(sa, 4))
+    return fail(PI05W4A4_EINVAL, "x and q must be 16-byte aligned, sa 4-byte aligned");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  const float inv_sqrt_k = static_cast<float>(1.0 / std::sqrt(static_cast<double>(k)));
+  return hip_status(w4a4::launch_quantize(x_fp16, m, k, q, sa, inv_sqrt_k,
+                                          static_cast<hipStream_t>(stream)),
+                    "quantize launch");
+}
+
+size_t pi05w4a4_mfma_words(int32_t n, int32_t k) {
+  if (n <= 0 || k <= 0) return 0;
+  return static_cast<size_t>(n) * (static_cast<size_t>(k) / 8 + 1);
+}
+
+int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
+                           int64_t src_stride, int32_t* dst, void* stream) {
+  if (src == nullptr || dst == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  if (n <= 0 || n % 16 != 0)
+    return fail(PI05W4A4_EINVAL, "N must be a positive multiple of 16, got %d", n);
+  if (src_layout == PI05W4A4_LAYOUT_ROW_MAJOR) {
+    if (src_stride < k / 8 + 1)
+      return fail(PI05W4A4_EINVAL,
+                  "row stride must contain K/8 packed words plus a scale (%lld < %d)",
+                  (long long)src_stride, k / 8 + 1);
+  } else if (src_layout != PI05W4A4_LAYOUT_WMMA_TILED) {
+    return fail(PI05W4A4_EINVAL, "unknown source layout %d", src_layout);
+  }
+  return hip_status(w4a4::launch_repack(src, src_layout, n, k, src_stride, dst,
+                                        static_cast<hipStream_t>(stream)),
+                    "repack launch");
+}
+
+size_t pi05w4a4_gemm_workspace_bytes(int64_t m, int32_t k, int32_t ngroups, const int32_t* n,
+                                     int32_t gelu) {
+  if (m <= 0 || k <= 0 || ngroups < 1 || ngroups > w4a4::kMaxGroups || n == nullptr) return 0;
+  const Plan pl = make_plan(m, k, ngroups, n, gelu != 0, true);
+  if (pl.ksplit <= 1) return 0;
+  int64_t n_total = 0;
+  for (int g = 0; g < ngroups; ++g) n_total += n[g];
+  return static_cast<size_t>(pl.ksplit) * static_cast<size_t>(m) * static_cast<size_t>(n_total) *
+         sizeof(int32_t);
+}
+
+int pi05w4a4_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                  const int32_t* w_mfma, int32_t n, void* y_fp16, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  const int32_t* ws[1] = {w_mfma};
+  const int32_t ns[1] = {n};
+  void* ys[1] = {y_fp16};
+  return pi05w4a4_gemm_multi(q, sa, m, k, 1, ws, ns, ys, workspace, workspace_bytes, stream);
+}
+
+int pi05w4a4_gemm_multi(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                        int32_t ngroups, const int32_t* const* w_mfma, const int32_t* n,
+                        void* const* y_fp16, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  int rc = validate_gemm_common(q, sa, m, k);
+  if (rc) return rc;
+  if (ngroups < 1 || ngroups > w4a4::kMaxGroups || w_mfma == nullptr || n == nullptr ||
+      y_fp16 == nullptr)
+    return fail(PI05W4A4_EINVAL, "ngroups must be 1..3 with non-null arrays");
+  for (int g = 0; g < ngroups; ++g) {
+    rc = validate_weight(w_mfma[g], n[g], "weight");
+    if (rc) return rc;
+    if (m > 0 && y_fp16[g] == nullptr) return fail(PI05W4A4_EINVAL, "null output");
+    if (!aligned(y_fp16[g], 2)) return fail(PI05W4A4_EINVAL, "output must be 2-byte aligned");
+  }
+  if (m == 0) return ok();
+  return run_gemm(q, sa, m, k, ngroups, w_mfma, n, y_fp16, w4a4::kEpiFp16, workspace,
+                  workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                          const int32_t* w_gate_mfma, const int32_t* w_up_mfma, int32_t n,
+                          void* h_fp16, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_gemm_common(q, sa, m, k);
+  if (rc) return rc;
+  rc = validate_weight(w_gate_mfma, n, "gate weight");
+  if (rc) return rc;
+  rc = validate_weight(w_up_mfma, n, "up weight");
+  if (rc) return rc;
+  if (m > 0 && h_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null output");
+  if (m == 0) return ok();
+  const int32_t* ws[2] = {w_gate_mfma, w_up_mfma};
+  const int32_t ns[2] = {n, n};
+  void* ys[2] = {h_fp16, h_fp16};
+  return run_gemm(q, sa, m, k, 2, ws, ns, ys, w4a4::kEpiGeluUp, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream));
+}
+
+int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_mfma,
+                      int32_t n, int32_t* acc, void* stream) {
+  static const float kDummy = 0.0f;
+  int rc = validate_gemm_common(q, &kDummy, m, k);
+  if (rc) return rc;
+  if (k > 65536) return fail(PI05W4A4_EINVAL, "accumulator readout supports K <= 65536");
+  rc = validate_weight(w_mfma, n, "weight");
+  if (rc) return rc;
+  if (m > 0 && acc == nullptr) return fail(PI05W4A4_EINVAL, "null accumulator output");
+  if (!aligned(acc, 4)) return fail(PI05W4A4_EINVAL, "accumulator output must be 4-byte aligned");
+  if (m == 0) return ok();
+  const int32_t* ws[1] = {w_mfma};
+  const int32_t ns[1] = {n};
+  void* ys[1] = {acc};
+  return run_gemm(q, nullptr, m, k, 1, ws, ns, ys, w4a4::kEpiAcc, nullptr, 0,
+                  static_cast<hipStream_t>(stream));
+}
+
+int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
+                       int32_t n, void* y_fp16, int32_t* qbuf, float* sabuf, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  int rc = pi05w4a4_quantize(x_fp16, m, k, qbuf, sabuf, stream);
+  if (rc) return rc;
+  return pi05w4a4_gemm(qbuf, sabuf, m, k, w_mfma, n, y_fp16, workspace, workspace_bytes, stream);
+}
+
+}  // extern "C"

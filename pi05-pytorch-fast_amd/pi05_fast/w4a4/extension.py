@@ -1,0 +1,400 @@
+"""W4A4 INT4 GEMM ops for MI355X (gfx950) as torch custom ops (torch.compile friendly).
+
+Mirrors the reference op surface of ``pi05_fast/w4a4/extension.py`` (lines 15-178):
+the ``torch.ops.pi05_w4a4.{int4_gemm, int4_gemm_tiled, int4_gemm2, int4_gemm2_tiled,
+int4_gemm3}`` custom ops with shape-only fake implementations, the Python wrappers of
+the same names, ``load_int4_gemm()`` and ``preload()``.  The op bodies call the
+hipcc-built C-ABI library ``_lib/libpi05_w4a4.so`` (``include/pi05_w4a4.h``) through
+ctypes, on the current torch stream, with torch-allocated outputs and temporaries.
+
+Validation and error messages follow the reference's TORCH_CHECKs
+(``pi05_fast/w4a4/csrc/int4_gemm.cu:487-501, 570-577``); they surface as RuntimeError.
+
+Weight layouts accepted (the reference's marker-stride convention):
+  * row-major ``[N, K/8+1]`` (L1) or row-padded ``[N, K/8+P]`` (L2) -- repacked into a
+    temporary MFMA-layout buffer on every call (slow path, kept for drop-in use);
+  * WMMA-tiled ``[N, K/8+9]`` (L3) -- ``*_tiled`` ops, repacked per call likewise;
+  * MFMA-fragment-major ``[N, K/8+16]`` -- produced once by ``repack_weight`` (and by
+    ``apply.replace_linears_from_packed`` at load), consumed directly (fast path).
+
+There is no CPU fallback: without the library (or without a GPU) the ops raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import torch
+
+MFMA_MARKER_WORDS = 16
+WMMA_MARKER_WORDS = 9
+
+_LAYOUT_ROW_MAJOR = 0
+_LAYOUT_WMMA_TILED = 1
+
+_LIB_NAME = "libpi05_w4a4.so"
+_lib = None
+_op_registered = False
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Optional observer used by benchmarks: called as hook(kind, "begin"/"end") around the
+# GEMM launches of an op (kind in {"gemm", "gemm2", "gemm3", "gemm2_gelu"}).
+_launch_hook = None
+
+
+def library_path() -> Path:
+    override = os.environ.get("PI05_W4A4_LIB")
+    if override:
+        return Path(override)
+    return Path(__file__).resolve().parent / "_lib" / _LIB_NAME
+
+
+def load_int4_gemm():
+    """Load the gfx950 C-ABI library (the reference JIT-built a pybind module here)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    path = library_path()
+    if not path.is_file():
+        raise RuntimeError(
+            f"W4A4 HIP library not found at {path}; build it first "
+            "(python -c 'import __graft_entry__ as g; g.build()' from the repository root)"
+        )
+    lib = ctypes.CDLL(str(path))
+    vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
+    sig = {
+        "pi05w4a4_version": (ctypes.c_int, []),
+        "pi05w4a4_last_error": (ctypes.c_char_p, []),
+        "pi05w4a4_quantize": (ctypes.c_int, [vp, i64, i32, vp, vp, vp]),
+        "pi05w4a4_mfma_words": (sz, [i32, i32]),
+        "pi05w4a4_repack_weight": (ctypes.c_int, [vp, i32, i32, i32, i64, vp, vp]),
+        "pi05w4a4_gemm_workspace_bytes": (sz, [i64, i32, i32, vp, i32]),
+        "pi05w4a4_gemm": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, sz, vp]),
+        "pi05w4a4_gemm_multi": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, vp, vp, vp, sz, vp]),
+        "pi05w4a4_gemm_gelu_up": (ctypes.c_int, [vp, vp, i64, i32, vp, vp, i32, vp, vp, sz, vp]),
+        "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
+        "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_int4_gemm().pi05w4a4_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")
+
+
+def _stream(device: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
+    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Split-K workspace cached per (device, stream); fully overwritten by every call."""
+    if nbytes <= 0:
+        return None
+    key = (device.index if device.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(device).cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+# ----------------------------------------------------------------------------- checks
+def _check_x(x: torch.Tensor) -> int:
+    """quantize_x preconditions (int4_gemm.cu:497-501)."""
+    if not x.is_cuda:
+        raise RuntimeError("int4_gemm expects CUDA/HIP tensors")
+    if x.dtype != torch.float16:
+        raise RuntimeError("int4_gemm activations must be float16")
+    if x.dim() == 0 or x.size(-1) <= 0:
+        raise RuntimeError("Expected x.size(-1) > 0 to be true, but got false.")
+    k = int(x.size(-1))
+    if k % 64 != 0:
+        raise RuntimeError(f"K must be a multiple of 64, got {k}")
+    return k
+
+
+def _check_packed(w: torch.Tensor, k: int, name: str = "packed W") -> None:
+    """check_packed (int4_gemm.cu:487-494)."""
+    if not w.is_cuda:
+        raise RuntimeError(f"{name} must be on CUDA/HIP")
+    if w.dtype != torch.int32 or w.dim() != 2:
+        raise RuntimeError(f"{name} must be int32 [N, K/8+1]")
+    if w.size(1) < k // 8 + 1:
+        raise RuntimeError(f"{name} second dim must contain K/8 packed words plus a scale")
+
+
+def _check_tiled(w: torch.Tensor, k: int) -> None:
+    """Tiled-layout checks of gemm_from_q<true> (int4_gemm.cu:570-577)."""
+    n = int(w.size(0))
+    if w.size(1) == k // 8 + MFMA_MARKER_WORDS and n % 16 == 0:
+        return  # already MFMA-fragment-major: accepted by the tiled ops as well
+    if not (k == 2048 and n == 16384):
+        raise RuntimeError("WMMA-fragment-major weights currently support only K=2048, N=16384")
+    if w.size(1) != k // 8 + WMMA_MARKER_WORDS:
+        raise RuntimeError("WMMA-fragment-major weights must use the K/8+9 marker stride")
+
+
+def is_mfma_layout(w: torch.Tensor, k: int) -> bool:
+    return w.dim() == 2 and w.size(1) == k // 8 + MFMA_MARKER_WORDS and w.size(0) % 16 == 0
+
+
+# ----------------------------------------------------------------------------- pieces
+def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Fused FWHT + per-token INT4 quant + nibble pack: x fp16 [..., K] -> (q int32 [M, K/8],
+    sa fp32 [M]) (the reference's quantize_x, int4_gemm.cu:496-531)."""
+    k = _check_x(x)
+    x2 = x.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    m = x2.numel() // k
+    q = torch.empty((m, k // 8), dtype=torch.int32, device=x2.device)
+    sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
+    lib = load_int4_gemm()
+    with torch.cuda.device(x2.device):
+        _check(lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device)),
+               "pi05w4a4_quantize")
+    return q, sa
+
+
+def repack_weight(w: torch.Tensor, k: int | None = None, tiled: bool | None = None) -> torch.Tensor:
+    """Repack an L1/L2 (row-major) or L3 (WMMA-tiled, [N, K/8+9]) packed weight into the
+    MFMA-fragment-major tensor int32 [N, K/8+16].  N must be a multiple of 16.
+
+    ``k`` defaults to (size(1)-1)*8 for row-major input and (size(1)-9)*8 for tiled input.
+    ``tiled`` defaults to the K/8+9 marker-stride convention (pack.py:45-50).
+    """
+    if not w.is_cuda:
+        raise RuntimeError("packed W must be on CUDA/HIP")
+    if w.dtype != torch.int32 or w.dim() != 2:
+        raise RuntimeError("packed W must be int32 [N, K/8+1]")
+    n = int(w.size(0))
+    if tiled is None:
+        tiled = k is not None and w.size(1) == k // 8 + WMMA_MARKER_WORDS
+    if k is None:
+        k = (int(w.size(1)) - (WMMA_MARKER_WORDS if tiled else 1)) * 8
+    if k % 64 != 0:
+        raise RuntimeError(f"K must be a multiple of 64, got {k}")
+    if n % 16 != 0:
+        raise RuntimeError(f"MFMA layout needs N % 16 == 0, got N={n}")
+    src = w.contiguous()
+    if not tiled and src.size(1) < k // 8 + 1:
+        raise RuntimeError("packed W second dim must contain K/8 packed words plus a scale")
+    out = torch.zeros((n, k // 8 + MFMA_MARKER_WORDS), dtype=torch.int32, device=w.device)
+    lib = load_int4_gemm()
+    layout = _LAYOUT_WMMA_TILED if tiled else _LAYOUT_ROW_MAJOR
+    with torch.cuda.device(w.device):
+        _check(lib.pi05w4a4_repack_weight(_ptr(src), layout, n, k, int(src.size(1)), _ptr(out),
+                                          _stream(w.device)), "pi05w4a4_repack_weight")
+    return out
+
+
+def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
+    """Weight in MFMA layout (converting per call when needed) and its true N."""
+    n = int(w.size(0))
+    if is_mfma_layout(w, k):
+        return w, n
+    if tiled:
+        return repack_weight(w, k, tiled=True), n
+    if n % 16 != 0:
+        pad = 16 - n % 16
+        w = torch.nn.functional.pad(w.contiguous(), (0, 0, 0, pad))
+    return repack_weight(w, k, tiled=False), n
+
+
+def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
+    """Shared-activation GEMMs of 1..3 MFMA-layout weights (one launch)."""
+    lib = load_int4_gemm()
+    m = int(q.size(0))
+    ns = [int(w.size(0)) for (w, _) in weights]
+    if gelu:
+        n = ns[0]
+        outs = [torch.empty((m, n), dtype=torch.float16, device=device)]
+        out_ptrs = [outs[0], outs[0]]
+    else:
+        outs = [torch.empty((m, nn), dtype=torch.float16, device=device) for nn in ns]
+        out_ptrs = outs
+    g = len(weights)
+    n_arr = (ctypes.c_int32 * g)(*ns)
+    ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0)
+    ws = _workspace(device, ws_bytes)
+    stream = _stream(device)
+    if _launch_hook is not None:
+        _launch_hook(kind, "begin")
+    if gelu:
+        rc = lib.pi05w4a4_gemm_gelu_up(_ptr(q), _ptr(sa), m, k, _ptr(weights[0][0]),
+                                       _ptr(weights[1][0]), ns[0], _ptr(outs[0]), _ptr(ws),
+                                       ws_bytes, stream)
+    else:
+        w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for (w, _) in weights])
+        y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in out_ptrs])
+        rc = lib.pi05w4a4_gemm_multi(_ptr(q), _ptr(sa), m, k, g, w_arr, n_arr, y_arr, _ptr(ws),
+                                     ws_bytes, stream)
+    if _launch_hook is not None:
+        _launch_hook(kind, "end")
+    _check(rc, "pi05w4a4_gemm")
+    results = []
+    for o, (w, n_true) in zip(outs, weights):
+        if o.size(1) != n_true:
+            o = o[:, :n_true].contiguous()
+        results.append(o.view(*out_shape_prefix, n_true))
+    return results
+
+
+def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False):
+    k = _check_x(x)
+    q, sa = quantize(x)  # the reference quantizes before checking the weights
+    conv = []
+    for w in ws:
+        _check_packed(w, k)
+        if tiled:
+            _check_tiled(w, k)
+        conv.append(_as_mfma(w, k, tiled))
+    with torch.cuda.device(x.device):
+        return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), x.device, kind, gelu=gelu)
+
+
+# ----------------------------------------------------------------------------- custom ops
+def _register_custom_op() -> None:
+    global _op_registered
+    if _op_registered:
+        return
+    try:
+        torch.ops.pi05_w4a4.int4_gemm2_gelu
+        _op_registered = True
+        return
+    except (AttributeError, RuntimeError):
+        pass
+
+    def _fake_out(x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+        return torch.empty(*x.shape[:-1], packed.shape[0], device=x.device, dtype=torch.float16)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm", mutates_args=())
+    def _int4_gemm(x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+        return _run(x, [packed], tiled=False, kind="gemm")[0]
+
+    @_int4_gemm.register_fake
+    def _int4_gemm_fake(x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+        return _fake_out(x, packed)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm_tiled", mutates_args=())
+    def _int4_gemm_tiled(x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+        return _run(x, [packed], tiled=True, kind="gemm")[0]
+
+    @_int4_gemm_tiled.register_fake
+    def _int4_gemm_tiled_fake(x: torch.Tensor, packed: torch.Tensor) -> torch.Tensor:
+        return _fake_out(x, packed)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm2", mutates_args=())
+    def _int4_gemm2(
+        x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        a, b = _run(x, [w0, w1], tiled=False, kind="gemm2")
+        return a, b
+
+    @_int4_gemm2.register_fake
+    def _int4_gemm2_fake(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor):
+        return _fake_out(x, w0), _fake_out(x, w1)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm2_tiled", mutates_args=())
+    def _int4_gemm2_tiled(
+        x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        a, b = _run(x, [w0, w1], tiled=True, kind="gemm2")
+        return a, b
+
+    @_int4_gemm2_tiled.register_fake
+    def _int4_gemm2_tiled_fake(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor):
+        return _fake_out(x, w0), _fake_out(x, w1)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm3", mutates_args=())
+    def _int4_gemm3(
+        x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        a, b, c = _run(x, [w0, w1, w2], tiled=False, kind="gemm3")
+        return a, b, c
+
+    @_int4_gemm3.register_fake
+    def _int4_gemm3_fake(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor):
+        return _fake_out(x, w0), _fake_out(x, w1), _fake_out(x, w2)
+
+    # Not in the reference: gate/up GEMMs with the GELU-tanh(gate) * up epilogue fused.
+    @torch.library.custom_op("pi05_w4a4::int4_gemm2_gelu", mutates_args=())
+    def _int4_gemm2_gelu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+        if w_gate.shape != w_up.shape:
+            raise RuntimeError("gate and up weights must have the same shape")
+        return _run(x, [w_gate, w_up], tiled=False, kind="gemm2_gelu", gelu=True)[0]
+
+    @_int4_gemm2_gelu.register_fake
+    def _int4_gemm2_gelu_fake(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor):
+        return _fake_out(x, w_gate)
+
+    _op_registered = True
+
+
+_register_custom_op()
+
+
+def int4_gemm(x: torch.Tensor, packed_w: torch.Tensor) -> torch.Tensor:
+    """Compiled-graph-friendly INT4 GEMM. x: fp16 [..., K], packed: int32 [N, K/8+1|+P|+16]."""
+    return torch.ops.pi05_w4a4.int4_gemm(x, packed_w)
+
+
+def int4_gemm_tiled(x: torch.Tensor, packed_w: torch.Tensor) -> torch.Tensor:
+    """INT4 GEMM with fragment-major weights (WMMA-tiled K/8+9 or MFMA K/8+16)."""
+    return torch.ops.pi05_w4a4.int4_gemm_tiled(x, packed_w)
+
+
+def int4_gemm2(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Shared activation quant plus two INT4 GEMMs (one launch)."""
+    return torch.ops.pi05_w4a4.int4_gemm2(x, w0, w1)
+
+
+def int4_gemm2_tiled(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Shared activation quant plus two fragment-major INT4 GEMMs."""
+    return torch.ops.pi05_w4a4.int4_gemm2_tiled(x, w0, w1)
+
+
+def int4_gemm3(
+    x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Shared activation quant plus three INT4 GEMMs (QKV, one launch)."""
+    return torch.ops.pi05_w4a4.int4_gemm3(x, w0, w1, w2)
+
+
+def int4_gemm2_gelu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """h = gelu_tanh(x @ W_gate^T) * (x @ W_up^T) with one shared activation quant."""
+    return torch.ops.pi05_w4a4.int4_gemm2_gelu(x, w_gate, w_up)
+
+
+def int4_gemm_acc(x: torch.Tensor, packed_w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Debug: (int32 accumulators [M, N], codes q [M, K/8], scales sa [M]) for bit-exact checks."""
+    k = _check_x(x)
+    _check_packed(packed_w, k)
+    q, sa = quantize(x)
+    w, n_true = _as_mfma(packed_w, k, tiled=packed_w.size(1) == k // 8 + WMMA_MARKER_WORDS)
+    m = int(q.size(0))
+    acc = torch.empty((m, int(w.size(0))), dtype=torch.int32, device=x.device)
+    lib = load_int4_gemm()
+    with torch.cuda.device(x.device):
+        _check(lib.pi05w4a4_gemm_acc(_ptr(q), m, k, _ptr(w), int(w.size(0)), _ptr(acc),
+                                     _stream(x.device)), "pi05w4a4_gemm_acc")
+    return acc[:, :n_true], q, sa
+
+
+def preload() -> None:
+    """Load the HIP library before torch.compile traces the graph."""
+    load_int4_gemm()
+    _register_custom_op()

@@ -1,0 +1,206 @@
+"""Offline INT4 weight packing and the packed formats (CPU, torch).
+
+API mirror of the reference's ``pi05_fast/w4a4/pack.py``: the same function names,
+argument meanings and on-disk/in-memory formats (Hadamard on K in {1024, 2048, 16384},
+INT4 codes in [-7, 7], ``[N, K/8+1]`` int32 rows with the fp32 scale bits in word K/8).
+Adds the gfx950 MFMA-fragment-major layout (``pack_mfma_weight`` /
+``unpack_mfma_weight``) so weights can be packed straight into the layout the MI355X
+kernels read.
+
+Everything here is offline / CPU code.  The GPU ops never call into this module.
+``quant_activation_cpu`` and ``int4_gemm_ref`` are the reference's exported CPU
+reference functions, kept for API compatibility.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+ROTATE_K = frozenset({1024, 2048, 16384})
+WMMA_PRESHUFFLE_PAD_WORDS = 9
+MFMA_MARKER_WORDS = 16
+
+
+def fwht_unnormalized(x: torch.Tensor) -> torch.Tensor:
+    """Unnormalised Sylvester Walsh-Hadamard transform along the last dim (pack.py:18-31).
+
+    Radix-2 stages of stride h = 1, 2, 4, ...; each stage maps the pair (i, i+h) with bit
+    h of i clear to (a + b, a - b).
+    """
+    n = x.shape[-1]
+    if n <= 0 or (n & (n - 1)) != 0:
+        raise ValueError(f"FWHT length must be a power of 2, got {n}")
+    lead = x.shape[:-1]
+    y = x.contiguous().clone()
+    h = 1
+    while h < n:
+        pairs = y.view(*lead, n // (2 * h), 2, h)
+        lo, hi = pairs.unbind(dim=-2)
+        y = torch.stack((lo + hi, lo - hi), dim=-2).reshape(*lead, n)
+        h *= 2
+    return y
+
+
+def pack_nibbles(q: torch.Tensor) -> torch.Tensor:
+    """codes [..., K] in [-8, 7] -> int32 [..., K/8]; element 8p+j in bits 4j..4j+3 (pack.py:34-42)."""
+    if q.shape[-1] % 8 != 0:
+        raise ValueError(f"K must be a multiple of 8, got {q.shape[-1]}")
+    nib = (q.to(torch.int32) & 0xF).view(*q.shape[:-1], q.shape[-1] // 8, 8)
+    word = torch.zeros(nib.shape[:-1], dtype=torch.int32, device=nib.device)
+    for j in range(8):
+        word = word | (nib[..., j] << (4 * j))
+    return word
+
+
+def unpack_nibbles(packed: torch.Tensor, k: int) -> torch.Tensor:
+    """int32 [..., K/8] -> int32 codes [..., K]; nibble >= 8 is value - 16 (pack.py:71-76)."""
+    shifts = torch.arange(0, 32, 4, dtype=torch.int32, device=packed.device)
+    nib = (packed.to(torch.int32).unsqueeze(-1) >> shifts) & 0xF
+    q = torch.where(nib >= 8, nib - 16, nib)
+    return q.reshape(*packed.shape[:-1], k)
+
+
+def should_rotate(k: int, rotate: bool | None = None) -> bool:
+    """Rotation iff K in {1024, 2048, 16384} unless forced (pack.py:79-82)."""
+    if rotate is not None:
+        return bool(rotate)
+    return k in ROTATE_K
+
+
+def pack_linear_weight(weight: torch.Tensor, rotate: bool | None = None) -> torch.Tensor:
+    """Linear.weight [N, K] -> int32 [N, K/8+1] (pack.py:85-101).
+
+    W' = FWHT(W) * fp32(1/sqrt(K)) when rotating; s = max(amax(|W'|), 1e-12) / 7;
+    codes = clamp(round_half_even(W' / s), -7, 7); word K/8 holds the fp32 bits of s.
+    """
+    if weight.dim() != 2:
+        raise ValueError(f"expected 2D weight, got {tuple(weight.shape)}")
+    n, k = weight.shape
+    if k % 64 != 0:
+        raise ValueError(f"K must be a multiple of 64 for gemm_iu4, got {k}")
+    w = weight.detach().to(device="cpu", dtype=torch.float32)
+    if should_rotate(k, rotate):
+        w = fwht_unnormalized(w) * (1.0 / math.sqrt(k))
+    scale = w.abs().amax(dim=-1).clamp_min(1e-12) / 7.0
+    codes = torch.round(w / scale[:, None]).clamp(-7, 7).to(torch.int32)
+    return torch.cat([pack_nibbles(codes), scale.contiguous().view(torch.int32)[:, None]], dim=1)
+
+
+def unpack_linear_weight(packed: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, int]:
+    """int32 [N, K/8+1] -> (codes [N, K], scale fp32 [N], K) (pack.py:104-110)."""
+    _, row = packed.shape
+    k = (row - 1) * 8
+    codes = unpack_nibbles(packed[:, :-1], k)
+    scale = packed[:, -1].contiguous().view(torch.float32)
+    return codes, scale, k
+
+
+def preshuffle_wmma_weight(packed: torch.Tensor, k: int) -> torch.Tensor:
+    """Layout L3 (pack.py:45-68): flat[(t*N + n)*2 + h] = L1[n, 2t + h], then the N scales,
+    in an int32 [N, K/8+9] tensor (the ninth pad word is the layout marker)."""
+    if packed.dim() != 2:
+        raise ValueError(f"expected 2D packed weight, got {tuple(packed.shape)}")
+    n = packed.shape[0]
+    words = k // 8
+    if k % 16 != 0 or packed.shape[1] < words + 1:
+        raise ValueError(f"invalid packed weight shape {tuple(packed.shape)} for K={k}")
+    out = torch.zeros((n, words + WMMA_PRESHUFFLE_PAD_WORDS), dtype=packed.dtype, device=packed.device)
+    flat = out.view(-1)
+    flat[: n * words] = packed[:, :words].reshape(n, words // 2, 2).transpose(0, 1).reshape(-1)
+    flat[n * words : n * words + n] = packed[:, words]
+    return out
+
+
+def mfma_word_permutation(n: int, k: int, device: torch.device | str = "cpu") -> torch.Tensor:
+    """Index map of the MFMA-fragment-major layout: dst_word -> L1 word index n*(K/8) + kw.
+
+    dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j]
+    (the B operand of v_mfma_i32_16x16x64_i8 for a 16-column, 64-deep block).
+    """
+    if n % 16 != 0 or k % 64 != 0:
+        raise ValueError(f"MFMA layout needs N % 16 == 0 and K % 64 == 0, got N={n}, K={k}")
+    kw_total = k // 8
+    idx = torch.arange(n * kw_total, dtype=torch.int64, device=device)
+    j = idx & 1
+    lane = (idx >> 1) & 63
+    blk = idx >> 7
+    kb = blk % (k // 64)
+    nb = blk // (k // 64)
+    col = nb * 16 + (lane & 15)
+    kw = kb * 8 + 2 * (lane >> 4) + j
+    return col * kw_total + kw
+
+
+def pack_mfma_weight(packed: torch.Tensor, k: int | None = None) -> torch.Tensor:
+    """L1/L2 packed weight -> MFMA-fragment-major int32 [N, K/8+16] (CPU/offline form of the
+    device repack)."""
+    n = packed.shape[0]
+    if k is None:
+        k = (packed.shape[1] - 1) * 8
+    words = k // 8
+    payload = packed[:, :words].contiguous().view(-1)
+    perm = mfma_word_permutation(n, k, packed.device)
+    out = torch.zeros((n, words + MFMA_MARKER_WORDS), dtype=torch.int32, device=packed.device)
+    flat = out.view(-1)
+    flat[: n * words] = payload[perm]
+    flat[n * words : n * words + n] = packed[:, words]
+    return out
+
+
+def unpack_mfma_weight(mfma: torch.Tensor, k: int) -> torch.Tensor:
+    """Inverse of ``pack_mfma_weight``: MFMA layout -> L1 [N, K/8+1]."""
+    n = mfma.shape[0]
+    words = k // 8
+    flat = mfma.contiguous().view(-1)
+    perm = mfma_word_permutation(n, k, mfma.device)
+    payload = torch.empty(n * words, dtype=torch.int32, device=mfma.device)
+    payload[perm] = flat[: n * words]
+    return torch.cat([payload.view(n, words), flat[n * words : n * words + n, None]], dim=1)
+
+
+def quant_activation_cpu(x: torch.Tensor, rotate: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """CPU statement of the activation quant (pack.py:113-131): x [M, K] -> (codes [M, K], scale [M]).
+
+    sdiv = amax/7 + 1e-12; codes = clamp(round_half_even(x'/sdiv), -7, 7);
+    scale = sdiv * fp32(1/sqrt(K)) when rotating, else sdiv.
+    """
+    if x.dim() != 2:
+        raise ValueError("quant_activation_cpu expects [M, K]")
+    _, k = x.shape
+    xf = x.detach().float()
+    rot = should_rotate(k, rotate)
+    if rot:
+        xf = fwht_unnormalized(xf)
+    sdiv = xf.abs().amax(dim=-1) / 7.0 + 1e-12
+    scale = sdiv * (1.0 / math.sqrt(k)) if rot else sdiv
+    codes = torch.round(xf / sdiv[:, None]).clamp(-7, 7).to(torch.int32)
+    return codes, scale
+
+
+def int4_gemm_ref(x: torch.Tensor, packed_w: torch.Tensor, rotate: bool | None = None) -> torch.Tensor:
+    """CPU reference of one W4A4 linear (pack.py:134-145): fp32 matmul of the codes (exact,
+    |acc| < 2^24), then (acc * s_a) * s_w rounded to fp16."""
+    lead = x.shape[:-1]
+    k = x.shape[-1]
+    q_a, s_a = quant_activation_cpu(x.reshape(-1, k), rotate=rotate)
+    q_w, s_w, k_w = unpack_linear_weight(packed_w)
+    if k_w != k:
+        raise ValueError(f"K mismatch act={k} weight={k_w}")
+    acc = q_a.float() @ q_w.float().T
+    y = acc * s_a[:, None] * s_w[None, :]
+    return y.reshape(*lead, packed_w.shape[0]).to(torch.float16)
+
+
+def layer_meta(name: str, packed: torch.Tensor, rotate: bool, has_bias: bool) -> dict[str, Any]:
+    """Per-layer entry of meta.json (pack.py:148-157)."""
+    n, row = packed.shape
+    return {
+        "name": name,
+        "in_features": (row - 1) * 8,
+        "out_features": n,
+        "rotate": rotate,
+        "has_bias": has_bias,
+    }
