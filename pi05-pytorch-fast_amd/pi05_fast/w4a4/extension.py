@@ -37,9 +37,9 @@ _LAYOUT_WMMA_TILED = 1
 _LIB_NAME = "libpi05_w4a4.so"
 _lib = None
 _op_registered = False
-_workspaces: dict[tuple[int, int], torch.Tensor] = {}
-# Optional observer used by benchmarks: called as hook(kind, "begin"/"end") around the
-# GEMM launches of an op (kind in {"gemm", "gemm2", "gemm3", "gemm2_gelu"}).
+# Optional observer used by benchmarks: called as hook(kind, phase, m, k, ns) with phase
+# "begin"/"end" around the GEMM launches of an op (after its activation quant), kind in
+# {"gemm", "gemm2", "gemm3", "gemm2_gelu"}, ns the output widths of the weights.
 _launch_hook = None
 
 
@@ -99,16 +99,11 @@ def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Split-K workspace cached per (device, stream); fully overwritten by every call."""
+    """Split-K workspace for one call.  Every call overwrites it completely (no zeroing),
+    so a fresh block from the caching allocator is enough, also under graph capture."""
     if nbytes <= 0:
         return None
-    key = (device.index if device.index is not None else torch.cuda.current_device(),
-           torch.cuda.current_stream(device).cuda_stream)
-    ws = _workspaces.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
-        _workspaces[key] = ws
-    return ws
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 # ----------------------------------------------------------------------------- checks
@@ -130,6 +125,10 @@ def _check_packed(w: torch.Tensor, k: int, name: str = "packed W") -> None:
     """check_packed (int4_gemm.cu:487-494)."""
     if not w.is_cuda:
         raise RuntimeError(f"{name} must be on CUDA/HIP")
+    _check_packed_shape(w, k, name)
+
+
+def _check_packed_shape(w: torch.Tensor, k: int, name: str = "packed W") -> None:
     if w.dtype != torch.int32 or w.dim() != 2:
         raise RuntimeError(f"{name} must be int32 [N, K/8+1]")
     if w.size(1) < k // 8 + 1:
@@ -164,8 +163,12 @@ def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
     lib = load_int4_gemm()
     with torch.cuda.device(x2.device):
-        _check(lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device)),
-               "pi05w4a4_quantize")
+        if _launch_hook is not None:
+            _launch_hook("quant", "begin", m, k, [])
+        rc = lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device))
+        if _launch_hook is not None:
+            _launch_hook("quant", "end", m, k, [])
+        _check(rc, "pi05w4a4_quantize")
     return q, sa
 
 
@@ -232,7 +235,7 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
     ws = _workspace(device, ws_bytes)
     stream = _stream(device)
     if _launch_hook is not None:
-        _launch_hook(kind, "begin")
+        _launch_hook(kind, "begin", m, k, ns)
     if gelu:
         rc = lib.pi05w4a4_gemm_gelu_up(_ptr(q), _ptr(sa), m, k, _ptr(weights[0][0]),
                                        _ptr(weights[1][0]), ns[0], _ptr(outs[0]), _ptr(ws),
@@ -243,7 +246,7 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
         rc = lib.pi05w4a4_gemm_multi(_ptr(q), _ptr(sa), m, k, g, w_arr, n_arr, y_arr, _ptr(ws),
                                      ws_bytes, stream)
     if _launch_hook is not None:
-        _launch_hook(kind, "end")
+        _launch_hook(kind, "end", m, k, ns)
     _check(rc, "pi05w4a4_gemm")
     results = []
     for o, (w, n_true) in zip(outs, weights):

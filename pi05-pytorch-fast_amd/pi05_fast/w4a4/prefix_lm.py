@@ -155,7 +155,7 @@ def build_prefix_lm(
                 norm.weight.copy_(torch.randn(norm.weight.shape, generator=cpu_gen) * 0.05)
     layers = layers.to(device=device, dtype=torch.float16)
     norm = GemmaRMSNorm(cfg.hidden_size, eps=cfg.rms_norm_eps).to(device=device, dtype=torch.float16)
-    rotary = GemmaRotaryEmbedding(cfg, device=device)
+    rotary = GemmaRotaryEmbedding(cfg).to(device)
     model = PrefixLM(cfg, layers, norm, rotary).eval()
     if fuse:
         fuse_shared_activation_quant(model)

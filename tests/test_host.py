@@ -1,0 +1,329 @@
+"""Host-side logic of the W4A4 package and the C ABI boundary -- CPU only (no GPU calls).
+
+* The package's packer / CPU reference API (pi05_fast.w4a4.pack) against the golden
+  vectors and the oracle.
+* Layout transforms: WMMA preshuffle round trip (the reference's CPU test,
+  tests/test_w4a4.py:24-42) and the MFMA-fragment-major permutation.
+* The C-ABI library loads and exports every symbol include/pi05_w4a4.h declares; its
+  argument validation rejects bad calls before touching the GPU.
+* The custom ops are registered under the reference's names with shape-only fakes;
+  host-side checks raise the reference's messages.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4a4_oracle as orc
+from tests import w4a4_inputs as inp
+from tests.conftest import ROOT
+
+
+@pytest.fixture(scope="module")
+def pack():
+    from pi05_fast.w4a4 import pack as p
+
+    return p
+
+
+# ----------------------------------------------------------------------------- packer API
+@pytest.mark.parametrize("shape", [(8, 64), (8, 192), (8, 1024), (16, 2048), (2, 16384)])
+def test_pack_linear_weight_matches_golden(golden, pack, shape):
+    n, k = shape
+    got = pack.pack_linear_weight(torch.from_numpy(golden[f"w_in_{n}x{k}"]))
+    assert np.array_equal(got.numpy(), golden[f"w_packed_{n}x{k}"])
+
+
+@pytest.mark.parametrize("k", [64, 192, 512, 1024, 2048, 16384])
+def test_quant_activation_cpu_matches_golden(golden, pack, k):
+    q, s = pack.quant_activation_cpu(torch.from_numpy(golden[f"act_x_{k}"]))
+    assert np.array_equal(q.numpy(), golden[f"act_q_{k}"])
+    assert np.array_equal(s.numpy().view(np.int32), golden[f"act_s_{k}"].view(np.int32))
+
+
+@pytest.mark.parametrize("m,n,k", [(6, 8, 64), (8, 16, 2048), (4, 2, 16384), (6, 8, 1024)])
+def test_int4_gemm_ref_matches_golden(golden, pack, m, n, k):
+    y = pack.int4_gemm_ref(torch.from_numpy(golden[f"act_x_{k}"][:m]),
+                           torch.from_numpy(golden[f"w_packed_{n}x{k}"]))
+    assert np.array_equal(y.numpy().view(np.int16), golden[f"gemm_y_{m}x{n}x{k}"].view(np.int16))
+
+
+def test_nibbles_match_golden(golden, pack):
+    assert np.array_equal(pack.pack_nibbles(torch.from_numpy(golden["nib_codes"])).numpy(),
+                          golden["nib_packed"])
+    assert np.array_equal(pack.unpack_nibbles(torch.from_numpy(golden["nib_words"]), 40).numpy(),
+                          golden["nib_unpacked"])
+
+
+def test_fwht_matches_golden(golden, pack):
+    for n in (8, 64, 2048):
+        got = pack.fwht_unnormalized(torch.from_numpy(golden[f"fwht_in_{n}"])).numpy()
+        assert np.array_equal(got.view(np.int32), golden[f"fwht_out_{n}"].view(np.int32))
+
+
+# ----------------------------------------------------------------------------- layouts
+def test_payload_and_scales_round_trip(pack):
+    """The reference's PreshuffleLayoutTest (tests/test_w4a4.py:24-42)."""
+    n, k = 7, 64
+    packed = inp.random_packed(inp.generator(1), n, k)
+    tiled = pack.preshuffle_wmma_weight(packed, k)
+    words = k // 8
+    flat = tiled.view(-1)
+    restored_payload = flat[: n * words].view(words // 2, n, 2).permute(1, 0, 2).reshape(n, words)
+    restored_scales = flat[n * words : n * words + n]
+    assert tuple(tiled.shape) == (n, words + 9)
+    assert torch.equal(restored_payload, packed[:, :words])
+    assert torch.equal(restored_scales, packed[:, words])
+    assert np.array_equal(tiled.numpy(), orc.preshuffle_wmma_weight(packed.numpy(), k))
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (32, 192), (48, 2048)])
+def test_mfma_layout_definition(pack, n, k):
+    """dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j]."""
+    packed = inp.random_packed(inp.generator(n + k), n, k)
+    mf = pack.pack_mfma_weight(packed, k)
+    assert tuple(mf.shape) == (n, k // 8 + pack.MFMA_MARKER_WORDS)
+    flat = mf.view(-1).numpy()
+    l1 = packed.numpy()
+    kb64 = k // 64
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        nb, kb, lane, j = (int(rng.integers(0, n // 16)), int(rng.integers(0, kb64)),
+                           int(rng.integers(0, 64)), int(rng.integers(0, 2)))
+        dst = ((nb * kb64 + kb) * 64 + lane) * 2 + j
+        assert flat[dst] == l1[16 * nb + lane % 16, 8 * kb + 2 * (lane // 16) + j]
+    assert np.array_equal(flat[n * (k // 8) : n * (k // 8) + n], l1[:, k // 8])
+    assert np.all(flat[n * (k // 8) + n :] == 0)
+    assert torch.equal(pack.unpack_mfma_weight(mf, k), packed)
+
+
+def test_mfma_layout_rejects_bad_shapes(pack):
+    with pytest.raises(ValueError):
+        pack.mfma_word_permutation(8, 64)
+    with pytest.raises(ValueError):
+        pack.mfma_word_permutation(16, 96)
+
+
+# ----------------------------------------------------------------------------- C ABI
+HEADER = ROOT / "include" / "pi05_w4a4.h"
+
+
+def _declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(pi05w4a4_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from pi05_fast.w4a4 import extension
+
+    path = extension.library_path()
+    if not path.is_file():
+        pytest.fail(f"{path} is not built (run __graft_entry__.build())")
+    return extension.load_int4_gemm()
+
+
+def test_library_exports_every_declared_symbol(lib):
+    syms = _declared_symbols()
+    assert len(syms) >= 10
+    raw = ctypes.CDLL(str(lib._name))
+    missing = [s for s in syms if not hasattr(raw, s)]
+    assert not missing, f"missing exports: {missing}"
+
+
+def test_library_version_and_sizes(lib):
+    assert lib.pi05w4a4_version() >= 100
+    assert lib.pi05w4a4_mfma_words(2048, 2048) == 2048 * (2048 // 8 + 1)
+    assert lib.pi05w4a4_mfma_words(0, 64) == 0
+
+
+def test_workspace_sizing(lib):
+    n1 = (ctypes.c_int32 * 1)(2048)
+    ws_down = lib.pi05w4a4_gemm_workspace_bytes(776, 16384, 1, n1, 0)
+    assert ws_down % (776 * 2048 * 4) == 0
+    n2 = (ctypes.c_int32 * 2)(16384, 16384)
+    assert lib.pi05w4a4_gemm_workspace_bytes(776, 2048, 2, n2, 0) == 0  # enough tiles: no split
+    assert lib.pi05w4a4_gemm_workspace_bytes(0, 2048, 1, n1, 0) == 0
+
+
+def _err(lib) -> str:
+    return lib.pi05w4a4_last_error().decode()
+
+
+def test_abi_validation_without_gpu(lib):
+    vp = ctypes.c_void_p
+    # K not a multiple of 64
+    assert lib.pi05w4a4_quantize(vp(16), 4, 100, vp(16), vp(16), vp(0)) == 1
+    assert "multiple of 64" in _err(lib)
+    # null pointers
+    assert lib.pi05w4a4_quantize(vp(0), 4, 128, vp(16), vp(16), vp(0)) == 1
+    # misaligned activations
+    assert lib.pi05w4a4_quantize(vp(18), 4, 128, vp(16), vp(16), vp(0)) == 1
+    assert "aligned" in _err(lib)
+    # M == 0 is a no-op success
+    assert lib.pi05w4a4_quantize(vp(0), 0, 128, vp(0), vp(0), vp(0)) == 0
+    # repack: N not a multiple of 16, short row stride, bad layout
+    assert lib.pi05w4a4_repack_weight(vp(16), 0, 7, 64, 9, vp(16), vp(0)) == 1
+    assert lib.pi05w4a4_repack_weight(vp(16), 0, 16, 64, 8, vp(16), vp(0)) == 1
+    assert "scale" in _err(lib)
+    assert lib.pi05w4a4_repack_weight(vp(16), 5, 16, 64, 9, vp(16), vp(0)) == 1
+    # gemm: bad ngroups, misaligned codes, bad N
+    n1 = (ctypes.c_int32 * 1)(16)
+    w1 = (ctypes.c_void_p * 1)(16)
+    y1 = (ctypes.c_void_p * 1)(16)
+    assert lib.pi05w4a4_gemm_multi(vp(16), vp(16), 4, 64, 4, w1, n1, y1, vp(0), 0, vp(0)) == 1
+    assert lib.pi05w4a4_gemm_multi(vp(20), vp(16), 4, 64, 1, w1, n1, y1, vp(0), 0, vp(0)) == 1
+    assert lib.pi05w4a4_gemm(vp(16), vp(16), 4, 64, vp(16), 24, vp(16), vp(0), 0, vp(0)) == 1
+    assert "multiple of 16" in _err(lib)
+    # accumulator readout limited to K <= 65536
+    assert lib.pi05w4a4_gemm_acc(vp(16), 4, 131072, vp(16), 16, vp(16), vp(0)) == 1
+    # M == 0 GEMM is a no-op success
+    assert lib.pi05w4a4_gemm(vp(16), vp(16), 0, 64, vp(16), 16, vp(0), vp(0), 0, vp(0)) == 0
+
+
+# ----------------------------------------------------------------------------- op surface
+def test_custom_ops_registered_with_fakes():
+    from pi05_fast.w4a4 import extension  # noqa: F401
+
+    for name in ("int4_gemm", "int4_gemm_tiled", "int4_gemm2", "int4_gemm2_tiled", "int4_gemm3",
+                 "int4_gemm2_gelu"):
+        assert hasattr(torch.ops.pi05_w4a4, name)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    with FakeTensorMode():
+        x = torch.empty(2, 776, 2048, dtype=torch.float16)
+        w = torch.empty(2560, 2048 // 8 + 16, dtype=torch.int32)
+        y = torch.ops.pi05_w4a4.int4_gemm(x, w)
+        assert tuple(y.shape) == (2, 776, 2560) and y.dtype == torch.float16
+        a, b, c = torch.ops.pi05_w4a4.int4_gemm3(x, w, w[:256], w[:256])
+        assert tuple(b.shape) == (2, 776, 256)
+        g, u = torch.ops.pi05_w4a4.int4_gemm2_tiled(x, w, w)
+        assert tuple(u.shape) == (2, 776, 2560)
+
+
+def test_ops_reject_cpu_tensors_with_reference_message():
+    from pi05_fast.w4a4 import extension
+
+    x = torch.zeros(3, 2048, dtype=torch.float16)
+    w = torch.zeros(16, 2048 // 8 + 1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="int4_gemm expects CUDA/HIP tensors"):
+        extension.int4_gemm(x, w)
+    with pytest.raises(RuntimeError, match="int4_gemm expects CUDA/HIP tensors"):
+        extension.int4_gemm3(x, w, w, w)
+
+
+def test_host_checks_messages():
+    from pi05_fast.w4a4 import extension as ext
+
+    meta = lambda *s, dt: torch.empty(*s, dtype=dt, device="meta")  # noqa: E731
+    # packed weight checks (check_packed, int4_gemm.cu:487-494) on shape/dtype only
+    with pytest.raises(RuntimeError, match="packed W must be int32 \\[N, K/8\\+1\\]"):
+        ext._check_packed_shape(meta(16, 257, dt=torch.float32), 2048)
+    with pytest.raises(RuntimeError, match="must be int32"):
+        ext._check_packed_shape(meta(16, 257, 1, dt=torch.int32), 2048)
+    with pytest.raises(RuntimeError, match="second dim must contain K/8 packed words plus a scale"):
+        ext._check_packed_shape(meta(16, 256, dt=torch.int32), 2048)
+    ext._check_packed_shape(meta(16, 257, dt=torch.int32), 2048)
+    with pytest.raises(RuntimeError, match="must be on CUDA/HIP"):
+        ext._check_packed(meta(16, 257, dt=torch.int32), 2048)
+    w_row = meta(16384, 2048 // 8 + 1, dt=torch.int32)
+    with pytest.raises(RuntimeError, match="K/8\\+9 marker stride"):
+        ext._check_tiled(w_row, 2048)
+    with pytest.raises(RuntimeError, match="only K=2048, N=16384"):
+        ext._check_tiled(meta(128, 2048 // 8 + 9, dt=torch.int32), 2048)
+    ext._check_tiled(meta(16384, 2048 // 8 + 9, dt=torch.int32), 2048)
+    ext._check_tiled(meta(256, 2048 // 8 + 16, dt=torch.int32), 2048)  # MFMA accepted
+    assert ext.is_mfma_layout(meta(256, 2048 // 8 + 16, dt=torch.int32), 2048)
+    assert not ext.is_mfma_layout(meta(256, 2048 // 8 + 8, dt=torch.int32), 2048)
+
+
+def test_library_missing_fails_loudly(monkeypatch, tmp_path):
+    from pi05_fast.w4a4 import extension
+
+    monkeypatch.setenv("PI05_W4A4_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(extension, "_lib", None)
+    with pytest.raises(RuntimeError, match="HIP library not found"):
+        extension.load_int4_gemm()
+
+
+# ----------------------------------------------------------------------------- module / apply
+def test_w4a4_linear_surface():
+    from pi05_fast.w4a4 import W4A4Linear
+
+    w = inp.random_packed(inp.generator(5), 32, 2048)
+    lin = W4A4Linear(w, in_features=2048)
+    assert lin.in_features == 2048 and lin.out_features == 32 and lin.rotate
+    assert lin.weight.dtype == torch.float16 and lin.weight.numel() == 0
+    assert "packed" in lin.state_dict() and "weight" not in lin.state_dict()
+    with pytest.raises(ValueError, match="K/8\\+9 marker stride"):
+        W4A4Linear(w, in_features=2048, preshuffled=True)
+    with pytest.raises(ValueError, match="too short"):
+        W4A4Linear(w[:, :100], in_features=2048)
+    assert not lin.mfma
+    from pi05_fast.w4a4.pack import pack_mfma_weight
+
+    assert W4A4Linear(pack_mfma_weight(w), in_features=2048).mfma
+
+
+def test_apply_reference_layouts_on_cpu(monkeypatch):
+    from pi05_fast.w4a4.apply import load_time_weight
+
+    w = inp.random_packed(inp.generator(6), 16384, 2048)
+    pre, is_pre = load_time_weight(w, "x.layers.0.mlp.gate_proj", 2048, 16384, None)
+    assert is_pre and tuple(pre.shape) == (16384, 2048 // 8 + 9)
+    pad, is_pre = load_time_weight(w[:256], "x.layers.0.self_attn.k_proj", 2048, 256, None)
+    assert not is_pre and tuple(pad.shape) == (256, 2048 // 8 + 8)
+    monkeypatch.setenv("PI05_W4A4_ROW_PAD_WORDS", "16")
+    with pytest.raises(ValueError, match="collides"):
+        load_time_weight(w[:256], "x.layers.0.self_attn.k_proj", 2048, 256, None)
+
+
+def test_pack_checkpoint_format(tmp_path):
+    from safetensors.torch import save_file
+
+    from pi05_fast.w4a4.pack_w4a4_prefix import FORMAT, pack_checkpoint, weight_to_module_name
+
+    prefix = "model.paligemma_with_expert.paligemma.model.language_model.layers.0."
+    tensors = {
+        prefix + "self_attn.k_proj.weight": torch.randn(256, 2048) * 0.02,
+        prefix + "mlp.down_proj.weight": torch.randn(64, 16384) * 0.02,
+        prefix + "input_layernorm.weight": torch.zeros(2048),
+        "model.other.weight": torch.zeros(4, 4),
+    }
+    save_file(tensors, str(tmp_path / "model.safetensors"))
+    meta = pack_checkpoint(tmp_path / "model.safetensors", tmp_path / "out")
+    assert meta["format"] == FORMAT == "embedl-int4-gemm-v1"
+    on_disk = json.loads((tmp_path / "out" / "meta.json").read_text())
+    name = "paligemma_with_expert.paligemma.model.language_model.layers.0.self_attn.k_proj"
+    assert on_disk["layers"][name] == {"in_features": 2048, "out_features": 256, "rotate": True,
+                                       "has_bias": False}
+    from safetensors.torch import load_file
+
+    packed = load_file(str(tmp_path / "out" / "packed.safetensors"))
+    want = orc.pack_linear_weight(tensors[prefix + "self_attn.k_proj.weight"].numpy())
+    assert np.array_equal(packed[name + ".packed"].numpy(), want)
+    assert weight_to_module_name(prefix + "input_layernorm.weight") is None
+
+
+def test_prefix_lm_builds_and_fails_loudly_on_cpu():
+    from pi05_fast.w4a4 import W4A4Linear
+    from pi05_fast.w4a4.prefix_lm import build_prefix_lm, prefix_inputs, prefix_ops
+
+    model, weights = build_prefix_lm("cpu", num_layers=1)
+    layer = model.layers[0]
+    for proj in ("q_proj", "k_proj", "v_proj", "o_proj"):
+        assert isinstance(getattr(layer.self_attn, proj), W4A4Linear)
+    for proj in ("gate_proj", "up_proj", "down_proj"):
+        assert isinstance(getattr(layer.mlp, proj), W4A4Linear)
+    assert len(weights) == 7
+    assert layer.mlp.gate_proj.preshuffled  # reference layouts off the GPU
+    with pytest.raises(RuntimeError, match="CUDA/HIP"):
+        model(prefix_inputs(1, 8, "cpu"))
+    ops = prefix_ops(776)
+    assert abs(sum(ops.values()) / 1e9 - 3075.8) < 0.1
