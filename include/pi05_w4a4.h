@@ -14,13 +14,22 @@
  * Kernels are launched asynchronously on `stream`; nothing synchronises the host.
  *
  * Data formats
- *   x      fp16 [M, K] row-major activations (K % 64 == 0).
- *   q      int32 [M, K/8] nibble-packed activation codes: element k of a row is
- *          nibble (k & 7) of word k >> 3, two's complement, values in [-7, 7].
+ *   x      fp16 [M, K] row-major activations (K % 64 == 0), 16-byte aligned.
+ *   q      nibble-packed activation codes (values in [-7, 7], two's complement) in the
+ *          MFMA-fragment-major layout shared with the weights.  With KB = ceil(K/128),
+ *          the codes of 16-row block mb and 128-deep k block b form one 1 KB fragment at
+ *          word (mb*KB + b)*256; its lane L (words 4L .. 4L+3) holds codes
+ *          128*b + 16*(L/16) .. +15 (words 4L, 4L+1) and 128*b + 64 + 16*(L/16) .. +15
+ *          (words 4L+2, 4L+3) of row 16*mb + L%16, code k in nibble (k & 7) of its word.
+ *          Row-major word (row, kw) of the reference's [M, K/8] codes therefore sits at
+ *          ((row/16)*KB + kw/16)*256 + 4*(row%16 + 16*((kw%8)/2)) + 2*((kw/8)%2) + kw%2.
+ *          The buffer holds pi05w4a4_q_words(M, K) words (M rounded up to 16 rows, K to
+ *          128; padding is never read into an output).  16-byte aligned.
  *   sa     fp32 [M] per-token activation scales.
  *   w_mfma weights in the gfx950 MFMA-fragment-major layout (see
  *          pi05w4a4_repack_weight).  N % 16 == 0.  Word count pi05w4a4_mfma_words().
- *   y      fp16 [M, N] row-major outputs.
+ *          16-byte aligned.
+ *   y      fp16 [M, N] row-major outputs, 16-byte aligned.
  */
 #ifndef PI05_W4A4_H_
 #define PI05_W4A4_H_
@@ -61,9 +70,16 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
                       void* stream);
 
 /*
+ * Words of a quantized-activation buffer q for M rows of K codes:
+ * ceil(M/16)*16 * ceil(K/128)*16.
+ * (The reference keeps row-major [M, K/8] codes inside its QuantizedX, int4_gemm.cu:479-485.)
+ */
+size_t pi05w4a4_q_words(int64_t m, int32_t k);
+
+/*
  * Words of the MFMA-fragment-major weight buffer for an [N, K] weight: payload
- * N*K/8 words followed by N fp32 scale words.  Equals N * (K/8 + 1).  The persistent
- * tensor form is int32 [N, K/8 + PI05W4A4_MFMA_MARKER_WORDS] (the extra words are zero).
+ * N*ceil(K/128)*16 words followed by N fp32 scale words.  The persistent tensor form is
+ * int32 [N, K/8 + PI05W4A4_MFMA_MARKER_WORDS], which always holds that many words.
  */
 size_t pi05w4a4_mfma_words(int32_t n, int32_t k);
 
@@ -76,9 +92,9 @@ size_t pi05w4a4_mfma_words(int32_t n, int32_t k);
  *   src_stride row stride in words for PI05W4A4_LAYOUT_ROW_MAJOR (>= K/8 + 1), ignored
  *              for PI05W4A4_LAYOUT_WMMA_TILED;
  *   dst        device buffer of at least pi05w4a4_mfma_words(n, k) int32 words.
- * Layout of dst, for 16-column block nb, 64-deep k block kb, lane L in [0, 64), word j
- * in {0, 1}: dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j];
- * then dst[N*K/8 + n] = scale bits of column n.
+ * Layout of dst: the q layout above applied to weight columns (column n in place of row
+ * `row`), K padded to a multiple of 128 with zero codes, then dst[N*ceil(K/128)*16 + n]
+ * = scale bits of column n.
  */
 int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
                            int64_t src_stride, int32_t* dst, void* stream);
@@ -130,7 +146,7 @@ int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_m
 /*
  * Convenience: quantize + GEMM(s), mirroring the reference's host entry points
  * int4_gemm / int4_gemm2 / int4_gemm3 (int4_gemm.cu:618-642) for MFMA-layout weights.
- * `qbuf` must hold M*K/8 int32 words and `sabuf` M floats.
+ * `qbuf` must hold pi05w4a4_q_words(M, K) int32 words and `sabuf` M floats.
  */
 int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
                        int32_t n, void* y_fp16, int32_t* qbuf, float* sabuf, void* workspace,

@@ -46,58 +46,69 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kNumCUs = 256;  // MI355X: 8 XCDs x 32 CUs
 
 struct TileCfg {
-  int id, mi, ni;
+  int id, mi, ni, kw;  // kw = waves of a workgroup along K (the other 4/kw along N)
+  int cols(bool gelu) const { return (gelu ? 8 : 16) * ni * (4 / kw); }  // workgroup tile width
 };
-constexpr TileCfg kCfgs[] = {{0, 7, 4}, {1, 7, 2}, {2, 4, 2}, {3, 2, 2}, {4, 1, 2}};
+constexpr TileCfg kCfg7x4{w4a4::kCfg7x4, 7, 4, 1};
+constexpr TileCfg kCfg7x4K4{w4a4::kCfg7x4K4, 7, 4, 4};
+constexpr TileCfg kCfg4x2{w4a4::kCfg4x2, 4, 2, 1};
+constexpr TileCfg kCfg2x2{w4a4::kCfg2x2, 2, 2, 1};
+constexpr TileCfg kCfg1x2{w4a4::kCfg1x2, 1, 2, 1};
 
 struct Plan {
   TileCfg cfg;
   int64_t mtiles;
   int64_t ntiles;
   int ksplit;
-  int kstages;
+  int kblocks;
 };
 
 // Tile configuration, tile counts and K split for one call.
+//  * M > 64: 112-row tiles (MI = 7: 776 = 7 x 112 - 8).  Wide GEMMs (gate/up) use 4 waves
+//    along N (112 x 256 workgroup tiles); when that leaves fewer than 1.5 workgroups per
+//    CU (QKV, o, down) the 4 waves split K instead (112 x 64 tiles, 4x the workgroups).
+//  * Small M: narrower tiles; the remaining parallelism comes from a global K split.
 Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
   Plan pl{};
   if (m <= 16)
-    pl.cfg = kCfgs[4];
+    pl.cfg = kCfg1x2;
   else if (m <= 32)
-    pl.cfg = kCfgs[3];
+    pl.cfg = kCfg2x2;
   else if (m <= 64)
-    pl.cfg = kCfgs[2];
+    pl.cfg = kCfg4x2;
   else
-    pl.cfg = kCfgs[0];
+    pl.cfg = kCfg7x4;
   auto count_tiles = [&](const TileCfg& c) {
     int64_t t = 0;
     if (gelu) {
-      t = cdiv(n[0], 32 * c.ni);
+      t = cdiv(n[0], c.cols(true));
     } else {
-      for (int g = 0; g < ngroups; ++g) t += cdiv(n[g], 64 * c.ni);
+      for (int g = 0; g < ngroups; ++g) t += cdiv(n[g], c.cols(false));
     }
     return t;
   };
   pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
   pl.ntiles = count_tiles(pl.cfg);
-  if (pl.cfg.id == 0 && pl.mtiles * pl.ntiles < 2 * kNumCUs) {
-    pl.cfg = kCfgs[1];
+  if (pl.cfg.id == w4a4::kCfg7x4 && 2 * pl.mtiles * pl.ntiles < 3 * kNumCUs) {
+    pl.cfg = kCfg7x4K4;
     pl.ntiles = count_tiles(pl.cfg);
   }
-  const int nst = static_cast<int>(cdiv(k, 128));
-  // |256 * acc| < 2^31 needs <= 65536 k per slice: at most 512 stages per slice.
+  const int nkb = w4a4::kblocks128(k);
+  // |256 * acc| < 2^31 needs <= 65536 k per slice: at most 512 k blocks per slice.
   int ks = 1;
   if (allow_split) {
+    // A global split costs an int32 workspace round trip and a reduce launch; it only
+    // pays when fewer than half of the CUs would get a workgroup.
     const int64_t base = pl.mtiles * pl.ntiles;
-    if (base < kNumCUs) ks = static_cast<int>(cdiv(kNumCUs, base));
+    if (2 * base < kNumCUs) ks = static_cast<int>(cdiv(kNumCUs, base));
     if (ks > w4a4::kMaxKSplit) ks = w4a4::kMaxKSplit;
   }
-  if (ks > nst) ks = nst;
+  if (ks > nkb) ks = nkb;
   if (ks < 1) ks = 1;
-  int stages = static_cast<int>(cdiv(nst, ks));
-  if (stages > 512) stages = 512;
-  pl.kstages = stages;
-  pl.ksplit = static_cast<int>(cdiv(nst, stages));
+  int per = static_cast<int>(cdiv(nkb, ks));
+  if (per > 512) per = 512;
+  pl.kblocks = per;
+  pl.ksplit = static_cast<int>(cdiv(nkb, per));
   return pl;
 }
 
@@ -115,7 +126,7 @@ int validate_weight(const int32_t* w, int32_t n, const char* name) {
   if (w == nullptr) return fail(PI05W4A4_EINVAL, "%s is null", name);
   if (n <= 0 || n % 16 != 0)
     return fail(PI05W4A4_EINVAL, "%s: N must be a positive multiple of 16, got %d", name, n);
-  if (!aligned(w, 8)) return fail(PI05W4A4_EINVAL, "%s must be 8-byte aligned", name);
+  if (!aligned(w, 16)) return fail(PI05W4A4_EINVAL, "%s must be 16-byte aligned", name);
   return PI05W4A4_OK;
 }
 
@@ -138,13 +149,14 @@ int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroup
     p.g[g].y = y[g];
     p.g[g].n = n[g];
     p.g[g].tile_begin = tile_begin;
-    tile_begin += static_cast<int>(cdiv(n[g], 64 * pl.cfg.ni));
+    tile_begin += static_cast<int>(cdiv(n[g], pl.cfg.cols(false)));
     n_total += n[g];
   }
   p.ntiles = static_cast<int32_t>(pl.ntiles);
   p.mtiles = static_cast<int32_t>(pl.mtiles);
   p.ksplit = pl.ksplit;
-  p.kstages_per_split = pl.kstages;
+  p.kblocks_per_split = pl.kblocks;
+  p.mblocks = static_cast<int32_t>(cdiv(m, 16));
   p.n_total = static_cast<int32_t>(n_total);
   p.gelu_pair_n = gelu ? n[0] : 0;
   if (pl.ksplit > 1) {
@@ -189,9 +201,14 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
                     "quantize launch");
 }
 
+size_t pi05w4a4_q_words(int64_t m, int32_t k) {
+  if (m <= 0 || k <= 0) return 0;
+  return static_cast<size_t>(cdiv(m, 16) * 16) * static_cast<size_t>(w4a4::kblocks128(k)) * 16;
+}
+
 size_t pi05w4a4_mfma_words(int32_t n, int32_t k) {
   if (n <= 0 || k <= 0) return 0;
-  return static_cast<size_t>(n) * (static_cast<size_t>(k) / 8 + 1);
+  return static_cast<size_t>(n) * (static_cast<size_t>(w4a4::kblocks128(k)) * 16 + 1);
 }
 
 int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
@@ -246,7 +263,7 @@ int pi05w4a4_gemm_multi(const int32_t* q, const float* sa, int64_t m, int32_t k,
     rc = validate_weight(w_mfma[g], n[g], "weight");
     if (rc) return rc;
     if (m > 0 && y_fp16[g] == nullptr) return fail(PI05W4A4_EINVAL, "null output");
-    if (!aligned(y_fp16[g], 2)) return fail(PI05W4A4_EINVAL, "output must be 2-byte aligned");
+    if (!aligned(y_fp16[g], 16)) return fail(PI05W4A4_EINVAL, "output must be 16-byte aligned");
   }
   if (m == 0) return ok();
   return run_gemm(q, sa, m, k, ngroups, w_mfma, n, y_fp16, w4a4::kEpiFp16, workspace,
@@ -263,6 +280,7 @@ int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t 
   rc = validate_weight(w_up_mfma, n, "up weight");
   if (rc) return rc;
   if (m > 0 && h_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null output");
+  if (!aligned(h_fp16, 16)) return fail(PI05W4A4_EINVAL, "output must be 16-byte aligned");
   if (m == 0) return ok();
   const int32_t* ws[2] = {w_gate_mfma, w_up_mfma};
   const int32_t ns[2] = {n, n};

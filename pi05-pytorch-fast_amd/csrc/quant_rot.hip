@@ -10,8 +10,9 @@
 //
 // Work decomposition: one workgroup of T threads per row.  Thread t owns J = K/(8T)
 // chunks of 8 consecutive elements; element i = e + 8*(t + T*j), e in [0,8), j in [0,J).
-// Every chunk is one 16-byte fp16 load and one packed int32 store, so both the load of
-// the row and the store of the codes are fully coalesced.  The radix-2 stages of the
+// Every chunk is one 16-byte fp16 load (the row is read fully coalesced) and one packed
+// int32 store into the fragment-major code layout that the GEMM reads (frag_word_index in
+// w4a4_internal.h).  The radix-2 stages of the
 // unnormalised Sylvester transform run in increasing order of the stride h:
 //   h = 1, 2, 4            inside a chunk (registers),
 //   h = 8 .. 256           across lanes of the wave (lane xor 1..32),
@@ -162,9 +163,8 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
 
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
-  int32_t* qr = q + row * (K / 8);
 #pragma unroll
-  for (int j = 0; j < J; ++j) qr[t + T * j] = quant_pack8(v[j], sdiv);
+  for (int j = 0; j < J; ++j) q[frag_word_index(row, t + T * j, kblocks128(K))] = quant_pack8(v[j], sdiv);
 }
 
 // Unrotated quantization for every other K (K % 64 == 0): int4_gemm.cu:451-477.
@@ -187,13 +187,12 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
   amax = block_max<256>(amax, red);
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (t == 0) sa[row] = sdiv;
-  int32_t* qr = q + row * chunks;
   for (int c = t; c < chunks; c += 256) {
     const half8 h = *reinterpret_cast<const half8*>(xr + 8 * c);
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(h[e]);
-    qr[c] = quant_pack8(v, sdiv);
+    q[frag_word_index(row, c, kblocks128(k))] = quant_pack8(v, sdiv);
   }
 }
 

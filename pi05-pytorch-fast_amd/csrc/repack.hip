@@ -6,12 +6,15 @@
 //   WMMA-tiled L3 [N, K/8+9] read flat: word (n, kw) at ((kw>>1)*N + n)*2 + (kw&1),
 //              scale at N*K/8 + n (pack.py:45-68).
 //
-// Destination (this library's layout): the B operand of v_mfma_i32_16x16x64_i8 for a
-// 16-column block nb and a 64-deep k block kb is one contiguous 512-byte fragment;
-// lane L of the wave reads words 2L, 2L+1 of it, which hold the 16 codes of column
-// 16*nb + L%16 at k = 64*kb + 16*(L/16) .. +15.  Fragments of one column block are
-// consecutive along K, so a wave streams its weights with fully coalesced 8-byte-per-
-// lane loads.  The fp32 column scales follow the payload.
+// Destination (this library's layout, frag_word_index in w4a4_internal.h): for every
+// 16-column block and 128-deep k block one contiguous 1 KB fragment in which lane L of a
+// wave owns 16 bytes: the B operands of column 16*nb + L%16 for the two 64-deep halves of
+// the block.  Fragments of one column block are consecutive along K, so a wave streams
+// its weights with fully coalesced 16-byte-per-lane loads.  K is padded to a multiple of
+// 128 with zero codes; the fp32 column scales follow the payload.
+//
+// One thread per destination word: the writes are coalesced, the reads are gathers from
+// a layout that is only read once (this runs at load time, not per call).
 
 #include "w4a4_internal.h"
 
@@ -21,24 +24,30 @@ namespace {
 __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__ src, int32_t layout,
                                                      int32_t n, int32_t k, int64_t stride,
                                                      int32_t* __restrict__ dst) {
-  const int64_t kw_total = k / 8;
-  const int64_t payload = static_cast<int64_t>(n) * kw_total;
+  const int32_t kw_total = k / 8;
+  const int32_t kb128 = kblocks128(k);
+  const int64_t payload = static_cast<int64_t>(n) * kb128 * 16;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx < payload) {
-    const int64_t pair = idx >> 1;
+    // Invert frag_word_index: idx = (nb*kb128 + kb2)*256 + lane*4 + half*2 + j.
     const int j = static_cast<int>(idx & 1);
-    const int lane = static_cast<int>(pair & 63);
-    const int64_t blk = pair >> 6;
-    const int64_t kb64 = k / 64;
-    const int64_t kb = blk % kb64;
-    const int64_t nb = blk / kb64;
+    const int half = static_cast<int>((idx >> 1) & 1);
+    const int lane = static_cast<int>((idx >> 2) & 63);
+    const int64_t frag = idx >> 8;
+    const int64_t kb2 = frag % kb128;
+    const int64_t nb = frag / kb128;
     const int64_t col = nb * 16 + (lane & 15);
-    const int64_t kw = kb * 8 + 2 * (lane >> 4) + j;
-    const int64_t s = (layout == 0) ? col * stride + kw : ((kw >> 1) * n + col) * 2 + (kw & 1);
-    dst[idx] = src[s];
+    const int64_t kw = kb2 * 16 + half * 8 + 2 * (lane >> 4) + j;
+    int32_t v = 0;
+    if (kw < kw_total) {
+      const int64_t s = (layout == 0) ? col * stride + kw : ((kw >> 1) * n + col) * 2 + (kw & 1);
+      v = src[s];
+    }
+    dst[idx] = v;
   } else if (idx < payload + n) {
     const int64_t col = idx - payload;
-    const int64_t s = (layout == 0) ? col * stride + kw_total : payload + col;
+    const int64_t s = (layout == 0) ? col * stride + kw_total
+                                    : static_cast<int64_t>(n) * kw_total + col;
     dst[idx] = src[s];
   }
 }
@@ -47,7 +56,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__
 
 hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t k,
                          int64_t src_stride, int32_t* dst, hipStream_t stream) {
-  const int64_t total = static_cast<int64_t>(n) * (k / 8) + n;
+  const int64_t total = static_cast<int64_t>(n) * kblocks128(k) * 16 + n;
   const int64_t blocks = (total + 255) / 256;
   repack_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, stream>>>(src, layout, n, k,
                                                                          src_stride, dst);

@@ -19,27 +19,55 @@ enum EpilogueMode : int {
 };
 
 struct GemmGroup {
-  const int32_t* w;  // MFMA-layout payload (scales follow at w + N*K/8)
+  const int32_t* w;  // MFMA-layout payload (scales follow at w + N*kblocks128(K)*16)
   void* y;           // fp16 [M, N] output (or int32 for kEpiAcc)
   int32_t n;         // output columns
   int32_t tile_begin;  // first global n-tile index of this group
 };
 
 struct GemmParams {
-  const int32_t* q;   // int32 [M, K/8]
+  const int32_t* q;   // activation codes, MFMA-fragment-major (frag_word_index)
   const float* sa;    // fp32 [M]
   int64_t m;
+  int32_t mblocks;    // ceil(M / 16): 16-row blocks held by q
   int32_t k;
   int32_t ngroups;
   GemmGroup g[kMaxGroups];
   int32_t ntiles;     // total n-tiles over the groups
   int32_t mtiles;
   int32_t ksplit;     // number of K slices
-  int32_t kstages_per_split;  // 128-deep stages per K slice
+  int32_t kblocks_per_split;  // 128-deep k blocks per K slice
   int32_t mode;
   int32_t* partial;   // workspace for kEpiPartial: [ksplit, M, n_total]
   int32_t n_total;
   int32_t gelu_pair_n;  // for kEpiGeluUp: columns of the gate (= up) weight
+};
+
+// MFMA-fragment-major layout of packed INT4 codes, shared by the weights (r = output
+// column) and the quantized activations (r = row).  The codes of the 16-line block r/16
+// and the 128-deep k block kw/16 form one 1 KB fragment of 256 words; lane L of a wave
+// owns words 4L .. 4L+3 of it: words 4L, 4L+1 hold codes 16*(L/16) .. +15 of the first
+// 64-deep half (the v_mfma_i32_16x16x64_i8 operand of line 16*(r/16) + L%16), words 4L+2,
+// 4L+3 the same codes of the second half.  One 16-byte load per lane fetches the operand
+// pair of a 128-deep k step.  K is padded to a multiple of 128; weight pad codes are 0.
+// Word index of packed word kw (codes 8*kw .. 8*kw+7) of line r, kb128 = ceil(K/128):
+__host__ __device__ inline int64_t frag_word_index(int64_t r, int32_t kw, int32_t kb128) {
+  const int64_t frag = (r >> 4) * kb128 + (kw >> 4);
+  const int lane = static_cast<int>(r & 15) + 16 * ((kw & 7) >> 1);
+  return frag * 256 + lane * 4 + ((kw >> 3) & 1) * 2 + (kw & 1);
+}
+
+__host__ __device__ inline int32_t kblocks128(int32_t k) { return (k + 127) >> 7; }
+
+// GEMM tile configurations: wave tile (16*MI) x (16*NI); K4 = the 4 waves of a
+// workgroup split K (one column block per workgroup) instead of N.
+enum TileCfg : int {
+  kCfg7x4 = 0,    // MI 7, NI 4, 4 waves along N: workgroup tile 112 x 256
+  kCfg7x2 = 1,    // MI 7, NI 2, 4 waves along N: 112 x 128
+  kCfg4x2 = 2,    // MI 4, NI 2: 64 x 128
+  kCfg2x2 = 3,    // MI 2, NI 2: 32 x 128
+  kCfg1x2 = 4,    // MI 1, NI 2: 16 x 128
+  kCfg7x4K4 = 5,  // MI 7, NI 4, 4 waves along K: 112 x 64
 };
 
 // Launchers (return hipError_t of the launch).

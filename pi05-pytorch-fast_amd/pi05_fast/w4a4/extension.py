@@ -67,6 +67,7 @@ def load_int4_gemm():
         "pi05w4a4_version": (ctypes.c_int, []),
         "pi05w4a4_last_error": (ctypes.c_char_p, []),
         "pi05w4a4_quantize": (ctypes.c_int, [vp, i64, i32, vp, vp, vp]),
+        "pi05w4a4_q_words": (sz, [i64, i32]),
         "pi05w4a4_mfma_words": (sz, [i32, i32]),
         "pi05w4a4_repack_weight": (ctypes.c_int, [vp, i32, i32, i32, i64, vp, vp]),
         "pi05w4a4_gemm_workspace_bytes": (sz, [i64, i32, i32, vp, i32]),
@@ -152,14 +153,21 @@ def is_mfma_layout(w: torch.Tensor, k: int) -> bool:
 
 # ----------------------------------------------------------------------------- pieces
 def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Fused FWHT + per-token INT4 quant + nibble pack: x fp16 [..., K] -> (q int32 [M, K/8],
-    sa fp32 [M]) (the reference's quantize_x, int4_gemm.cu:496-531)."""
+    """Fused FWHT + per-token INT4 quant + nibble pack (the reference's quantize_x,
+    int4_gemm.cu:496-531): x fp16 [..., K] -> (q, sa fp32 [M]).
+
+    ``q`` is int32 ``[pi05w4a4_q_words(M, K)]`` holding the codes in the
+    MFMA-fragment-major layout the GEMM reads (``pack.codes_from_fragment_major`` converts
+    it back to the reference's row-major ``[M, K/8]`` words); M is padded to 16 rows and K
+    to 128 codes.
+    """
     k = _check_x(x)
     x2 = x.contiguous()
     if x2.data_ptr() % 16:
         x2 = x2.clone()
     m = x2.numel() // k
-    q = torch.empty((m, k // 8), dtype=torch.int32, device=x2.device)
+    lib = load_int4_gemm()
+    q = torch.empty((int(lib.pi05w4a4_q_words(m, k)),), dtype=torch.int32, device=x2.device)
     sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
     lib = load_int4_gemm()
     with torch.cuda.device(x2.device):
@@ -220,7 +228,7 @@ def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
 def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
     """Shared-activation GEMMs of 1..3 MFMA-layout weights (one launch)."""
     lib = load_int4_gemm()
-    m = int(q.size(0))
+    m = int(sa.size(0))
     ns = [int(w.size(0)) for (w, _) in weights]
     if gelu:
         n = ns[0]
@@ -383,12 +391,13 @@ def int4_gemm2_gelu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -
 
 
 def int4_gemm_acc(x: torch.Tensor, packed_w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Debug: (int32 accumulators [M, N], codes q [M, K/8], scales sa [M]) for bit-exact checks."""
+    """Debug: (int32 accumulators [M, N], codes q (fragment-major, see ``quantize``),
+    scales sa [M]) for bit-exact checks."""
     k = _check_x(x)
     _check_packed(packed_w, k)
     q, sa = quantize(x)
     w, n_true = _as_mfma(packed_w, k, tiled=packed_w.size(1) == k // 8 + WMMA_MARKER_WORDS)
-    m = int(q.size(0))
+    m = int(sa.size(0))
     acc = torch.empty((m, int(w.size(0))), dtype=torch.int32, device=x.device)
     lib = load_int4_gemm()
     with torch.cuda.device(x.device):

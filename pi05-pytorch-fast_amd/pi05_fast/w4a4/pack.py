@@ -114,39 +114,54 @@ def preshuffle_wmma_weight(packed: torch.Tensor, k: int) -> torch.Tensor:
     return out
 
 
-def mfma_word_permutation(n: int, k: int, device: torch.device | str = "cpu") -> torch.Tensor:
-    """Index map of the MFMA-fragment-major layout: dst_word -> L1 word index n*(K/8) + kw.
+def fragment_word_index(lines: int, k: int, device: torch.device | str = "cpu") -> torch.Tensor:
+    """Index map of the MFMA-fragment-major layout of packed INT4 codes, shared by the
+    weights (line = output column) and the quantized activations (line = row).
 
-    dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j]
-    (the B operand of v_mfma_i32_16x16x64_i8 for a 16-column, 64-deep block).
+    Returns int64 [lines, K/8]: row-major packed word (line, kw) -> word of the fragment
+    buffer.  With KB = ceil(K/128), the 16-line block b and 128-deep k block t form one
+    1 KB fragment at word (b*KB + t)*256; lane L (words 4L .. 4L+3) holds the codes
+    16*(L/16) .. +15 of both 64-deep halves of line 16*b + L%16.
     """
+    if k % 64 != 0:
+        raise ValueError(f"K must be a multiple of 64, got {k}")
+    kb128 = (k + 127) // 128
+    r = torch.arange(lines, dtype=torch.int64, device=device)[:, None]
+    kw = torch.arange(k // 8, dtype=torch.int64, device=device)[None, :]
+    frag = (r >> 4) * kb128 + (kw >> 4)
+    lane = (r & 15) + 16 * ((kw & 7) >> 1)
+    return frag * 256 + lane * 4 + ((kw >> 3) & 1) * 2 + (kw & 1)
+
+
+def mfma_payload_words(n: int, k: int) -> int:
+    """Payload words of an MFMA-layout weight (K padded to a multiple of 128)."""
+    return n * ((k + 127) // 128) * 16
+
+
+def mfma_word_permutation(n: int, k: int, device: torch.device | str = "cpu") -> torch.Tensor:
+    """dst payload word -> L1 word index n*(K/8) + kw, or -1 for a zero pad word."""
     if n % 16 != 0 or k % 64 != 0:
         raise ValueError(f"MFMA layout needs N % 16 == 0 and K % 64 == 0, got N={n}, K={k}")
-    kw_total = k // 8
-    idx = torch.arange(n * kw_total, dtype=torch.int64, device=device)
-    j = idx & 1
-    lane = (idx >> 1) & 63
-    blk = idx >> 7
-    kb = blk % (k // 64)
-    nb = blk // (k // 64)
-    col = nb * 16 + (lane & 15)
-    kw = kb * 8 + 2 * (lane >> 4) + j
-    return col * kw_total + kw
+    idx = fragment_word_index(n, k, device).reshape(-1)
+    perm = torch.full((mfma_payload_words(n, k),), -1, dtype=torch.int64, device=device)
+    perm[idx] = torch.arange(idx.numel(), dtype=torch.int64, device=device)
+    return perm
 
 
 def pack_mfma_weight(packed: torch.Tensor, k: int | None = None) -> torch.Tensor:
     """L1/L2 packed weight -> MFMA-fragment-major int32 [N, K/8+16] (CPU/offline form of the
-    device repack)."""
+    device repack): payload in ``fragment_word_index`` order (pad codes 0), then the N
+    fp32 scale words."""
     n = packed.shape[0]
     if k is None:
         k = (packed.shape[1] - 1) * 8
     words = k // 8
-    payload = packed[:, :words].contiguous().view(-1)
-    perm = mfma_word_permutation(n, k, packed.device)
     out = torch.zeros((n, words + MFMA_MARKER_WORDS), dtype=torch.int32, device=packed.device)
     flat = out.view(-1)
-    flat[: n * words] = payload[perm]
-    flat[n * words : n * words + n] = packed[:, words]
+    idx = fragment_word_index(n, k, packed.device).reshape(-1)
+    flat[idx] = packed[:, :words].contiguous().view(-1)
+    pw = mfma_payload_words(n, k)
+    flat[pw : pw + n] = packed[:, words]
     return out
 
 
@@ -155,10 +170,16 @@ def unpack_mfma_weight(mfma: torch.Tensor, k: int) -> torch.Tensor:
     n = mfma.shape[0]
     words = k // 8
     flat = mfma.contiguous().view(-1)
-    perm = mfma_word_permutation(n, k, mfma.device)
-    payload = torch.empty(n * words, dtype=torch.int32, device=mfma.device)
-    payload[perm] = flat[: n * words]
-    return torch.cat([payload.view(n, words), flat[n * words : n * words + n, None]], dim=1)
+    idx = fragment_word_index(n, k, mfma.device)
+    pw = mfma_payload_words(n, k)
+    return torch.cat([flat[idx], flat[pw : pw + n, None]], dim=1)
+
+
+def codes_from_fragment_major(q: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    """Fragment-major quantized activations (as written by the GPU quantizer) ->
+    the reference's row-major int32 words [M, K/8] (``quantize_x``'s ``q``)."""
+    flat = q.reshape(-1)
+    return flat[fragment_word_index(m, k, q.device)]
 
 
 def quant_activation_cpu(x: torch.Tensor, rotate: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:

@@ -26,8 +26,15 @@ def ext(cuda):
     return extension
 
 
-def _codes(q: torch.Tensor, k: int) -> np.ndarray:
-    return orc.unpack_nibbles(inp.to_np(q), k)
+def _words(q: torch.Tensor, m: int, k: int) -> np.ndarray:
+    """Fragment-major GPU codes -> row-major packed words [M, K/8]."""
+    from pi05_fast.w4a4.pack import codes_from_fragment_major
+
+    return inp.to_np(codes_from_fragment_major(q.cpu(), m, k))
+
+
+def _codes(q: torch.Tensor, m: int, k: int) -> np.ndarray:
+    return orc.unpack_nibbles(_words(q, m, k), k)
 
 
 def _assert_codes_equal(got: np.ndarray, want: np.ndarray, what: str) -> None:
@@ -50,7 +57,7 @@ def test_quantize_matches_golden(golden, ext, cuda, k):
     x = torch.from_numpy(golden[f"act_x_{k}"]).to(cuda)
     q, sa = ext.quantize(x)
     torch.cuda.synchronize()
-    _assert_codes_equal(_codes(q, k), golden[f"act_q_{k}"], f"golden K={k}")
+    _assert_codes_equal(_codes(q, x.shape[0], k), golden[f"act_q_{k}"], f"golden K={k}")
     assert np.array_equal(inp.to_np(sa).view(np.int32), golden[f"act_s_{k}"].view(np.int32))
 
 
@@ -65,8 +72,8 @@ def test_quantize_matches_oracle(ext, cuda, m, k, kind):
     q, sa = ext.quantize(x.to(cuda))
     torch.cuda.synchronize()
     q_ref, s_ref = orc.quant_activation(x.numpy())
-    _assert_codes_equal(_codes(q, k), q_ref, f"M={m} K={k} {kind}")
-    assert np.array_equal(inp.to_np(q), orc.pack_nibbles(q_ref)), "packed words differ"
+    _assert_codes_equal(_codes(q, m, k), q_ref, f"M={m} K={k} {kind}")
+    assert np.array_equal(_words(q, m, k), orc.pack_nibbles(q_ref)), "packed words differ"
     assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32)), "scale bits differ"
 
 
@@ -112,7 +119,7 @@ def test_gemm_acc_bit_exact(ext, cuda, m, n, k):
     torch.cuda.synchronize()
     q_ref, _ = orc.quant_activation(x.numpy())
     w_codes, _, _ = orc.unpack_linear_weight(packed.numpy())
-    _assert_codes_equal(_codes(q, k), q_ref, "codes")
+    _assert_codes_equal(_codes(q, m, k), q_ref, "codes")
     acc_ref = orc.gemm_acc_int32(q_ref, w_codes)
     got = inp.to_np(acc)
     nbad = int(np.count_nonzero(got != acc_ref))

@@ -85,22 +85,50 @@ def test_payload_and_scales_round_trip(pack):
 
 @pytest.mark.parametrize("n,k", [(16, 64), (32, 192), (48, 2048)])
 def test_mfma_layout_definition(pack, n, k):
-    """dst[((nb*(K/64) + kb)*64 + L)*2 + j] = L1[16*nb + L%16, 8*kb + 2*(L/16) + j]."""
+    """In terms of codes: lane L of fragment (column block nb, 128-deep block t) holds, for
+    half h, the codes of column 16*nb + L%16 at k = 128*t + 64*h + 16*(L//16) .. +15 in
+    words 4L + 2h, 4L + 2h + 1 (zero codes past K); scales follow the payload."""
     packed = inp.random_packed(inp.generator(n + k), n, k)
     mf = pack.pack_mfma_weight(packed, k)
     assert tuple(mf.shape) == (n, k // 8 + pack.MFMA_MARKER_WORDS)
     flat = mf.view(-1).numpy()
-    l1 = packed.numpy()
-    kb64 = k // 64
-    rng = np.random.default_rng(0)
-    for _ in range(200):
-        nb, kb, lane, j = (int(rng.integers(0, n // 16)), int(rng.integers(0, kb64)),
-                           int(rng.integers(0, 64)), int(rng.integers(0, 2)))
-        dst = ((nb * kb64 + kb) * 64 + lane) * 2 + j
-        assert flat[dst] == l1[16 * nb + lane % 16, 8 * kb + 2 * (lane // 16) + j]
-    assert np.array_equal(flat[n * (k // 8) : n * (k // 8) + n], l1[:, k // 8])
-    assert np.all(flat[n * (k // 8) + n :] == 0)
+    codes = orc.unpack_nibbles(packed.numpy()[:, : k // 8], k)
+    kb = (k + 127) // 128
+    for nb in range(n // 16):
+        for t in range(kb):
+            for lane in range(64):
+                for h in range(2):
+                    w = (nb * kb + t) * 256 + lane * 4 + 2 * h
+                    got = orc.unpack_nibbles(flat[w : w + 2][None, :], 16)[0]
+                    k0 = 128 * t + 64 * h + 16 * (lane // 16)
+                    want = codes[16 * nb + lane % 16, k0 : k0 + 16] if k0 < k else np.zeros(16)
+                    assert np.array_equal(got, want), (nb, t, lane, h)
+    pw = n * kb * 16
+    assert np.array_equal(flat[pw : pw + n], packed.numpy()[:, k // 8])
+    assert np.all(flat[pw + n :] == 0)
     assert torch.equal(pack.unpack_mfma_weight(mf, k), packed)
+
+
+@pytest.mark.parametrize("m,k", [(1, 64), (17, 128), (40, 2048)])
+def test_activation_fragment_layout(pack, m, k):
+    """Quantized activations use the weight fragment layout on 16-row blocks: the index map
+    is injective into the first ceil(M/16)*16 * ceil(K/128)*16 words and places word
+    (row, kw) in lane row%16 + 16*((kw%8)//2) of fragment (row//16, kw//16), half (kw//8)%2."""
+    idx = pack.fragment_word_index(m, k).numpy()
+    m16 = (m + 15) // 16 * 16
+    total = m16 * ((k + 127) // 128) * 16
+    full = pack.fragment_word_index(m16, k).numpy().reshape(-1)
+    assert len(np.unique(full)) == full.size and full.max() < total
+    assert np.array_equal(idx, full.reshape(m16, k // 8)[:m])
+    kb = (k + 127) // 128
+    for row, kw in [(0, 0), (m - 1, k // 8 - 1), (m // 2, k // 16)]:
+        frag = (row // 16) * kb + kw // 16
+        lane = row % 16 + 16 * ((kw % 8) // 2)
+        assert idx[row, kw] == frag * 256 + 4 * lane + 2 * ((kw // 8) % 2) + kw % 2
+    words = torch.randint(-(2**31), 2**31 - 1, (m, k // 8), dtype=torch.int32)
+    buf = torch.zeros(total, dtype=torch.int32)
+    buf[torch.from_numpy(idx.reshape(-1))] = words.reshape(-1)
+    assert torch.equal(pack.codes_from_fragment_major(buf, m, k), words)
 
 
 def test_mfma_layout_rejects_bad_shapes(pack):
@@ -139,7 +167,11 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_library_version_and_sizes(lib):
     assert lib.pi05w4a4_version() >= 100
+    assert lib.pi05w4a4_q_words(776, 2048) == 784 * 256
+    assert lib.pi05w4a4_q_words(16, 64) == 16 * 16  # K padded to 128
+    assert lib.pi05w4a4_q_words(0, 64) == 0
     assert lib.pi05w4a4_mfma_words(2048, 2048) == 2048 * (2048 // 8 + 1)
+    assert lib.pi05w4a4_mfma_words(32, 192) == 32 * (256 // 8 + 1)
     assert lib.pi05w4a4_mfma_words(0, 64) == 0
 
 
