@@ -18,11 +18,12 @@
  *   q      nibble-packed activation codes (values in [-7, 7], two's complement) in the
  *          MFMA-fragment-major layout shared with the weights.  With KB = ceil(K/128),
  *          the codes of 16-row block mb and 128-deep k block b form one 1 KB fragment at
- *          word (mb*KB + b)*256; its lane L (words 4L .. 4L+3) holds codes
- *          128*b + 16*(L/16) .. +15 (words 4L, 4L+1) and 128*b + 64 + 16*(L/16) .. +15
- *          (words 4L+2, 4L+3) of row 16*mb + L%16, code k in nibble (k & 7) of its word.
- *          Row-major word (row, kw) of the reference's [M, K/8] codes therefore sits at
- *          ((row/16)*KB + kw/16)*256 + 4*(row%16 + 16*((kw%8)/2)) + 2*((kw/8)%2) + kw%2.
+ *          word (mb*KB + b)*256 made of 64 16-byte slots: slot L (words 4L .. 4L+3) holds
+ *          codes 128*b + 32*(L/16) .. +31 of row 16*mb + L%16, code k in nibble (k & 7)
+ *          of its word.  Lane L of an MFMA wave loads slot L and feeds its codes 0-15 and
+ *          16-31 to the block's two v_mfma_i32_16x16x64_i8.  Row-major word (row, kw) of
+ *          the reference's [M, K/8] codes therefore sits at
+ *          ((row/16)*KB + kw/16)*256 + 4*(row%16 + 16*((kw%16)/4)) + kw%4.
  *          The buffer holds pi05w4a4_q_words(M, K) words (M rounded up to 16 rows, K to
  *          128; padding is never read into an output).  16-byte aligned.
  *   sa     fp32 [M] per-token activation scales.

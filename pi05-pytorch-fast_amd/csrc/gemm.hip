@@ -20,9 +20,9 @@
 // parts and add their accumulators through LDS at the end, which gives narrow GEMMs
 // (QKV, o, down) enough workgroups without a global split-K workspace.
 // Both operands live in HBM in the same MFMA-fragment-major layout (frag_word_index: one
-// 1 KB fragment per 16 rows/columns x 128 k, lane L holding the two 64-deep operands of
-// row/column L%16), so every operand fetch is one fully coalesced 16-byte-per-lane load
-// straight into registers.  (The vector memory pipeline issues about one wave-wide load
+// 1 KB fragment per 16 rows/columns x 128 k; lane L loads slot L = 32 codes of row/
+// column L%16, the operands of the block's two MFMAs), so every operand fetch is one
+// fully coalesced 16-byte-per-lane load straight into registers.  (The vector memory pipeline issues about one wave-wide load
 // per ~20 clocks per CU whatever its width, so 16-byte loads double the operand bandwidth
 // of 8-byte ones.)  The K loop walks 128-deep k blocks through a 2-deep register ring:
 // the loads of block kb + 1 are issued before block kb is multiplied, and a 4-byte-per-
@@ -188,8 +188,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) b[ni] = *reinterpret_cast<const uint4*>(bptr[ni] + off);
   };
-  // Both 64-deep halves of a 128-deep block.  Pad codes of a K that is not a multiple of
-  // 128 are zero in the weights, so the second half needs no guard.
+  // The two MFMAs of a 128-deep block (codes 0-15 and 16-31 of each lane's 32).  Pad
+  // codes of a K that is not a multiple of 128 are zero in the weights: no guard.
   auto compute = [&](const uint4 (&a)[MI], const uint4 (&b)[NI]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {

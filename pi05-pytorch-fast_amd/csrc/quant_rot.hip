@@ -46,6 +46,26 @@ __device__ __forceinline__ int32_t quant_pack8(const float (&v)[8], float sdiv) 
   return static_cast<int32_t>(word);
 }
 
+// Same eight codes without a division per element.  qa = v * rcp(sdiv) differs from the
+// exact quotient q = v / sdiv by less than 2e-6 (|q| <= 7 and the hardware reciprocal
+// and the product each round within an ulp or two), so rint(qa) == rint(q) unless q lies
+// within 2e-6 of a half-integer.  Any lane that sees qa within 1e-5 of one raises
+// `near_tie`; the caller then redoes the row's codes with quant_pack8 (exact division).
+// Both paths therefore produce the reference's round-half-even codes bit for bit.
+__device__ __forceinline__ int32_t quant_pack8_rcp(const float (&v)[8], float rcp,
+                                                   bool& near_tie) {
+  uint32_t word = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float qa = v[e] * rcp;
+    float r = __builtin_rintf(qa);
+    near_tie |= fabsf(qa - r) > 0.49999f;
+    r = fminf(fmaxf(r, -7.0f), 7.0f);
+    word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFu) << (4 * e);
+  }
+  return static_cast<int32_t>(word);
+}
+
 template <int T>
 __device__ __forceinline__ float block_max(float v, float* red) {
   v = wave_max(v);
@@ -167,6 +187,154 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
   for (int j = 0; j < J; ++j) q[frag_word_index(row, t + T * j, kblocks128(K))] = quant_pack8(v[j], sdiv);
 }
 
+// Register-FFT form of the same transform for K = 2^LOGK, T = 2^LOGT threads per row.
+// Each thread holds R = K/T values; the log2(K) butterfly stages are done in passes of
+// r = log2(R) consecutive stride bits, each pass entirely in registers, with an LDS
+// transpose between passes that re-deals the row so that the next pass's stride bits
+// index a thread's registers.  Stages still run in increasing order of the stride h
+// and each one writes (a + b, a - b), so the rotated values are bit-identical to the
+// CPU transform.  Pass p covers element bits [lo, lo + w): register j of thread t holds
+// element e_p(t, j), whose bits [lo, lo + w) are j mod 2^w and whose other bits, in
+// increasing order, are (t << (r - w)) | (j >> w).  Pass 0 is therefore R contiguous
+// elements per thread (one coalesced 2R-byte load), and after the last pass each thread
+// holds runs of 2^(r - w) >= 8 consecutive elements, which it packs into code words
+// directly.  LDS rows carry 4 pad floats per R floats so that both the 16-byte writes
+// of pass 0 and the per-lane reads of later passes are (nearly) bank-conflict free.
+// ROWS rows per workgroup; with T = 64 every row belongs to one wave and the passes
+// need no workgroup barrier.
+template <int LOGK, int LOGT, int ROWS>
+__global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
+    const _Float16* __restrict__ x, int64_t m, int32_t* __restrict__ q, float* __restrict__ sa,
+    float inv_sqrt_k) {
+  constexpr int K = 1 << LOGK;
+  constexpr int T = 1 << LOGT;
+  constexpr int r = LOGK - LOGT;
+  constexpr int R = 1 << r;
+  constexpr int PASSES = (LOGK + r - 1) / r;
+  constexpr int LAST_W = LOGK - (PASSES - 1) * r;
+  static_assert(r >= 3 && r - LAST_W >= 3, "the last pass must leave runs of >= 8 elements");
+  static_assert(T == 64 || ROWS == 1, "rows of more than one wave need a workgroup per row");
+  constexpr int LROW = K + 4 * (K / R);  // LDS floats per row (4 pad floats per R)
+  __shared__ __align__(16) float lds[ROWS * LROW];
+  __shared__ float red[ROWS * (T / 64 > 0 ? T / 64 : 1)];
+
+  const int sub = threadIdx.x >> LOGT;
+  const int t = threadIdx.x & (T - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * ROWS + sub;
+  if constexpr (T > 64) {
+    if (row >= m) return;  // ROWS == 1: the whole workgroup leaves together
+  } else {
+    if (row >= m) return;  // the wave owns its row: no workgroup barrier below
+  }
+  float* L = lds + sub * LROW;
+  auto addr = [](int e) { return e + 4 * (e >> r); };
+  auto elem = [](int p, int tt, int j) {
+    const int lo = p * r;
+    const int w = (LOGK - lo) < r ? (LOGK - lo) : r;
+    const int rest = (tt << (r - w)) | (j >> w);
+    return (rest & ((1 << lo) - 1)) | ((j & ((1 << w) - 1)) << lo) | ((rest >> lo) << (lo + w));
+  };
+  auto sync = [&]() {
+    if constexpr (T > 64) __syncthreads();
+    else __builtin_amdgcn_wave_barrier();
+  };
+
+  float v[R];
+  const _Float16* xr = x + row * K + t * R;
+#pragma unroll
+  for (int c = 0; c < R / 8; ++c) {
+    const half8 h = *reinterpret_cast<const half8*>(xr + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
+  }
+
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    if (p > 0) {
+      // Transpose: scatter with the previous pass's mapping, gather with this one's.
+      if (p == 1) {
+#pragma unroll
+        for (int c = 0; c < R / 4; ++c)
+          *reinterpret_cast<float4*>(&L[addr(t * R + 4 * c)]) =
+              make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < R; ++j) L[addr(elem(p - 1, t, j))] = v[j];
+      }
+      sync();
+#pragma unroll
+      for (int j = 0; j < R; ++j) v[j] = L[addr(elem(p, t, j))];
+      sync();
+    }
+    const int w = (LOGK - p * r) < r ? (LOGK - p * r) : r;
+#pragma unroll
+    for (int b = 0; b < r; ++b) {
+      if (b >= w) break;
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        if (j & (1 << b)) continue;
+        const float a = v[j], c = v[j + (1 << b)];
+        v[j] = __fadd_rn(a, c);
+        v[j + (1 << b)] = __fsub_rn(a, c);
+      }
+    }
+  }
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = wave_max(amax);
+  if constexpr (T > 64) {
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int i = 1; i < T / 64; ++i) amax = fmaxf(amax, red[i]);
+  }
+  const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
+  if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
+
+  // Last pass: for each value g of the pass bits the registers j = g + 2^w * i,
+  // i = 0 .. 2^(r-w) - 1, hold consecutive elements; pack them 8 at a time and store two
+  // words (16 codes, 8 bytes: consecutive words of the row's slot in its fragment) at once.
+  constexpr int RUN = R >> LAST_W;
+  constexpr int NW = (1 << LAST_W) * (RUN / 8);  // code words per thread
+  static_assert(RUN % 16 == 0, "runs of 16 codes per 8-byte store");
+  auto gather8 = [&](int g, int u, float (&c8)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c8[e] = v[g + (1 << LAST_W) * (8 * u + e)];
+  };
+  uint32_t words[NW];
+  bool near_tie = false;
+  const float rcp = __builtin_amdgcn_rcpf(sdiv);
+#pragma unroll
+  for (int g = 0; g < (1 << LAST_W); ++g)
+#pragma unroll
+    for (int u = 0; u < RUN / 8; ++u) {
+      float c8[8];
+      gather8(g, u, c8);
+      words[g * (RUN / 8) + u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+    }
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+#pragma unroll
+    for (int g = 0; g < (1 << LAST_W); ++g)
+#pragma unroll
+      for (int u = 0; u < RUN / 8; ++u) {
+        float c8[8];
+        gather8(g, u, c8);
+        words[g * (RUN / 8) + u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+      }
+  }
+#pragma unroll
+  for (int g = 0; g < (1 << LAST_W); ++g)
+#pragma unroll
+    for (int u = 0; u < RUN / 8; u += 2) {
+      const int e0 = elem(PASSES - 1, t, g + (1 << LAST_W) * 8 * u);
+      const uint2 wd = make_uint2(words[g * (RUN / 8) + u], words[g * (RUN / 8) + u + 1]);
+      *reinterpret_cast<uint2*>(&q[frag_word_index(row, e0 >> 3, kblocks128(K))]) = wd;
+    }
+}
+
 // Unrotated quantization for every other K (K % 64 == 0): int4_gemm.cu:451-477.
 // One workgroup of 256 threads per row, two passes over the row (amax, then codes).
 __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ x, int64_t m,
@@ -205,10 +373,11 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
   const dim3 grid(static_cast<unsigned>(m));
   switch (k) {
     case 16384:
-      quant_rot_kernel<16384, 256><<<grid, 256, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);
+      fwht_quant_kernel<14, 8, 1><<<grid, 256, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);
       break;
     case 2048:
-      quant_rot_kernel<2048, 256><<<grid, 256, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);
+      fwht_quant_kernel<11, 6, 4><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
+          xh, m, q, sa, inv_sqrt_k);
       break;
     case 1024:
       quant_rot_kernel<1024, 128><<<grid, 128, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);

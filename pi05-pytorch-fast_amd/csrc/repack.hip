@@ -7,11 +7,11 @@
 //              scale at N*K/8 + n (pack.py:45-68).
 //
 // Destination (this library's layout, frag_word_index in w4a4_internal.h): for every
-// 16-column block and 128-deep k block one contiguous 1 KB fragment in which lane L of a
-// wave owns 16 bytes: the B operands of column 16*nb + L%16 for the two 64-deep halves of
-// the block.  Fragments of one column block are consecutive along K, so a wave streams
-// its weights with fully coalesced 16-byte-per-lane loads.  K is padded to a multiple of
-// 128 with zero codes; the fp32 column scales follow the payload.
+// 16-column block and 128-deep k block one contiguous 1 KB fragment of 64 16-byte slots,
+// slot L = codes 32*(L/16) .. +31 of column 16*nb + L%16.  Fragments of one column block
+// are consecutive along K, so a wave streams its weights with fully coalesced
+// 16-byte-per-lane loads.  K is padded to a multiple of 128 with zero codes; the fp32
+// column scales follow the payload.
 //
 // One thread per destination word: the writes are coalesced, the reads are gathers from
 // a layout that is only read once (this runs at load time, not per call).
@@ -29,15 +29,14 @@ __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__
   const int64_t payload = static_cast<int64_t>(n) * kb128 * 16;
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (idx < payload) {
-    // Invert frag_word_index: idx = (nb*kb128 + kb2)*256 + lane*4 + half*2 + j.
-    const int j = static_cast<int>(idx & 1);
-    const int half = static_cast<int>((idx >> 1) & 1);
-    const int lane = static_cast<int>((idx >> 2) & 63);
+    // Invert frag_word_index: idx = (nb*kb128 + kb2)*256 + slot*4 + kw%4, slot = col%16 +
+    // 16*((kw%16)/4).
     const int64_t frag = idx >> 8;
     const int64_t kb2 = frag % kb128;
     const int64_t nb = frag / kb128;
-    const int64_t col = nb * 16 + (lane & 15);
-    const int64_t kw = kb2 * 16 + half * 8 + 2 * (lane >> 4) + j;
+    const int slot = static_cast<int>((idx >> 2) & 63);
+    const int64_t col = nb * 16 + (slot & 15);
+    const int64_t kw = kb2 * 16 + (slot >> 4) * 4 + (idx & 3);
     int32_t v = 0;
     if (kw < kw_total) {
       const int64_t s = (layout == 0) ? col * stride + kw : ((kw >> 1) * n + col) * 2 + (kw & 1);

@@ -45,16 +45,18 @@ struct GemmParams {
 
 // MFMA-fragment-major layout of packed INT4 codes, shared by the weights (r = output
 // column) and the quantized activations (r = row).  The codes of the 16-line block r/16
-// and the 128-deep k block kw/16 form one 1 KB fragment of 256 words; lane L of a wave
-// owns words 4L .. 4L+3 of it: words 4L, 4L+1 hold codes 16*(L/16) .. +15 of the first
-// 64-deep half (the v_mfma_i32_16x16x64_i8 operand of line 16*(r/16) + L%16), words 4L+2,
-// 4L+3 the same codes of the second half.  One 16-byte load per lane fetches the operand
-// pair of a 128-deep k step.  K is padded to a multiple of 128; weight pad codes are 0.
+// and the 128-deep k block kw/16 form one 1 KB fragment of 256 words made of 64 16-byte
+// slots, one per lane of a wave: slot L holds codes 32*(L/16) .. +31 of line 16*(r/16) +
+// L%16 (its packed words 16*(kw/16) + 4*(L/16) .. +3).  Lane L loads slot L (one fully
+// coalesced 16-byte-per-lane load fetches the whole fragment) and feeds codes 0-15 of it
+// to one v_mfma_i32_16x16x64_i8 and codes 16-31 to the next, so the two MFMAs of a
+// block together cover its 128 codes once.  A and B share this k permutation, which
+// leaves the integer dot product unchanged.  A line's 32 consecutive codes are
+// contiguous, so the quantizer writes them as whole 16-byte slots.
+// K is padded to a multiple of 128; weight pad codes are 0.
 // Word index of packed word kw (codes 8*kw .. 8*kw+7) of line r, kb128 = ceil(K/128):
 __host__ __device__ inline int64_t frag_word_index(int64_t r, int32_t kw, int32_t kb128) {
-  const int64_t frag = (r >> 4) * kb128 + (kw >> 4);
-  const int lane = static_cast<int>(r & 15) + 16 * ((kw & 7) >> 1);
-  return frag * 256 + lane * 4 + ((kw >> 3) & 1) * 2 + (kw & 1);
+  return ((r >> 4) * kb128 + (kw >> 4)) * 256 + ((r & 15) + 16 * ((kw & 15) >> 2)) * 4 + (kw & 3);
 }
 
 __host__ __device__ inline int32_t kblocks128(int32_t k) { return (k + 127) >> 7; }

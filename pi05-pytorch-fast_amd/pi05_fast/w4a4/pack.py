@@ -120,17 +120,17 @@ def fragment_word_index(lines: int, k: int, device: torch.device | str = "cpu") 
 
     Returns int64 [lines, K/8]: row-major packed word (line, kw) -> word of the fragment
     buffer.  With KB = ceil(K/128), the 16-line block b and 128-deep k block t form one
-    1 KB fragment at word (b*KB + t)*256; lane L (words 4L .. 4L+3) holds the codes
-    16*(L/16) .. +15 of both 64-deep halves of line 16*b + L%16.
+    1 KB fragment at word (b*KB + t)*256 made of 64 16-byte slots: slot L holds codes
+    32*(L//16) .. +31 of block t of line 16*b + L%16 (the 16 bytes lane L of an MFMA wave
+    loads).
     """
     if k % 64 != 0:
         raise ValueError(f"K must be a multiple of 64, got {k}")
     kb128 = (k + 127) // 128
     r = torch.arange(lines, dtype=torch.int64, device=device)[:, None]
     kw = torch.arange(k // 8, dtype=torch.int64, device=device)[None, :]
-    frag = (r >> 4) * kb128 + (kw >> 4)
-    lane = (r & 15) + 16 * ((kw & 7) >> 1)
-    return frag * 256 + lane * 4 + ((kw >> 3) & 1) * 2 + (kw & 1)
+    slot = (r & 15) + 16 * ((kw & 15) >> 2)
+    return ((r >> 4) * kb128 + (kw >> 4)) * 256 + slot * 4 + (kw & 3)
 
 
 def mfma_payload_words(n: int, k: int) -> int:

@@ -77,6 +77,38 @@ def test_quantize_matches_oracle(ext, cuda, m, k, kind):
     assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32)), "scale bits differ"
 
 
+@pytest.mark.parametrize("k", [2048, 16384])
+def test_quantize_exact_ties(ext, cuda, k):
+    """Rows whose rotated values hit exact half-integer multiples of the scale: the GPU's
+    reciprocal fast path must fall back to exact division and round half to even.
+
+    x = FWHT(y) / K for y = 2^-4 * (7 e_0 + c_1 e_1 + c_2 e_2 ...) is exact in fp16, the fp32
+    FWHT returns y exactly (H.H = K.I on dyadic values), amax = 7/16 makes sdiv = 1/16
+    exactly (the 1e-12 is absorbed), and x'/sdiv = c_i are the chosen quotients.
+    """
+    quotients = [2.5, -2.5, 0.5, -0.5, 3.5, 1.5, -6.5, 4.5, 1.25, -3.75]
+    m = 8
+    y = np.zeros((m, k), np.float64)
+    rng = np.random.default_rng(k)
+    for r in range(m):
+        y[r, 0] = 7.0 if r % 2 == 0 else -7.0
+        cols = rng.choice(np.arange(1, k), size=len(quotients), replace=False)
+        y[r, cols] = quotients
+    y /= 16.0
+    x = orc.fwht_unnormalized(y.astype(np.float32)).astype(np.float64) / k
+    x16 = x.astype(np.float16)
+    assert np.array_equal(x16.astype(np.float64), x), "inputs must be exact in fp16"
+    q, sa = ext.quantize(torch.from_numpy(x16).to(cuda))
+    torch.cuda.synchronize()
+    q_ref, s_ref = orc.quant_activation(x16)
+    got = _codes(q, m, k)
+    _assert_codes_equal(got, q_ref, f"ties K={k}")
+    assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32))
+    # half-even: 2.5 -> 2, -2.5 -> -2, 0.5 -> 0, 3.5 -> 4, 1.5 -> 2, -6.5 -> -6, 4.5 -> 4
+    r0_cols = np.flatnonzero(y[0])
+    assert sorted(np.unique(got[0, r0_cols]).tolist()) == sorted({7, 2, -2, 0, 4, -6, 1, -4})
+
+
 # ----------------------------------------------------------------------------- repack
 @pytest.mark.parametrize("n,k", [(16, 64), (48, 192), (256, 2048), (128, 16384)])
 def test_repack_matches_cpu_layout(ext, cuda, n, k):

@@ -85,9 +85,10 @@ def test_payload_and_scales_round_trip(pack):
 
 @pytest.mark.parametrize("n,k", [(16, 64), (32, 192), (48, 2048)])
 def test_mfma_layout_definition(pack, n, k):
-    """In terms of codes: lane L of fragment (column block nb, 128-deep block t) holds, for
-    half h, the codes of column 16*nb + L%16 at k = 128*t + 64*h + 16*(L//16) .. +15 in
-    words 4L + 2h, 4L + 2h + 1 (zero codes past K); scales follow the payload."""
+    """Fragment (column block nb, 128-deep block t) is 1 KB at word (nb*KB + t)*256 made of
+    64 16-byte slots; slot L holds codes 128*t + 32*(L//16) .. +31 of column 16*nb + L%16
+    (zero codes past K), so lane L's two MFMA operands are codes 0-15 and 16-31 of it and
+    the 4 lane groups cover the block's 128 codes once.  The scales follow the payload."""
     packed = inp.random_packed(inp.generator(n + k), n, k)
     mf = pack.pack_mfma_weight(packed, k)
     assert tuple(mf.shape) == (n, k // 8 + pack.MFMA_MARKER_WORDS)
@@ -96,13 +97,17 @@ def test_mfma_layout_definition(pack, n, k):
     kb = (k + 127) // 128
     for nb in range(n // 16):
         for t in range(kb):
+            seen = np.zeros((16, 128), np.int32)
             for lane in range(64):
-                for h in range(2):
-                    w = (nb * kb + t) * 256 + lane * 4 + 2 * h
-                    got = orc.unpack_nibbles(flat[w : w + 2][None, :], 16)[0]
-                    k0 = 128 * t + 64 * h + 16 * (lane // 16)
-                    want = codes[16 * nb + lane % 16, k0 : k0 + 16] if k0 < k else np.zeros(16)
-                    assert np.array_equal(got, want), (nb, t, lane, h)
+                w = (nb * kb + t) * 256 + 4 * lane
+                got = orc.unpack_nibbles(flat[w : w + 4][None, :], 32)[0]
+                k0 = 128 * t + 32 * (lane // 16)
+                want = np.zeros(32, np.int32)
+                seg = codes[16 * nb + lane % 16, k0 : k0 + 32]
+                want[: seg.size] = seg
+                assert np.array_equal(got, want), (nb, t, lane)
+                seen[lane % 16, 32 * (lane // 16) : 32 * (lane // 16) + 32] += 1
+            assert np.all(seen == 1)
     pw = n * kb * 16
     assert np.array_equal(flat[pw : pw + n], packed.numpy()[:, k // 8])
     assert np.all(flat[pw + n :] == 0)
@@ -113,7 +118,7 @@ def test_mfma_layout_definition(pack, n, k):
 def test_activation_fragment_layout(pack, m, k):
     """Quantized activations use the weight fragment layout on 16-row blocks: the index map
     is injective into the first ceil(M/16)*16 * ceil(K/128)*16 words and places word
-    (row, kw) in lane row%16 + 16*((kw%8)//2) of fragment (row//16, kw//16), half (kw//8)%2."""
+    (row, kw) in slot row%16 + 16*((kw%16)//4) of fragment (row//16, kw//16)."""
     idx = pack.fragment_word_index(m, k).numpy()
     m16 = (m + 15) // 16 * 16
     total = m16 * ((k + 127) // 128) * 16
@@ -122,9 +127,8 @@ def test_activation_fragment_layout(pack, m, k):
     assert np.array_equal(idx, full.reshape(m16, k // 8)[:m])
     kb = (k + 127) // 128
     for row, kw in [(0, 0), (m - 1, k // 8 - 1), (m // 2, k // 16)]:
-        frag = (row // 16) * kb + kw // 16
-        lane = row % 16 + 16 * ((kw % 8) // 2)
-        assert idx[row, kw] == frag * 256 + 4 * lane + 2 * ((kw // 8) % 2) + kw % 2
+        slot = row % 16 + 16 * ((kw % 16) // 4)
+        assert idx[row, kw] == ((row // 16) * kb + kw // 16) * 256 + 4 * slot + kw % 4
     words = torch.randint(-(2**31), 2**31 - 1, (m, k // 8), dtype=torch.int32)
     buf = torch.zeros(total, dtype=torch.int32)
     buf[torch.from_numpy(idx.reshape(-1))] = words.reshape(-1)
