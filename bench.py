@@ -3,19 +3,25 @@
 
     python bench.py [--steps K] [--warmup W] [--tokens 776] [--batch 1] [--layers 18]
 
-Workload: the 18-layer Gemma-2B-shaped prefix LM (hidden 2048, 8x256 heads, 1 KV head,
-intermediate 16384) over a 776-token prefix, batch 1, with all q/k/v/o/gate/up/down
-projections running the W4A4 path (quantize + int8-MFMA GEMM) and attention fp16 eager.
-Weights are synthetic packed INT4 (random codes with the statistics of a packed
-N(0, 0.02) weight), inputs synthetic N(0, 1/sqrt(2048)) prefix embeddings.
+Workload (`value`): one forward of the 18-layer Gemma-2B-shaped prefix LM (hidden 2048,
+8x256 heads, 1 KV head, intermediate 16384) over a 776-token prefix, batch 1, every
+q/k/v/o/gate/up/down projection running the W4A4 path (FWHT + INT4 quant, int8-MFMA
+GEMM) and attention fp16 eager.  Weights are synthetic packed INT4 (random codes with the
+statistics of a packed N(0, 0.02) weight), inputs synthetic N(0, 1/sqrt(2048)) prefix
+embeddings, all resident in HBM.  Timed region: K replays of the whole forward captured
+in one HIP graph, bracketed by device synchronisation; `value` = ms per forward.
 
-Timed region: K replays of the whole forward captured in one HIP graph (inputs resident
-in HBM), bracketed by device synchronisation.  `value` = ms per prefix forward.
-Per-GEMM timings come from a second, eager timed region in which HIP events (recorded on
-the stream the kernels run on) bracket every GEMM launch; they give int8 TOPS and the
-fraction of the MI355X dense int8 MFMA peak per GEMM class and the `roofline` object of
-the dominant kernel.  `cpu_baseline` times the CPU oracle (numpy) on one decoder layer's
-W4A4 work at the same M and scales it to the full depth.
+Per-kernel figures (`gemms`, `roofline`): each W4A4 kernel of the forward is launched
+back to back through the C ABI with preallocated buffers at the forward's shapes; HIP
+events recorded on the launching stream (torch's current stream, which the library
+uses) bracket the launches, giving the average kernel duration, int8 TOPS and the
+fraction of the MI355X dense int8 MFMA peak (GEMMs) or of HBM bandwidth (quantizers).
+The dominant kernel of the forward (gate/up GEMM) is the `roofline` object; its `traffic`
+(HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed
+under profiles/ when present.
+
+`cpu_baseline` times the CPU oracle (numpy) on one decoder layer's W4A4 work at the
+same M and scales it to the full depth.
 
 Prints one JSON line.
 """
@@ -23,8 +29,10 @@ Prints one JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -38,6 +46,7 @@ for _p in (ROOT / "pi05-pytorch-fast_amd", ROOT):
 METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X)"
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
+TRAFFIC_FILE = ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md"
 
 
 def parse_args():
@@ -48,73 +57,130 @@ def parse_args():
     ap.add_argument("--tokens", type=int, default=776)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layers", type=int, default=18)
-    ap.add_argument("--kernel-steps", type=int, default=10, help="eager forwards for per-GEMM events")
+    ap.add_argument("--kernel-iters", type=int, default=30, help="back-to-back launches per kernel")
     ap.add_argument("--no-graph", action="store_true", help="time eager forwards instead of graph replays")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
     ap.add_argument("--fuse-gelu", action="store_true", help="gate/up with the fused GELU*up epilogue")
+    ap.add_argument("--only-kernel", default="",
+                    help="skip the forward; launch only this kernel class (for rocprofv3 --pmc runs)")
     return ap.parse_args()
 
 
-def gemm_class(kind: str, k: int, ns: list[int]) -> str:
-    if kind == "quant":
-        return f"quant_k{k}"
-    if kind == "gemm3":
-        return "qkv"
-    if kind in ("gemm2", "gemm2_gelu"):
-        return "gate_up"
-    return "down" if k > 2048 else "o"
+# ----------------------------------------------------------------------------- kernels
+class KernelBench:
+    """Back-to-back launches of one W4A4 kernel through the C ABI, timed with HIP events
+    recorded on the launching stream."""
 
+    def __init__(self, torch, ext, dev, iters):
+        self.torch, self.ext, self.dev, self.iters = torch, ext, dev, iters
+        self.lib = ext.load_int4_gemm()
 
-def gemm_ops(kind: str, m: int, k: int, ns: list[int]) -> float:
-    return 2.0 * m * k * sum(ns)
+    def _stream(self):
+        return ctypes.c_void_p(self.torch.cuda.current_stream(self.dev).cuda_stream)
 
+    def _time(self, fn) -> float:
+        torch = self.torch
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(self.iters):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / self.iters
 
-class EventRecorder:
-    """HIP events around each GEMM / quant launch on the launching (current) stream."""
+    def _check(self, rc):
+        if rc != 0:
+            raise RuntimeError(self.lib.pi05w4a4_last_error().decode())
 
-    def __init__(self, torch):
-        self.torch = torch
-        self.open: dict[str, tuple] = {}
-        self.done: list[tuple] = []
+    def _packed(self, n, k, gen):
+        torch = self.torch
+        w = torch.randint(-(2**31), 2**31 - 1, (n, k // 8 + 1), dtype=torch.int32, device=self.dev,
+                          generator=gen)
+        w[:, -1] = (torch.rand(n, device=self.dev, generator=gen) * 0.05 + 0.01).view(torch.int32)
+        return self.ext.repack_weight(w, k=k)
 
-    def __call__(self, kind, phase, m, k, ns):
-        key = (kind, k, tuple(ns))
-        if phase == "begin":
-            ev = self.torch.cuda.Event(enable_timing=True)
-            ev.record()
-            self.open[key] = (ev, m)
+    def quant(self, m, k):
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16)
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        us = self._time(lambda: self._check(lib.pi05w4a4_quantize(P(x), m, k, P(q), P(sa), self._stream())))
+        nbytes = 2.0 * m * k + m * k / 2 + 4 * m
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+    def gemm(self, m, k, ns, gelu=False):
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        gen = torch.Generator(device=self.dev).manual_seed(20260923 + k + sum(ns))
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        self._check(lib.pi05w4a4_quantize(P(x), m, k, P(q), P(sa), self._stream()))
+        ws = [self._packed(n, k, gen) for n in ns]
+        g = len(ns)
+        n_arr = (ctypes.c_int32 * g)(*ns)
+        wsb = int(lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0))
+        work = torch.empty(max(wsb, 16), dtype=torch.uint8, device=self.dev)
+        if gelu:
+            out = torch.empty(m, ns[0], dtype=torch.float16, device=self.dev)
+            fn = lambda: self._check(lib.pi05w4a4_gemm_gelu_up(  # noqa: E731
+                P(q), P(sa), m, k, P(ws[0]), P(ws[1]), ns[0], P(out), P(work), wsb, self._stream()))
+            out_bytes = 2.0 * m * ns[0]
         else:
-            ev0, m0 = self.open.pop(key)
-            ev1 = self.torch.cuda.Event(enable_timing=True)
-            ev1.record()
-            self.done.append((kind, m0, k, list(ns), ev0, ev1))
-
-    def summary(self, steps: int) -> dict:
-        self.torch.cuda.synchronize()
-        acc: dict[str, dict] = {}
-        for kind, m, k, ns, e0, e1 in self.done:
-            cls = gemm_class(kind, k, ns)
-            d = acc.setdefault(cls, {"times_us": [], "m": m, "k": k, "n": sum(ns), "kind": kind})
-            d["times_us"].append(e0.elapsed_time(e1) * 1e3)
-        out = {}
-        for cls, d in acc.items():
-            avg = sum(d["times_us"]) / len(d["times_us"])
-            calls_per_step = len(d["times_us"]) / steps
-            m, k, n = d["m"], d["k"], d["n"]
-            entry = {"m": m, "k": k, "n": n, "calls_per_forward": calls_per_step, "avg_us": round(avg, 3)}
-            if cls.startswith("quant"):
-                nbytes = 2.0 * m * k + m * k / 2 + 4 * m
-                gbs = nbytes / (avg * 1e-6) / 1e9
-                entry.update(bytes=nbytes, gbs=round(gbs, 1), frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
-            else:
-                ops = 2.0 * m * n * k
-                tops = ops / (avg * 1e-6) / 1e12
-                entry.update(ops=ops, tops=round(tops, 1), frac_int8_peak=round(tops / INT8_PEAK_TOPS, 4))
-            out[cls] = entry
-        return out
+            outs = [torch.empty(m, n, dtype=torch.float16, device=self.dev) for n in ns]
+            w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for w in ws])
+            y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in outs])
+            fn = lambda: self._check(lib.pi05w4a4_gemm_multi(  # noqa: E731
+                P(q), P(sa), m, k, g, w_arr, n_arr, y_arr, P(work), wsb, self._stream()))
+            out_bytes = 2.0 * m * sum(ns)
+        us = self._time(fn)
+        n = sum(ns)
+        ops = 2.0 * m * n * k
+        nbytes = m * k / 2 + 4 * m + n * k / 2 + 4 * n + out_bytes
+        tops = ops / (us * 1e-6) / 1e12
+        return {"m": m, "k": k, "n": n, "avg_us": round(us, 3), "ops": ops, "tops": round(tops, 1),
+                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "bytes": nbytes,
+                "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb}
 
 
+def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
+    h, inter = 2048, 16384
+    jobs = {
+        "quant_k2048": lambda: kb.quant(m, h),
+        "quant_k16384": lambda: kb.quant(m, inter),
+        "qkv": lambda: kb.gemm(m, h, [2048, 256, 256]),
+        "o": lambda: kb.gemm(m, h, [2048]),
+        "gate_up": lambda: kb.gemm(m, h, [inter, inter]),
+        "gate_up_gelu": lambda: kb.gemm(m, h, [inter, inter], gelu=True),
+        "down": lambda: kb.gemm(m, inter, [h]),
+    }
+    if only == "copy":  # calibration for the HBM traffic counters: a plain 64 MiB copy
+        src = kb.torch.empty(64 << 20, dtype=kb.torch.uint8, device=kb.dev).fill_(1)
+        dst = kb.torch.empty_like(src)
+        us = kb._time(lambda: dst.copy_(src))
+        return {"copy": {"bytes_read": float(64 << 20), "bytes_written": float(64 << 20), "avg_us": round(us, 3)}}
+    if only:
+        return {only: jobs[only]()}
+    return {name: fn() for name, fn in jobs.items()}
+
+
+def read_traffic() -> tuple[float | None, str | None]:
+    """HBM bytes per launch of the gate/up GEMM from the committed rocprofv3 summary."""
+    if not TRAFFIC_FILE.is_file():
+        return None, None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text())
+    if not m:
+        return None, None
+    return float(m.group(1)), str(TRAFFIC_FILE.relative_to(ROOT))
+
+
+# ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(tokens: int, batch: int, layers: int, budget_s: float) -> dict:
     """CPU oracle (numpy) on one decoder layer's W4A4 work at M = tokens*batch, scaled to
     `layers`.  Per GEMM: quantize the activation (fp32 FWHT + INT4), exact integer matmul
@@ -172,6 +238,7 @@ def cpu_baseline(tokens: int, batch: int, layers: int, budget_s: float) -> dict:
     }
 
 
+# ----------------------------------------------------------------------------- main
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -185,13 +252,20 @@ def main() -> int:
     import torch
 
     from pi05_fast.w4a4 import extension as ext
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ext.preload()
+    m = args.tokens * args.batch
+    kb = KernelBench(torch, ext, dev, args.kernel_iters)
+    if args.only_kernel:
+        print(json.dumps(kernel_table(kb, m, args.only_kernel)), flush=True)
+        return 0
+
     from pi05_fast.w4a4.prefix_lm import build_prefix_lm, prefix_inputs, prefix_ops
 
     if args.fuse_gelu:
         os.environ["PI05_W4A4_FUSE_GELU"] = "1"
-    dev = torch.device("cuda:0")
-    torch.cuda.set_device(dev)
-    ext.preload()
     model, _ = build_prefix_lm(dev, num_layers=args.layers)
     x = prefix_inputs(args.batch, args.tokens, dev)
     s = args.tokens
@@ -238,11 +312,12 @@ def main() -> int:
 
         # Eager forwards, for reference (host-dispatch bound).
         torch.cuda.synchronize()
+        n_eager = max(3, args.steps // 4)
         t0 = time.perf_counter()
-        for _ in range(max(3, args.steps // 4)):
+        for _ in range(n_eager):
             model(x, mask)
         torch.cuda.synchronize()
-        eager_ms = (time.perf_counter() - t0) * 1e3 / max(3, args.steps // 4)
+        eager_ms = (time.perf_counter() - t0) * 1e3 / n_eager
 
         def step():
             if graph is not None:
@@ -258,33 +333,32 @@ def main() -> int:
             step()
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        del graph
 
-        # Per-GEMM kernel times: eager forwards with HIP events around every launch.
-        rec = EventRecorder(torch)
-        ext._launch_hook = rec
-        try:
-            torch.cuda.synchronize()
-            for _ in range(args.kernel_steps):
-                model(x, mask)
-            kernels = rec.summary(args.kernel_steps)
-        finally:
-            ext._launch_hook = None
+        kernels = kernel_table(kb, m)
 
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
-    gemm_classes = [c for c in kernels if not c.startswith("quant")]
-    dominant = max(gemm_classes, key=lambda c: kernels[c]["avg_us"] * kernels[c]["calls_per_forward"])
-    dk = kernels[dominant]
+    calls = {"quant_k2048": 3, "quant_k16384": 1, "qkv": 1, "o": 1, "down": 1,
+             "gate_up": 0 if args.fuse_gelu else 1, "gate_up_gelu": 1 if args.fuse_gelu else 0}
+    for name, c in calls.items():
+        kernels[name]["calls_per_layer"] = c
+    w4a4_us_per_layer = sum(kernels[n]["avg_us"] * c for n, c in calls.items())
+    dk = kernels["gate_up_gelu" if args.fuse_gelu else "gate_up"]
+    traffic, traffic_src = read_traffic()
     roofline = {
         "bound": "mfma",
-        "kernel": dominant,
         "achieved": dk["tops"],
         "peak": INT8_PEAK_TOPS,
         "unit": "TFLOP/s",
         "frac": round(dk["tops"] / INT8_PEAK_TOPS, 4),
-        "traffic": None,
-        "per_launch_ops": dk["ops"],
+        "traffic": traffic,
+        "kernel": "gemm_w4a4_kernel (gate/up, int4_gemm2)",
+        "ops_per_launch": dk["ops"],
         "avg_launch_us": dk["avg_us"],
+        "ops_unit": "int8 MAC x 2 per second (dense int8 MFMA)",
+        "traffic_source": traffic_src,
+        "algorithmic_bytes_per_launch": dk["bytes"],
     }
     out = {
         "metric": METRIC,
@@ -306,13 +380,13 @@ def main() -> int:
             "tokens": args.tokens,
             "batch": args.batch,
             "layers": args.layers,
-            "timed": "hip-graph replay" if graph is not None else "eager",
+            "timed": "hip-graph replay" if not args.no_graph else "eager",
             "fused_gelu_up": bool(args.fuse_gelu),
             "graph_replay_bit_exact_vs_eager": graph_exact,
         },
         "eager_ms_per_forward": round(eager_ms, 3),
         "w4a4_gop_per_forward": round(total_ops / 1e9, 1),
-        "effective_tops_whole_forward": round(total_ops / (ms * 1e-3) / 1e12, 1),
+        "w4a4_kernel_ms_per_forward": round(w4a4_us_per_layer * args.layers / 1e3, 3),
         "gemms": kernels,
         "roofline": roofline,
     }

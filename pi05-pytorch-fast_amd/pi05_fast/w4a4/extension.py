@@ -37,10 +37,6 @@ _LAYOUT_WMMA_TILED = 1
 _LIB_NAME = "libpi05_w4a4.so"
 _lib = None
 _op_registered = False
-# Optional observer used by benchmarks: called as hook(kind, phase, m, k, ns) with phase
-# "begin"/"end" around the GEMM launches of an op (after its activation quant), kind in
-# {"gemm", "gemm2", "gemm3", "gemm2_gelu"}, ns the output widths of the weights.
-_launch_hook = None
 
 
 def library_path() -> Path:
@@ -171,11 +167,7 @@ def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
     lib = load_int4_gemm()
     with torch.cuda.device(x2.device):
-        if _launch_hook is not None:
-            _launch_hook("quant", "begin", m, k, [])
         rc = lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device))
-        if _launch_hook is not None:
-            _launch_hook("quant", "end", m, k, [])
         _check(rc, "pi05w4a4_quantize")
     return q, sa
 
@@ -242,8 +234,6 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
     ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0)
     ws = _workspace(device, ws_bytes)
     stream = _stream(device)
-    if _launch_hook is not None:
-        _launch_hook(kind, "begin", m, k, ns)
     if gelu:
         rc = lib.pi05w4a4_gemm_gelu_up(_ptr(q), _ptr(sa), m, k, _ptr(weights[0][0]),
                                        _ptr(weights[1][0]), ns[0], _ptr(outs[0]), _ptr(ws),
@@ -253,8 +243,6 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
         y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in out_ptrs])
         rc = lib.pi05w4a4_gemm_multi(_ptr(q), _ptr(sa), m, k, g, w_arr, n_arr, y_arr, _ptr(ws),
                                      ws_bytes, stream)
-    if _launch_hook is not None:
-        _launch_hook(kind, "end", m, k, ns)
     _check(rc, "pi05w4a4_gemm")
     results = []
     for o, (w, n_true) in zip(outs, weights):
