@@ -15,17 +15,23 @@
  *
  * Data formats
  *   x      fp16 [M, K] row-major activations (K % 64 == 0), 16-byte aligned.
- *   q      nibble-packed activation codes (values in [-7, 7], two's complement) in the
- *          MFMA-fragment-major layout shared with the weights.  With KB = ceil(K/128),
+ *   q      nibble-packed activation codes (values in [-7, 7]) in the MFMA-fragment-major
+ *          layout shared with the weights.  Byte j of a word holds the codes of k = 2j
+ *          (low nibble, offset binary: code + 8) and k = 2j + 1 (high nibble, two's
+ *          complement); the reference's word is this word XOR 0x08080808.
+ *          With KB = ceil(K/128),
  *          the codes of 16-row block mb and 128-deep k block b form one 1 KB fragment at
  *          word (mb*KB + b)*256 made of 64 16-byte slots: slot L (words 4L .. 4L+3) holds
  *          codes 128*b + 32*(L/16) .. +31 of row 16*mb + L%16, code k in nibble (k & 7)
- *          of its word.  Lane L of an MFMA wave loads slot L and feeds its codes 0-15 and
+ *          of its word (encoded as above).  Lane L of an MFMA wave loads slot L and feeds its codes 0-15 and
  *          16-31 to the block's two v_mfma_i32_16x16x64_i8.  Row-major word (row, kw) of
  *          the reference's [M, K/8] codes therefore sits at
  *          ((row/16)*KB + kw/16)*256 + 4*(row%16 + 16*((kw%16)/4)) + kw%4.
- *          The buffer holds pi05w4a4_q_words(M, K) words (M rounded up to 16 rows, K to
- *          128; padding is never read into an output).  16-byte aligned.
+ *          The codes of ceil(M/16)*16 rows (K rounded up to 128) are followed by one
+ *          int32 per row, qcorr[row] = -128 * (sum of the row's odd-k codes): the GEMM
+ *          unpacks each code byte with one AND and needs these to undo the offsets.
+ *          The buffer holds pi05w4a4_q_words(M, K) words (padding is never read into
+ *          an output).  16-byte aligned.
  *   sa     fp32 [M] per-token activation scales.
  *   w_mfma weights in the gfx950 MFMA-fragment-major layout (see
  *          pi05w4a4_repack_weight).  N % 16 == 0.  Word count pi05w4a4_mfma_words().
@@ -72,14 +78,14 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
 
 /*
  * Words of a quantized-activation buffer q for M rows of K codes:
- * ceil(M/16)*16 * ceil(K/128)*16.
+ * ceil(M/16)*16 * ceil(K/128)*16 code words + ceil(M/16)*16 qcorr words.
  * (The reference keeps row-major [M, K/8] codes inside its QuantizedX, int4_gemm.cu:479-485.)
  */
 size_t pi05w4a4_q_words(int64_t m, int32_t k);
 
 /*
  * Words of the MFMA-fragment-major weight buffer for an [N, K] weight: payload
- * N*ceil(K/128)*16 words followed by N fp32 scale words.  The persistent tensor form is
+ * N*ceil(K/128)*16 words, then N fp32 scale words, then N wcorr words.  The persistent tensor form is
  * int32 [N, K/8 + PI05W4A4_MFMA_MARKER_WORDS], which always holds that many words.
  */
 size_t pi05w4a4_mfma_words(int32_t n, int32_t k);
@@ -94,8 +100,11 @@ size_t pi05w4a4_mfma_words(int32_t n, int32_t k);
  *              for PI05W4A4_LAYOUT_WMMA_TILED;
  *   dst        device buffer of at least pi05w4a4_mfma_words(n, k) int32 words.
  * Layout of dst: the q layout above applied to weight columns (column n in place of row
- * `row`), K padded to a multiple of 128 with zero codes, then dst[N*ceil(K/128)*16 + n]
- * = scale bits of column n.
+ * `row`) with the weight nibble encoding: byte j holds the code of k = 2j in its high
+ * nibble (two's complement) and that of k = 2j + 1 in its low nibble (offset binary).
+ * K is padded to a multiple of 128 with zero words.  Then dst[P + n] = scale bits of
+ * column n and dst[P + N + n] = wcorr[n] = -128 * (sum of column n's even-k codes),
+ * P = N*ceil(K/128)*16.
  */
 int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
                            int64_t src_stride, int32_t* dst, void* stream);
@@ -113,6 +122,7 @@ size_t pi05w4a4_gemm_workspace_bytes(int64_t m, int32_t k, int32_t ngroups, cons
 /*
  * y = fp16((float(acc) * sa[m]) * sw[n]), acc[m,n] = sum_k q[m,k] * w[n,k] in int32.
  * Replaces gemm_from_q + gemm_iu4 / gemm_iu4_shape (int4_gemm.cu:63-394, 566-616).
+ * All GEMM entry points accept K up to 524288 (the int32 MFMA sum is at most 2048 K).
  */
 int pi05w4a4_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k,
                   const int32_t* w_mfma, int32_t n, void* y_fp16, void* workspace,

@@ -46,14 +46,15 @@ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 constexpr int kNumCUs = 256;  // MI355X: 8 XCDs x 32 CUs
 
 struct TileCfg {
-  int id, mi, ni, kw;  // kw = waves of a workgroup along K (the other 4/kw along N)
-  int cols(bool gelu) const { return (gelu ? 8 : 16) * ni * (4 / kw); }  // workgroup tile width
+  int id, mi, ni, nwaves, kw;  // kw of the nwaves waves of a workgroup split K
+  int cols(bool gelu) const { return (gelu ? 8 : 16) * ni * (nwaves / kw); }  // tile width
 };
-constexpr TileCfg kCfg7x4{w4a4::kCfg7x4, 7, 4, 1};
-constexpr TileCfg kCfg7x4K4{w4a4::kCfg7x4K4, 7, 4, 4};
-constexpr TileCfg kCfg4x2{w4a4::kCfg4x2, 4, 2, 1};
-constexpr TileCfg kCfg2x2{w4a4::kCfg2x2, 2, 2, 1};
-constexpr TileCfg kCfg1x2{w4a4::kCfg1x2, 1, 2, 1};
+constexpr TileCfg kCfg7x4{w4a4::kCfg7x4, 7, 4, 4, 1};
+constexpr TileCfg kCfg7x4K4{w4a4::kCfg7x4K4, 7, 4, 4, 4};
+constexpr TileCfg kCfg7x4K8{w4a4::kCfg7x4K8, 7, 4, 8, 8};
+constexpr TileCfg kCfg4x2{w4a4::kCfg4x2, 4, 2, 4, 1};
+constexpr TileCfg kCfg2x2{w4a4::kCfg2x2, 2, 2, 4, 1};
+constexpr TileCfg kCfg1x2{w4a4::kCfg1x2, 1, 2, 4, 1};
 
 struct Plan {
   TileCfg cfg;
@@ -66,7 +67,8 @@ struct Plan {
 // Tile configuration, tile counts and K split for one call.
 //  * M > 64: 112-row tiles (MI = 7: 776 = 7 x 112 - 8).  Wide GEMMs (gate/up) use 4 waves
 //    along N (112 x 256 workgroup tiles); when that leaves fewer than 1.5 workgroups per
-//    CU (QKV, o, down) the 4 waves split K instead (112 x 64 tiles, 4x the workgroups).
+//    CU (QKV, o, down) the waves split K instead (112 x 64 tiles, 4x the workgroups):
+//    4 waves for moderate K, 8 waves (2 per SIMD, each with 1/8 of K) when K >= 8192.
 //  * Small M: narrower tiles; the remaining parallelism comes from a global K split.
 Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
   Plan pl{};
@@ -90,11 +92,10 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
   pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
   pl.ntiles = count_tiles(pl.cfg);
   if (pl.cfg.id == w4a4::kCfg7x4 && 2 * pl.mtiles * pl.ntiles < 3 * kNumCUs) {
-    pl.cfg = kCfg7x4K4;
+    pl.cfg = (k >= 8192) ? kCfg7x4K8 : kCfg7x4K4;
     pl.ntiles = count_tiles(pl.cfg);
   }
   const int nkb = w4a4::kblocks128(k);
-  // |256 * acc| < 2^31 needs <= 65536 k per slice: at most 512 k blocks per slice.
   int ks = 1;
   if (allow_split) {
     // A global split costs an int32 workspace round trip and a reduce launch; it only
@@ -105,16 +106,20 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
   }
   if (ks > nkb) ks = nkb;
   if (ks < 1) ks = 1;
-  int per = static_cast<int>(cdiv(nkb, ks));
-  if (per > 512) per = 512;
+  const int per = static_cast<int>(cdiv(nkb, ks));
   pl.kblocks = per;
   pl.ksplit = static_cast<int>(cdiv(nkb, per));
   return pl;
 }
 
+// The MFMA sum S = 16 acc + row and column terms is bounded by 2048 K: int32 holds it for
+// every K up to 2^19.
+constexpr int32_t kMaxK = 1 << 19;
+
 int validate_gemm_common(const int32_t* q, const float* sa, int64_t m, int32_t k) {
   if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
   if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  if (k > kMaxK) return fail(PI05W4A4_EINVAL, "K must be at most %d, got %d", kMaxK, k);
   if (m > 0 && (q == nullptr || sa == nullptr))
     return fail(PI05W4A4_EINVAL, "null activation codes or scales");
   if (!aligned(q, 16)) return fail(PI05W4A4_EINVAL, "activation codes must be 16-byte aligned");
@@ -203,12 +208,12 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
 
 size_t pi05w4a4_q_words(int64_t m, int32_t k) {
   if (m <= 0 || k <= 0) return 0;
-  return static_cast<size_t>(cdiv(m, 16) * 16) * static_cast<size_t>(w4a4::kblocks128(k)) * 16;
+  return static_cast<size_t>(w4a4::q_total_words(cdiv(m, 16), w4a4::kblocks128(k)));
 }
 
 size_t pi05w4a4_mfma_words(int32_t n, int32_t k) {
   if (n <= 0 || k <= 0) return 0;
-  return static_cast<size_t>(n) * (static_cast<size_t>(w4a4::kblocks128(k)) * 16 + 1);
+  return static_cast<size_t>(n) * (static_cast<size_t>(w4a4::kblocks128(k)) * 16 + 2);
 }
 
 int pi05w4a4_repack_weight(const int32_t* src, int32_t src_layout, int32_t n, int32_t k,
@@ -294,7 +299,6 @@ int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_m
   static const float kDummy = 0.0f;
   int rc = validate_gemm_common(q, &kDummy, m, k);
   if (rc) return rc;
-  if (k > 65536) return fail(PI05W4A4_EINVAL, "accumulator readout supports K <= 65536");
   rc = validate_weight(w_mfma, n, "weight");
   if (rc) return rc;
   if (m > 0 && acc == nullptr) return fail(PI05W4A4_EINVAL, "null accumulator output");

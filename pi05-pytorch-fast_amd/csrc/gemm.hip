@@ -5,31 +5,35 @@
 //   acc[m, n] = sum_k qa[m, k] * qw[n, k]            (int32, exact)
 //   y[m, n]   = fp16((float(acc) * sa[m]) * sw[n])   (two fp32 products, RNE to fp16)
 //
-// INT4 -> INT8.  A packed word holds codes k0..k7 as nibbles 0..7.  Two ALU ops per
-// int8 word produce the codes scaled by 16 with their sign intact:
-//   w & 0xF0F0F0F0        -> bytes 16*k1, 16*k3, 16*k5, 16*k7
-//   (w << 4) & 0xF0F0F0F0 -> bytes 16*k0, 16*k2, 16*k4, 16*k6
-// A and B are unpacked identically, so byte position p of an MFMA operand holds the same
-// k for both (the dot product is invariant under a common permutation of k), and the
-// int32 accumulator equals 256 * acc exactly: |256 * acc| <= 256 * 64 * K < 2^31 for
-// K <= 65536 per K slice (the host splits larger K).  The epilogue shifts it back.
+// INT4 -> INT8.  Packed words hold two codes per byte in the nibble encodings of
+// w4a4_internal.h (activations: offset-binary low nibble, two's complement high nibble;
+// weights: the reverse).  One AND per int8 word unpacks either operand into exact signed
+// bytes (c + 8 or 16 c), and the MFMA pairs every activation byte with the weight byte of
+// the same k, so its int32 sum is
+//   S = 16 * acc + 128 * sum_{k odd} a + 128 * sum_{k even} b.
+// The row and column terms are precomputed (qcorr after the activation codes, wcorr after
+// the weight scales) and the epilogue forms 16 * acc = S + qcorr[m] + wcorr[n] exactly;
+// |S| <= 2048 K < 2^31 for any K the host accepts.  This costs 2 ALU ops per packed word
+// instead of the 3 of a shift-and-mask unpack, which matters: the unpack is the largest
+// non-MFMA cost of the loop.
 //
-// Tiling.  A wave owns a (16*MI) x (16*NI) tile = MI x NI accumulators of 16x16.  The 4
-// waves of a workgroup are arranged NW along N times KW along K (NW * KW = 4): with
-// KW > 1 the waves of one column block split the workgroup's k range into KW contiguous
-// parts and add their accumulators through LDS at the end, which gives narrow GEMMs
-// (QKV, o, down) enough workgroups without a global split-K workspace.
+// Tiling.  A wave owns a (16*MI) x (16*NI) tile = MI x NI accumulators of 16x16.  The
+// NWAVES waves of a workgroup are arranged NW along N times KW along K: with KW > 1 the
+// waves of one column block split the workgroup's k range into KW contiguous parts and
+// fold their accumulators together through LDS at the end, which gives narrow GEMMs
+// (QKV, o, down) enough waves without a global split-K workspace.
 // Both operands live in HBM in the same MFMA-fragment-major layout (frag_word_index: one
 // 1 KB fragment per 16 rows/columns x 128 k; lane L loads slot L = 32 codes of row/
 // column L%16, the operands of the block's two MFMAs), so every operand fetch is one
 // fully coalesced 16-byte-per-lane load straight into registers.  (The vector memory pipeline issues about one wave-wide load
 // per ~20 clocks per CU whatever its width, so 16-byte loads double the operand bandwidth
 // of 8-byte ones.)  The K loop walks 128-deep k blocks through a 2-deep register ring:
-// the loads of block kb + 1 are issued before block kb is multiplied, and a 4-byte-per-
-// lane touch warms the L2 with the weights PF blocks ahead.  There is no LDS traffic and
-// no barrier in the loop: the waves of a workgroup share their A fragments through the
-// L1/L2 caches only.  (A variant staging A through a double-buffered LDS tile measured
-// slower: the per-stage barrier stalls the MFMA pipe more than the shared loads save.)
+// the loads of block kb + 1 are issued before block kb is multiplied.  There is no LDS
+// traffic and no barrier in the loop: the waves of a workgroup share their A fragments
+// through the L1/L2 caches only.  (Measured alternatives that lost: A staged through a
+// double-buffered LDS tile, whose per-stage barrier stalls the MFMA pipe more than the
+// shared loads save; and L2 warm-up touches of the weights a few blocks ahead, whose
+// extra load instructions cost more than the misses they avoid.)
 // Every global load in the loop is unconditional (out-of-range rows, columns and k
 // blocks are clamped to valid addresses and their results are discarded), so the
 // compiler's vmcnt bookkeeping stays exact and the prefetches overlap the MFMAs.
@@ -40,8 +44,10 @@
 // m-minor order.  The m-tiles that share one weight column block therefore run side by
 // side on one XCD and read those weights from its L2.
 //
-// Epilogue modes: fp16 with scales, int32 split-K partials, raw int32 accumulators, and
-// paired gate/up tiles finished as fp16(gelu_tanh(gate) * up).
+// Epilogue.  The weights are MFMA operand A, so each lane ends with four consecutive
+// output columns of one row and writes them as one 8-byte store (16 rows x 32 bytes per
+// store instruction), with no staging.  Modes: fp16 with scales, int32 split-K partials,
+// int32 accumulators, and paired gate/up tiles finished as fp16(gelu_tanh(gate) * up).
 
 #include "w4a4_internal.h"
 
@@ -50,15 +56,17 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr uint32_t kHiNib = 0xF0F0F0F0u;
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ v4i unpack16(uint2 w) {
-  v4i r;
-  r[0] = static_cast<int>((w.x << 4) & kHiNib);
-  r[1] = static_cast<int>(w.x & kHiNib);
-  r[2] = static_cast<int>((w.y << 4) & kHiNib);
-  r[3] = static_cast<int>(w.y & kHiNib);
-  return r;
+// Activation operand bytes: (a[2j] + 8, 16 a[2j+1]) for the 8 codes of word x, then y.
+__device__ __forceinline__ v4i unpack_a(uint32_t x, uint32_t y) {
+  return v4i{static_cast<int>(x & kLoNib), static_cast<int>(x & kHiNib),
+             static_cast<int>(y & kLoNib), static_cast<int>(y & kHiNib)};
+}
+// Weight operand bytes: (16 b[2j], b[2j+1] + 8), aligned with unpack_a's k order.
+__device__ __forceinline__ v4i unpack_w(uint32_t x, uint32_t y) {
+  return v4i{static_cast<int>(x & kHiNib), static_cast<int>(x & kLoNib),
+             static_cast<int>(y & kHiNib), static_cast<int>(y & kLoNib)};
 }
 
 __device__ __forceinline__ float gelu_tanh(float x) {
@@ -77,11 +85,11 @@ __device__ __forceinline__ _Float16 dequant(int32_t acc, float sa, float sw) {
   return static_cast<_Float16>(y);
 }
 
-template <int MI, int NI, int KW, bool GELU, int PF>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w4a4_kernel(const GemmParams p) {
+template <int MI, int NI, int NWAVES, int KW, bool GELU>
+__global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
-  static_assert(KW == 1 || KW == 2 || KW == 4, "4 waves split as NW x KW");
-  constexpr int NW = 4 / KW;
+  static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
+  constexpr int NW = NWAVES / KW;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -133,10 +141,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
   const int wcol = GELU ? (nt * (8 * NI * NW) + wn * (8 * NI))
                         : ((nt - tile_begin) * (16 * NI * NW) + wn * (16 * NI));
 
-  // Fragment base pointers.  Row blocks past M and column blocks past N are clamped to
+  // Fragment base addresses.  Row blocks past M and column blocks past N are clamped to
   // the last valid block; their accumulators are never stored.
   const int nb_last = (N >> 4) - 1;
-  const int32_t* bptr[NI];
+  const char* bbase[NI];
   bool bvalid[NI];
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
@@ -151,13 +159,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
     bvalid[ni] = col < N;
     const int nb = min(col >> 4, nb_last);
-    bptr[ni] = base + static_cast<int64_t>(nb) * KB128 * 256;
+    bbase[ni] = reinterpret_cast<const char*>(base + static_cast<int64_t>(nb) * KB128 * 256);
   }
-  const int32_t* aptr[MI];
+  const char* abase[MI];
 #pragma unroll
   for (int mi = 0; mi < MI; ++mi) {
     const int mb = min(mt * MI + mi, p.mblocks - 1);
-    aptr[mi] = p.q + static_cast<int64_t>(mb) * KB128 * 256;
+    abase[mi] = reinterpret_cast<const char*>(p.q + static_cast<int64_t>(mb) * KB128 * 256);
   }
 
   // k blocks of this wave: part wk of the workgroup's slice.
@@ -178,86 +186,51 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4i{0, 0, 0, 0};
 
   // ---- main loop: A and B straight from global memory into a 2-deep register ring.
-  constexpr int RING = 2;
-  uint4 ra[RING][MI];
-  uint4 rb[RING][NI];
+  // Each load is a scalar fragment base plus one shared unsigned 32-bit lane offset
+  // (global_load_dwordx4 with an SGPR base): no per-load address arithmetic.
+  uint4 ra[2][MI];
+  uint4 rb[2][NI];
   auto load = [&](int kb, uint4 (&a)[MI], uint4 (&b)[NI]) {
-    const int off = min(kb, kb_end - 1) * 256 + lane * 4;  // < 2^31: one fragment column
+    const uint32_t off = static_cast<uint32_t>(min(kb, kb_end - 1)) * 1024u + static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[mi] = *reinterpret_cast<const uint4*>(aptr[mi] + off);
+    for (int mi = 0; mi < MI; ++mi) a[mi] = *reinterpret_cast<const uint4*>(abase[mi] + off);
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) b[ni] = *reinterpret_cast<const uint4*>(bptr[ni] + off);
+    for (int ni = 0; ni < NI; ++ni) b[ni] = *reinterpret_cast<const uint4*>(bbase[ni] + off);
   };
-  // The two MFMAs of a 128-deep block (codes 0-15 and 16-31 of each lane's 32).  Pad
-  // codes of a K that is not a multiple of 128 are zero in the weights: no guard.
+  // The two MFMAs of a 128-deep block (codes 0-15 and 16-31 of each lane's 32).  The
+  // weights are operand A of the MFMA and the activations operand B, so accumulator
+  // element r of lane L is output row 16*mi + L%16, column 16*ni + 4*(L/16) + r: four
+  // consecutive columns of one row per lane.  Pad codes of a K that is not a multiple
+  // of 128 multiply zero weight words: no guard.
   auto compute = [&](const uint4 (&a)[MI], const uint4 (&b)[NI]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       v4i bop[NI];
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        bop[ni] = unpack16(h ? make_uint2(b[ni].z, b[ni].w) : make_uint2(b[ni].x, b[ni].y));
+      for (int ni = 0; ni < NI; ++ni) bop[ni] = h ? unpack_w(b[ni].z, b[ni].w) : unpack_w(b[ni].x, b[ni].y);
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
-        const v4i aop = unpack16(h ? make_uint2(a[mi].z, a[mi].w) : make_uint2(a[mi].x, a[mi].y));
+        const v4i aop = h ? unpack_a(a[mi].z, a[mi].w) : unpack_a(a[mi].x, a[mi].y);
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
-          acc[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(aop, bop[ni], acc[mi][ni], 0, 0, 0);
+          acc[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[ni], aop, acc[mi][ni], 0, 0, 0);
       }
     }
   };
-  // L2 warm-up of the weights PF blocks ahead.  The register ring holds only one block
-  // in flight, which hides an L2 hit but not an HBM miss; the m-tiles that share a column
-  // block all wait on the same miss.  One 4-byte load per lane and block touches every
-  // 128-byte line of the wave's NI weight fragments PF blocks ahead (lane l: fragment
-  // (l/8) % NI, line l % 8), so the ring's own loads find the lines in L2.  The touched
-  // words are folded into a sink that is only read after the loop.
-  const int32_t* tptr = bptr[0];
-#pragma unroll
-  for (int ni = 1; ni < NI; ++ni)
-    if (((lane >> 3) % NI) == ni) tptr = bptr[ni];
-  tptr += (lane & 7) * 32;
-  int tring[PF > 0 ? PF : 1];
-  int tsink = 0;
-  constexpr int UNROLL = (PF == 3) ? 6 : ((PF == 4) ? 4 : 2);  // lcm(RING, PF)
   if (nkb > 0) {
-    if constexpr (PF > 0) {
-#pragma unroll
-      for (int j = 0; j < PF; ++j) tring[j] = tptr[min(kb_begin + j, kb_end - 1) * 256];
-    }
     load(kb_begin, ra[0], rb[0]);
     int i = 0;
-    for (; i + UNROLL <= nkb; i += UNROLL) {
-#pragma unroll
-      for (int j = 0; j < UNROLL; ++j) {
-        const int cur = j % RING;
-        const int nxt = (j + 1) % RING;
-        load(kb_begin + i + j + 1, ra[nxt], rb[nxt]);
-        if constexpr (PF > 0) {
-          tsink ^= tring[j % PF];
-          tring[j % PF] = tptr[min(kb_begin + i + j + PF, kb_end - 1) * 256];
-        }
-        // Keep the prefetch at the top of the step: under register pressure the
-        // scheduler would otherwise sink the loads next to their use.
-        __builtin_amdgcn_sched_barrier(0);
-        compute(ra[cur], rb[cur]);
-      }
+    for (; i + 2 <= nkb; i += 2) {
+      load(kb_begin + i + 1, ra[1], rb[1]);
+      // Keep each prefetch at the top of its step: under register pressure the
+      // scheduler would otherwise sink the loads next to their use.
+      __builtin_amdgcn_sched_barrier(0);
+      compute(ra[0], rb[0]);
+      load(kb_begin + i + 2, ra[0], rb[0]);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(ra[1], rb[1]);
     }
-    // Remainder (< UNROLL blocks): the ring position continues at slot 0.
-#pragma unroll
-    for (int j = 0; j < UNROLL - 1; ++j) {
-      if (i + j < nkb) {
-        const int cur = j % RING;
-        const int nxt = (j + 1) % RING;
-        load(kb_begin + i + j + 1, ra[nxt], rb[nxt]);
-        compute(ra[cur], rb[cur]);
-      }
-    }
-  }
-  if constexpr (PF > 0) {
-#pragma unroll
-    for (int j = 0; j < PF; ++j) tsink ^= tring[j];
-    if (tsink == 0x5f3759df && p.m < 0) static_cast<int32_t*>(Y)[0] = tsink;  // never true: m >= 0
+    if (i < nkb) compute(ra[0], rb[0]);  // odd count: the last block is in slot 0
   }
 
   // ---- k-part reduction through LDS (KW > 1): pairs of k parts are folded until part 0
@@ -277,87 +250,78 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] += red[(slot * NW + wn) * FR + (mi * NI + ni) * 64 + lane];
     };
-    if constexpr (KW == 4) {
-      if (wk >= 2) put(wk - 2);
+#pragma unroll
+    for (int active = KW; active > 1; active /= 2) {
+      const int half = active / 2;
+      if (wk >= half && wk < active) put(wk - half);
       __syncthreads();
-      if (wk < 2) add(wk);
+      if (wk < half) add(wk);
       __syncthreads();
     }
-    if (wk == 1) put(0);
-    __syncthreads();
-    if (wk == 0) add(0);
     if (wk != 0) return;
   }
 
-  // ---- epilogue.  Accumulator element r of fragment (mi, ni) in lane L is
-  // C[16*mi + 4*(L/16) + r][16*ni + L%16] of the wave tile.
-  const int lcol = lane & 15;
-  const int lrow = (lane >> 4) * 4;
+  // ---- epilogue.  Lane L holds rows 16*mi + L%16 and columns 16*ni + 4*(L/16) + 0..3.
+  const int lrow = lane & 15;
+  const int lcol = (lane >> 4) * 4;
+  auto out_col = [&](int ni) {  // first of the lane's four columns of fragment ni
+    return GELU ? (wcol + (ni % (NI / 2)) * 16 + lcol) : (wcol + ni * 16 + lcol);
+  };
+  // Row and column corrections (16 * acc = S + qcorr + wcorr).
+  const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
+  int32_t qc[MI];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi) qc[mi] = qcorr[min(mt * MI + mi, p.mblocks - 1) * 16 + lrow];
+  v4i wc[NI];
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int32_t* wcorr = ((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off + N;
+    wc[ni] = bvalid[ni] ? *reinterpret_cast<const v4i*>(wcorr + out_col(ni)) : v4i{0, 0, 0, 0};
+  }
   if (p.mode == kEpiFp16 || p.mode == kEpiGeluUp) {
-    // fp16 outputs are staged per wave through LDS so that global stores are 16 bytes
-    // per lane and every group of lanes writes whole rows of the wave's tile: 128-byte
-    // lines for a 64-column tile.  The staging area is private to the wave (no barrier).
-    constexpr int OC = GELU ? 8 * NI : 16 * NI;  // output columns of a wave
-    constexpr int RB = 2 * OC;                   // bytes of one output row of a wave
-    constexpr int LS = RB + 8;                   // LDS row stride (conflict-free b16 writes)
-    constexpr int LPR = RB / 16;                 // lanes per row in the write-out
-    constexpr int RPI = 64 / LPR;                // rows per write-out instruction
-    static_assert(RB % 16 == 0, "a wave's output row must be a multiple of 16 bytes");
-    __shared__ __align__(16) unsigned char stage_all[NW * 16 * LS];
-    unsigned char* stage = stage_all + wn * (16 * LS);
-    float sw[NI];
+    // Row scales are pre-multiplied by 1/16, which folds the 16 of the corrected sum into
+    // the scale: float(16 t) * (sa / 16) rounds exactly like float(t) * sa (both
+    // rescalings are exact powers of two and 16 t is at most 2^24 in magnitude).
+    float sv[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) sv[mi] = p.sa[min(m0 + mi * 16 + lrow, M - 1)] * 0.0625f;
+    float4 sw[NI];
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const int col = GELU ? (wcol + (ni % (NI / 2)) * 16 + lcol) : (wcol + ni * 16 + lcol);
-      const int32_t* scales = ((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off;
-      sw[ni] = bvalid[ni] ? __int_as_float(scales[col]) : 0.0f;
+      const float* scales = reinterpret_cast<const float*>(((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off);
+      sw[ni] = bvalid[ni] ? *reinterpret_cast<const float4*>(scales + out_col(ni)) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    // All row scales of the lane are fetched before the first store (the compiler cannot
-    // hoist them across the output stores itself).  They are pre-multiplied by 1/256,
-    // which folds the accumulator's 2^8 factor into the scale: float(256 t) * (sa / 256)
-    // rounds exactly like float(t) * sa (both rescalings are exact powers of two and t
-    // is below 2^24), so the fp16 results are unchanged.
-    float sav[MI][4];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        sav[mi][r] = p.sa[min(m0 + mi * 16 + lrow + r, M - 1)] * 0.00390625f;
     _Float16* y = static_cast<_Float16*>(Y);
-    const int out_lane_col = (lane % LPR) * 8;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
+      const int64_t row = m0 + mi * 16 + lrow;
+      if (row >= M) continue;  // only the last row tile has such lanes
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        _Float16* srow = reinterpret_cast<_Float16*>(stage + (lrow + r) * LS) + lcol;
+      for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
+        if (!bvalid[ni]) continue;
+        const v4i s = acc[mi][ni] + qc[mi] + wc[ni];
+        const float swv[4] = {sw[ni].x, sw[ni].y, sw[ni].z, sw[ni].w};
+        half4 o;
         if (GELU) {
+          const v4i su = acc[mi][ni + NI / 2] + qc[mi] + wc[ni + NI / 2];
+          const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
 #pragma unroll
-          for (int ni = 0; ni < NI / 2; ++ni) {
-            const float g = static_cast<float>(dequant(acc[mi][ni][r], sav[mi][r], sw[ni]));
-            const float u = static_cast<float>(dequant(acc[mi][ni + NI / 2][r], sav[mi][r], sw[ni + NI / 2]));
-            srow[ni * 16] = static_cast<_Float16>(gelu_tanh(g) * u);
+          for (int r = 0; r < 4; ++r) {
+            const float g = static_cast<float>(dequant(s[r], sv[mi], swv[r]));
+            const float u = static_cast<float>(dequant(su[r], sv[mi], swu[r]));
+            o[r] = static_cast<_Float16>(gelu_tanh(g) * u);
           }
         } else {
 #pragma unroll
-          for (int ni = 0; ni < NI; ++ni) srow[ni * 16] = dequant(acc[mi][ni][r], sav[mi][r], sw[ni]);
+          for (int r = 0; r < 4; ++r) o[r] = dequant(s[r], sv[mi], swv[r]);
         }
+        *reinterpret_cast<half4*>(y + row * N + out_col(ni)) = o;
       }
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < (16 + RPI - 1) / RPI; ++j) {
-        const int rr = j * RPI + lane / LPR;
-        const int64_t grow = m0 + mi * 16 + rr;
-        const int gcol = wcol + out_lane_col;
-        if (rr < 16 && grow < M && gcol < N) {
-          const uint4 v = *reinterpret_cast<const uint4*>(stage + rr * LS + (lane % LPR) * 16);
-          *reinterpret_cast<uint4*>(y + grow * N + gcol) = v;
-        }
-      }
-      __builtin_amdgcn_wave_barrier();
     }
   } else {
-    // kEpiPartial: int32 [ksplit, M, n_total] at column col_off + col;
-    // kEpiAcc:     int32 [M, N] in the group's output.
+    // kEpiPartial: raw sums S, int32 [ksplit, M, n_total] at column col_off + col (the
+    // corrections are added once after the K slices are summed);
+    // kEpiAcc:     int32 [M, N] accumulators of the group, (S + qcorr + wcorr) / 16.
     int32_t* out;
     int64_t ld;
     if (p.mode == kEpiPartial) {
@@ -369,22 +333,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void g
     }
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
+      const int64_t row = m0 + mi * 16 + lrow;
+      if (row >= M) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = m0 + mi * 16 + lrow + r;
-        if (row >= M) continue;
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) {
-          if (!bvalid[ni]) continue;
-          int col;
-          if (GELU) {
-            // partial columns: gate block [0, N), up block [N, 2N)
-            col = wcol + (ni % (NI / 2)) * 16 + lcol + ((ni >= NI / 2) ? N : 0);
-          } else {
-            col = wcol + ni * 16 + lcol;
-          }
-          out[row * ld + col] = acc[mi][ni][r] >> 8;
-        }
+      for (int ni = 0; ni < NI; ++ni) {
+        if (!bvalid[ni]) continue;
+        // partial columns in GELU mode: gate block [0, N), up block [N, 2N)
+        const int col = out_col(ni) + ((GELU && ni >= NI / 2) ? N : 0);
+        v4i v = acc[mi][ni];
+        if (p.mode == kEpiAcc) v = (v + qc[mi] + wc[ni]) >> 4;  // exact: a multiple of 16
+        *reinterpret_cast<v4i*>(out + row * ld + col) = v;
       }
     }
   }
@@ -403,7 +361,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   const int c = static_cast<int>(idx % quads) * 4;
   const int64_t scale_off = static_cast<int64_t>(kblocks128(p.k)) * 16;
   const int64_t plane = M * p.n_total;
-  const float sav = p.sa[row];
+  const float sav = p.sa[row] * 0.0625f;  // the sums below are 16 * acc
+  const int32_t qc = p.q[q_payload_words(p.mblocks, kblocks128(p.k)) + row];
   if (GELU) {
     const int N = p.gelu_pair_n;
     int4 g = make_int4(0, 0, 0, 0), u = make_int4(0, 0, 0, 0);
@@ -416,8 +375,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
     }
     const float* swg = reinterpret_cast<const float*>(p.g[0].w + N * scale_off);
     const float* swu = reinterpret_cast<const float*>(p.g[1].w + N * scale_off);
-    const int gv[4] = {g.x, g.y, g.z, g.w};
-    const int uv[4] = {u.x, u.y, u.z, u.w};
+    const int32_t* wcg = p.g[0].w + N * scale_off + N;
+    const int32_t* wcu = p.g[1].w + N * scale_off + N;
+    const int gv[4] = {g.x + qc + wcg[c], g.y + qc + wcg[c + 1], g.z + qc + wcg[c + 2], g.w + qc + wcg[c + 3]};
+    const int uv[4] = {u.x + qc + wcu[c], u.y + qc + wcu[c + 1], u.z + qc + wcu[c + 2], u.w + qc + wcu[c + 3]};
     _Float16* y = static_cast<_Float16*>(p.g[0].y) + row * N + c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -450,20 +411,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   }
   const int col = c - off;
   const float* sw = reinterpret_cast<const float*>(W + N * scale_off);
+  const int32_t* wc = W + N * scale_off + N + col;
   _Float16* y = static_cast<_Float16*>(Y) + row * N + col;
-  const int sv[4] = {s.x, s.y, s.z, s.w};
+  const int sv[4] = {s.x + qc + wc[0], s.y + qc + wc[1], s.z + qc + wc[2], s.w + qc + wc[3]};
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = dequant(sv[e], sav, sw[col + e]);
 }
 
-template <int MI, int NI, int KW, int PF = 3>
+template <int MI, int NI, int NWAVES, int KW>
 hipError_t launch_cfg(const GemmParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles),
                   static_cast<unsigned>(p.ksplit));
   if (p.mode == kEpiGeluUp || (p.mode == kEpiPartial && p.gelu_pair_n > 0))
-    gemm_w4a4_kernel<MI, NI, KW, true, PF><<<grid, 256, 0, stream>>>(p);
+    gemm_w4a4_kernel<MI, NI, NWAVES, KW, true><<<grid, 64 * NWAVES, 0, stream>>>(p);
   else
-    gemm_w4a4_kernel<MI, NI, KW, false, PF><<<grid, 256, 0, stream>>>(p);
+    gemm_w4a4_kernel<MI, NI, NWAVES, KW, false><<<grid, 64 * NWAVES, 0, stream>>>(p);
   return hipGetLastError();
 }
 
@@ -471,12 +433,13 @@ hipError_t launch_cfg(const GemmParams& p, hipStream_t stream) {
 
 hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
   switch (tile_cfg) {
-    case kCfg7x4: return launch_cfg<7, 4, 1>(p, stream);
-    case kCfg7x4K4: return launch_cfg<7, 4, 4>(p, stream);
-    case kCfg7x2: return launch_cfg<7, 2, 1>(p, stream);
-    case kCfg4x2: return launch_cfg<4, 2, 1>(p, stream);
-    case kCfg2x2: return launch_cfg<2, 2, 1>(p, stream);
-    case kCfg1x2: return launch_cfg<1, 2, 1>(p, stream);
+    case kCfg7x4: return launch_cfg<7, 4, 4, 1>(p, stream);
+    case kCfg7x4K4: return launch_cfg<7, 4, 4, 4>(p, stream);
+    case kCfg7x4K8: return launch_cfg<7, 4, 8, 8>(p, stream);
+    case kCfg7x2: return launch_cfg<7, 2, 4, 1>(p, stream);
+    case kCfg4x2: return launch_cfg<4, 2, 4, 1>(p, stream);
+    case kCfg2x2: return launch_cfg<2, 2, 4, 1>(p, stream);
+    case kCfg1x2: return launch_cfg<1, 2, 4, 1>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

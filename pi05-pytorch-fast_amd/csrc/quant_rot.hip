@@ -12,7 +12,9 @@
 // chunks of 8 consecutive elements; element i = e + 8*(t + T*j), e in [0,8), j in [0,J).
 // Every chunk is one 16-byte fp16 load (the row is read fully coalesced) and one packed
 // int32 store into the fragment-major code layout that the GEMM reads (frag_word_index in
-// w4a4_internal.h).  The radix-2 stages of the
+// w4a4_internal.h), with the low nibbles in offset binary (the activation encoding of that
+// header).  Each row also gets its correction qcorr = -128 * (sum of its odd-k codes),
+// stored after the code fragments.  The radix-2 stages of the
 // unnormalised Sylvester transform run in increasing order of the stride h:
 //   h = 1, 2, 4            inside a chunk (registers),
 //   h = 8 .. 256           across lanes of the wave (lane xor 1..32),
@@ -34,7 +36,34 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Eight codes clamp(rint(v / sdiv), -7, 7) packed as nibbles 0..7 of one word.
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// 16 * (sum of the four codes in the high nibbles of w, the odd-k codes): a signed dot
+// product of the bytes 16c with ones.
+__device__ __forceinline__ int odd_code_sum16(uint32_t w) {
+  return __builtin_amdgcn_sdot4(static_cast<int>(w & kHiNib), 0x01010101, 0, false);
+}
+
+// Sum over the T threads of a row (T / 64 waves); the result is valid in thread 0.
+template <int T>
+__device__ __forceinline__ int row_sum(int v, int* red) {
+  v = wave_sum(v);
+  if constexpr (T > 64) {
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    v = red[0];
+#pragma unroll
+    for (int i = 1; i < T / 64; ++i) v += red[i];
+  }
+  return v;
+}
+
+// Eight codes clamp(rint(v / sdiv), -7, 7) packed as nibbles 0..7 of one word (two's
+// complement; the stores flip the low nibbles to offset binary).
 __device__ __forceinline__ int32_t quant_pack8(const float (&v)[8], float sdiv) {
   uint32_t word = 0;
 #pragma unroll
@@ -81,7 +110,9 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 template <int K, int T>
 __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict__ x, int64_t m,
                                                       int32_t* __restrict__ q,
-                                                      float* __restrict__ sa, float inv_sqrt_k) {
+                                                      float* __restrict__ sa,
+                                                      int32_t* __restrict__ qcorr,
+                                                      float inv_sqrt_k) {
   constexpr int J = K / (8 * T);
   static_assert(J >= 1 && K == 8 * T * J, "K must be 8*T*J");
   static_assert(T >= 64 && (T & (T - 1)) == 0, "T must be a power of two >= 64");
@@ -89,6 +120,7 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
   constexpr int JG = J < 4 ? J : 4;
   __shared__ __align__(16) float xch[(T > 64) ? 8 * T * JG : 1];
   __shared__ float red[T / 64];
+  __shared__ int ired[T / 64];
 
   const int64_t row = blockIdx.x;
   if (row >= m) return;
@@ -183,8 +215,15 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
 
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
+  int s16 = 0;
 #pragma unroll
-  for (int j = 0; j < J; ++j) q[frag_word_index(row, t + T * j, kblocks128(K))] = quant_pack8(v[j], sdiv);
+  for (int j = 0; j < J; ++j) {
+    const uint32_t w = static_cast<uint32_t>(quant_pack8(v[j], sdiv));
+    s16 += odd_code_sum16(w);
+    q[frag_word_index(row, t + T * j, kblocks128(K))] = static_cast<int32_t>(w ^ kObFlipLo);
+  }
+  s16 = row_sum<T>(s16, ired);
+  if (t == 0) qcorr[row] = -8 * s16;
 }
 
 // Register-FFT form of the same transform for K = 2^LOGK, T = 2^LOGT threads per row.
@@ -205,7 +244,7 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
 template <int LOGK, int LOGT, int ROWS>
 __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     const _Float16* __restrict__ x, int64_t m, int32_t* __restrict__ q, float* __restrict__ sa,
-    float inv_sqrt_k) {
+    int32_t* __restrict__ qcorr, float inv_sqrt_k) {
   constexpr int K = 1 << LOGK;
   constexpr int T = 1 << LOGT;
   constexpr int r = LOGK - LOGT;
@@ -217,6 +256,7 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
   constexpr int LROW = K + 4 * (K / R);  // LDS floats per row (4 pad floats per R)
   __shared__ __align__(16) float lds[ROWS * LROW];
   __shared__ float red[ROWS * (T / 64 > 0 ? T / 64 : 1)];
+  __shared__ int ired[T / 64];
 
   const int sub = threadIdx.x >> LOGT;
   const int t = threadIdx.x & (T - 1);
@@ -330,17 +370,24 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
 #pragma unroll
     for (int u = 0; u < RUN / 8; u += 2) {
       const int e0 = elem(PASSES - 1, t, g + (1 << LAST_W) * 8 * u);
-      const uint2 wd = make_uint2(words[g * (RUN / 8) + u], words[g * (RUN / 8) + u + 1]);
+      const uint2 wd = make_uint2(words[g * (RUN / 8) + u] ^ kObFlipLo, words[g * (RUN / 8) + u + 1] ^ kObFlipLo);
       *reinterpret_cast<uint2*>(&q[frag_word_index(row, e0 >> 3, kblocks128(K))]) = wd;
     }
+  int s16 = 0;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) s16 += odd_code_sum16(words[i]);
+  s16 = row_sum<T>(s16, ired);  // T == 64: one wave per row, no barrier
+  if (t == 0) qcorr[row] = -8 * s16;
 }
 
 // Unrotated quantization for every other K (K % 64 == 0): int4_gemm.cu:451-477.
 // One workgroup of 256 threads per row, two passes over the row (amax, then codes).
 __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restrict__ x, int64_t m,
                                                          int32_t k, int32_t* __restrict__ q,
-                                                         float* __restrict__ sa) {
+                                                         float* __restrict__ sa,
+                                                         int32_t* __restrict__ qcorr) {
   __shared__ float red[4];
+  __shared__ int ired[4];
   const int64_t row = blockIdx.x;
   if (row >= m) return;
   const int t = threadIdx.x;
@@ -355,13 +402,18 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
   amax = block_max<256>(amax, red);
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (t == 0) sa[row] = sdiv;
+  int s16 = 0;
   for (int c = t; c < chunks; c += 256) {
     const half8 h = *reinterpret_cast<const half8*>(xr + 8 * c);
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(h[e]);
-    q[frag_word_index(row, c, kblocks128(k))] = quant_pack8(v, sdiv);
+    const uint32_t w = static_cast<uint32_t>(quant_pack8(v, sdiv));
+    s16 += odd_code_sum16(w);
+    q[frag_word_index(row, c, kblocks128(k))] = static_cast<int32_t>(w ^ kObFlipLo);
   }
+  s16 = row_sum<256>(s16, ired);
+  if (t == 0) qcorr[row] = -8 * s16;
 }
 
 }  // namespace
@@ -370,20 +422,21 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
                            float inv_sqrt_k, hipStream_t stream) {
   if (m <= 0) return hipSuccess;
   const _Float16* xh = static_cast<const _Float16*>(x);
+  int32_t* qcorr = q + q_payload_words((m + 15) / 16, kblocks128(k));
   const dim3 grid(static_cast<unsigned>(m));
   switch (k) {
     case 16384:
-      fwht_quant_kernel<14, 8, 1><<<grid, 256, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);
+      fwht_quant_kernel<14, 8, 1><<<grid, 256, 0, stream>>>(xh, m, q, sa, qcorr, inv_sqrt_k);
       break;
     case 2048:
       fwht_quant_kernel<11, 6, 4><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
-          xh, m, q, sa, inv_sqrt_k);
+          xh, m, q, sa, qcorr, inv_sqrt_k);
       break;
     case 1024:
-      quant_rot_kernel<1024, 128><<<grid, 128, 0, stream>>>(xh, m, q, sa, inv_sqrt_k);
+      quant_rot_kernel<1024, 128><<<grid, 128, 0, stream>>>(xh, m, q, sa, qcorr, inv_sqrt_k);
       break;
     default:
-      quant_rows_kernel<<<grid, 256, 0, stream>>>(xh, m, k, q, sa);
+      quant_rows_kernel<<<grid, 256, 0, stream>>>(xh, m, k, q, sa, qcorr);
       break;
   }
   return hipGetLastError();

@@ -10,8 +10,12 @@
 // 16-column block and 128-deep k block one contiguous 1 KB fragment of 64 16-byte slots,
 // slot L = codes 32*(L/16) .. +31 of column 16*nb + L%16.  Fragments of one column block
 // are consecutive along K, so a wave streams its weights with fully coalesced
-// 16-byte-per-lane loads.  K is padded to a multiple of 128 with zero codes; the fp32
-// column scales follow the payload.
+// 16-byte-per-lane loads.  Each byte is re-encoded for the GEMM's one-AND unpack (the
+// weight encoding of w4a4_internal.h): the even-k code moves to the high nibble (two's
+// complement) and the odd-k code to the low nibble (offset binary).  K is padded to a
+// multiple of 128 with zero words.  The fp32 column scales follow the payload, and the
+// column corrections wcorr[n] = -128 * (sum of the even-k codes of column n) follow the
+// scales.
 //
 // One thread per destination word: the writes are coalesced, the reads are gathers from
 // a layout that is only read once (this runs at load time, not per call).
@@ -20,6 +24,12 @@
 
 namespace w4a4 {
 namespace {
+
+// Reference word (code 8kw+e in nibble e, two's complement) -> weight encoding.
+__device__ __forceinline__ int32_t encode_weight_word(int32_t w) {
+  const uint32_t u = static_cast<uint32_t>(w);
+  return static_cast<int32_t>(((u & kLoNib) << 4) | (((u >> 4) & kLoNib) ^ kObFlipLo));
+}
 
 __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__ src, int32_t layout,
                                                      int32_t n, int32_t k, int64_t stride,
@@ -40,7 +50,7 @@ __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__
     int32_t v = 0;
     if (kw < kw_total) {
       const int64_t s = (layout == 0) ? col * stride + kw : ((kw >> 1) * n + col) * 2 + (kw & 1);
-      v = src[s];
+      v = encode_weight_word(src[s]);
     }
     dst[idx] = v;
   } else if (idx < payload + n) {
@@ -51,6 +61,26 @@ __global__ __launch_bounds__(256) void repack_kernel(const int32_t* __restrict__
   }
 }
 
+// wcorr of one column per wave: 16 * (even-k code sum) of a reference word is the signed
+// dot product of its low-nibble bytes 16c with ones.
+__global__ __launch_bounds__(256) void weight_corr_kernel(const int32_t* __restrict__ src,
+                                                          int32_t layout, int32_t n, int32_t k,
+                                                          int64_t stride, int32_t* __restrict__ dst) {
+  const int32_t col = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (col >= n) return;
+  const int32_t kw_total = k / 8;
+  int s16 = 0;
+  for (int32_t kw = lane; kw < kw_total; kw += 64) {
+    const int64_t s = (layout == 0) ? col * stride + kw : ((kw >> 1) * static_cast<int64_t>(n) + col) * 2 + (kw & 1);
+    const uint32_t w = static_cast<uint32_t>(src[s]);
+    s16 = __builtin_amdgcn_sdot4(static_cast<int>((w << 4) & kHiNib), 0x01010101, s16, false);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) s16 += __shfl_xor(s16, o, 64);
+  if (lane == 0) dst[static_cast<int64_t>(n) * kblocks128(k) * 16 + n + col] = -8 * s16;
+}
+
 }  // namespace
 
 hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t k,
@@ -59,6 +89,8 @@ hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t 
   const int64_t blocks = (total + 255) / 256;
   repack_kernel<<<dim3(static_cast<unsigned>(blocks)), 256, 0, stream>>>(src, layout, n, k,
                                                                          src_stride, dst);
+  weight_corr_kernel<<<dim3(static_cast<unsigned>((n + 3) / 4)), 256, 0, stream>>>(src, layout, n, k,
+                                                                               src_stride, dst);
   return hipGetLastError();
 }
 

@@ -19,14 +19,14 @@ enum EpilogueMode : int {
 };
 
 struct GemmGroup {
-  const int32_t* w;  // MFMA-layout payload (scales follow at w + N*kblocks128(K)*16)
+  const int32_t* w;  // MFMA-layout payload; fp32 scales at w + N*kblocks128(K)*16, wcorr after them
   void* y;           // fp16 [M, N] output (or int32 for kEpiAcc)
   int32_t n;         // output columns
   int32_t tile_begin;  // first global n-tile index of this group
 };
 
 struct GemmParams {
-  const int32_t* q;   // activation codes, MFMA-fragment-major (frag_word_index)
+  const int32_t* q;   // activation codes, MFMA-fragment-major (frag_word_index), then qcorr
   const float* sa;    // fp32 [M]
   int64_t m;
   int32_t mblocks;    // ceil(M / 16): 16-row blocks held by q
@@ -53,16 +53,45 @@ struct GemmParams {
 // block together cover its 128 codes once.  A and B share this k permutation, which
 // leaves the integer dot product unchanged.  A line's 32 consecutive codes are
 // contiguous, so the quantizer writes them as whole 16-byte slots.
-// K is padded to a multiple of 128; weight pad codes are 0.
+// K is padded to a multiple of 128; weight pad words are 0.
 // Word index of packed word kw (codes 8*kw .. 8*kw+7) of line r, kb128 = ceil(K/128):
 __host__ __device__ inline int64_t frag_word_index(int64_t r, int32_t kw, int32_t kb128) {
   return ((r >> 4) * kb128 + (kw >> 4)) * 256 + ((r & 15) + 16 * ((kw & 15) >> 2)) * 4 + (kw & 3);
 }
 
+// Nibble encodings.  Byte j of a packed word holds the codes of k = 2j and k = 2j + 1
+// (j = 0..3 within the word's 8 codes).  A nibble is either two's complement ("tc", code
+// c as c & 15) or offset binary ("ob", c + 8):
+//   activations: low nibble = ob(a[2j]),   high nibble = tc(a[2j+1])
+//   weights:     high nibble = tc(b[2j]),  low nibble = ob(b[2j+1])
+// One AND per int8 word unpacks either operand: w & 0x0F0F0F0F gives bytes c + 8 and
+// w & 0xF0F0F0F0 gives bytes 16c, both exact signed int8.  Pairing the activation's
+// (a[2j] + 8) with the weight's 16 b[2j], and 16 a[2j+1] with (b[2j+1] + 8), the MFMA
+// sums
+//   S = 16 * sum_k a[k] b[k] + 128 * sum_{k odd} a[k] + 128 * sum_{k even} b[k]
+// exactly in int32 (|S| <= 2048 K).  The last two terms are a row term and a column term,
+// stored with the codes as int32 corrections
+//   qcorr[m] = -128 * sum_{k odd} a[m, k]      (after the activation fragments)
+//   wcorr[n] = -128 * sum_{k even} b[n, k]     (after the weight scales)
+// so that S + qcorr[m] + wcorr[n] = 16 * acc[m, n].  Zero weight pad words contribute
+// nothing whatever the activation pad holds.
+constexpr uint32_t kLoNib = 0x0F0F0F0Fu;
+constexpr uint32_t kHiNib = 0xF0F0F0F0u;
+constexpr uint32_t kObFlipLo = 0x08080808u;  // tc <-> ob on the low nibbles
+
+// Words of activation codes for M rows (fragments of ceil(M/16) row blocks), followed by
+// qcorr for every row of those blocks.
+__host__ __device__ inline int64_t q_payload_words(int64_t mblocks, int32_t kb128) {
+  return mblocks * 16 * kb128 * 16;
+}
+__host__ __device__ inline int64_t q_total_words(int64_t mblocks, int32_t kb128) {
+  return q_payload_words(mblocks, kb128) + mblocks * 16;
+}
+
 __host__ __device__ inline int32_t kblocks128(int32_t k) { return (k + 127) >> 7; }
 
-// GEMM tile configurations: wave tile (16*MI) x (16*NI); K4 = the 4 waves of a
-// workgroup split K (one column block per workgroup) instead of N.
+// GEMM tile configurations: wave tile (16*MI) x (16*NI); K4 / K8 = the 4 / 8 waves of
+// a workgroup split K (one column block per workgroup) instead of N.
 enum TileCfg : int {
   kCfg7x4 = 0,    // MI 7, NI 4, 4 waves along N: workgroup tile 112 x 256
   kCfg7x2 = 1,    // MI 7, NI 2, 4 waves along N: 112 x 128
@@ -70,6 +99,7 @@ enum TileCfg : int {
   kCfg2x2 = 3,    // MI 2, NI 2: 32 x 128
   kCfg1x2 = 4,    // MI 1, NI 2: 16 x 128
   kCfg7x4K4 = 5,  // MI 7, NI 4, 4 waves along K: 112 x 64
+  kCfg7x4K8 = 6,  // MI 7, NI 4, 8 waves along K (2 per SIMD): 112 x 64, for very long K
 };
 
 // Launchers (return hipError_t of the launch).

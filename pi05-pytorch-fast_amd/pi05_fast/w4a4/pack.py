@@ -148,10 +148,49 @@ def mfma_word_permutation(n: int, k: int, device: torch.device | str = "cpu") ->
     return perm
 
 
+# Nibble encodings of the MFMA layouts.  Byte j of a packed word holds the codes of
+# k = 2j and 2j+1.  The reference packs both in two's complement (k = 2j in the low
+# nibble).  The MFMA layouts store one nibble of each byte in offset binary (code + 8) so
+# that the GPU unpacks either operand with one AND per int8 word:
+#   activations: low nibble = a[2j] + 8,  high nibble = a[2j+1] (two's complement)
+#   weights:     high nibble = b[2j],     low nibble = b[2j+1] + 8
+# The offsets add 128 * (sum of odd-k activation codes) per row and 128 * (sum of even-k
+# weight codes) per column to the integer dot product; those sums, times -128, are stored
+# after the activation codes (qcorr) and after the weight scales (wcorr).
+_LO = 0x0F0F0F0F
+_FLIP = 0x08080808
+
+
+def _u32(words: torch.Tensor) -> torch.Tensor:
+    return words.to(torch.int64) & 0xFFFFFFFF
+
+
+def _i32(words: torch.Tensor) -> torch.Tensor:
+    return torch.where(words >= 2**31, words - 2**32, words).to(torch.int32)
+
+
+def encode_weight_words(words: torch.Tensor) -> torch.Tensor:
+    """Reference int32 code words -> the MFMA weight encoding (nibbles of each byte swapped,
+    new low nibble in offset binary)."""
+    u = _u32(words)
+    return _i32(((u & _LO) << 4) | (((u >> 4) & _LO) ^ _FLIP))
+
+
+def decode_weight_words(words: torch.Tensor) -> torch.Tensor:
+    """Inverse of ``encode_weight_words``."""
+    u = _u32(words)
+    return _i32((((u & _LO) ^ _FLIP) << 4) | ((u >> 4) & _LO))
+
+
+def flip_activation_words(words: torch.Tensor) -> torch.Tensor:
+    """Reference code words <-> the MFMA activation encoding (its own inverse)."""
+    return _i32(_u32(words) ^ _FLIP)
+
+
 def pack_mfma_weight(packed: torch.Tensor, k: int | None = None) -> torch.Tensor:
     """L1/L2 packed weight -> MFMA-fragment-major int32 [N, K/8+16] (CPU/offline form of the
-    device repack): payload in ``fragment_word_index`` order (pad codes 0), then the N
-    fp32 scale words."""
+    device repack): encoded payload in ``fragment_word_index`` order (pad words 0), then the
+    N fp32 scale words, then the N column corrections wcorr = -128 * (even-k code sum)."""
     n = packed.shape[0]
     if k is None:
         k = (packed.shape[1] - 1) * 8
@@ -159,27 +198,41 @@ def pack_mfma_weight(packed: torch.Tensor, k: int | None = None) -> torch.Tensor
     out = torch.zeros((n, words + MFMA_MARKER_WORDS), dtype=torch.int32, device=packed.device)
     flat = out.view(-1)
     idx = fragment_word_index(n, k, packed.device).reshape(-1)
-    flat[idx] = packed[:, :words].contiguous().view(-1)
+    flat[idx] = encode_weight_words(packed[:, :words].contiguous()).view(-1)
     pw = mfma_payload_words(n, k)
     flat[pw : pw + n] = packed[:, words]
+    codes = unpack_nibbles(packed[:, :words], k)
+    flat[pw + n : pw + 2 * n] = (-128 * codes[:, 0::2].sum(dim=1)).to(torch.int32)
     return out
 
 
 def unpack_mfma_weight(mfma: torch.Tensor, k: int) -> torch.Tensor:
     """Inverse of ``pack_mfma_weight``: MFMA layout -> L1 [N, K/8+1]."""
     n = mfma.shape[0]
-    words = k // 8
     flat = mfma.contiguous().view(-1)
     idx = fragment_word_index(n, k, mfma.device)
     pw = mfma_payload_words(n, k)
-    return torch.cat([flat[idx], flat[pw : pw + n, None]], dim=1)
+    return torch.cat([decode_weight_words(flat[idx]), flat[pw : pw + n, None]], dim=1)
+
+
+def mfma_weight_corrections(mfma: torch.Tensor, k: int) -> torch.Tensor:
+    """The wcorr words [N] of an MFMA-layout weight."""
+    n = mfma.shape[0]
+    pw = mfma_payload_words(n, k)
+    return mfma.contiguous().view(-1)[pw + n : pw + 2 * n]
 
 
 def codes_from_fragment_major(q: torch.Tensor, m: int, k: int) -> torch.Tensor:
     """Fragment-major quantized activations (as written by the GPU quantizer) ->
     the reference's row-major int32 words [M, K/8] (``quantize_x``'s ``q``)."""
     flat = q.reshape(-1)
-    return flat[fragment_word_index(m, k, q.device)]
+    return flip_activation_words(flat[fragment_word_index(m, k, q.device)])
+
+
+def qcorr_from_fragment_major(q: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    """The qcorr words [M] stored after the fragment-major activation codes."""
+    pw = ((m + 15) // 16) * 16 * ((k + 127) // 128) * 16
+    return q.reshape(-1)[pw : pw + m]
 
 
 def quant_activation_cpu(x: torch.Tensor, rotate: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:

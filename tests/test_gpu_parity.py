@@ -37,6 +37,16 @@ def _codes(q: torch.Tensor, m: int, k: int) -> np.ndarray:
     return orc.unpack_nibbles(_words(q, m, k), k)
 
 
+def _assert_qcorr(q: torch.Tensor, codes: np.ndarray, what: str) -> None:
+    """The row corrections after the codes: -128 * (sum of the row's odd-k codes)."""
+    from pi05_fast.w4a4.pack import qcorr_from_fragment_major
+
+    m, k = codes.shape
+    got = inp.to_np(qcorr_from_fragment_major(q.cpu(), m, k))
+    want = -128 * codes[:, 1::2].astype(np.int64).sum(axis=1)
+    assert np.array_equal(got, want), f"{what}: qcorr differs"
+
+
 def _assert_codes_equal(got: np.ndarray, want: np.ndarray, what: str) -> None:
     diff = got.astype(np.int32) - want.astype(np.int32)
     nbad = int(np.count_nonzero(diff))
@@ -58,6 +68,7 @@ def test_quantize_matches_golden(golden, ext, cuda, k):
     q, sa = ext.quantize(x)
     torch.cuda.synchronize()
     _assert_codes_equal(_codes(q, x.shape[0], k), golden[f"act_q_{k}"], f"golden K={k}")
+    _assert_qcorr(q, golden[f"act_q_{k}"], f"golden K={k}")
     assert np.array_equal(inp.to_np(sa).view(np.int32), golden[f"act_s_{k}"].view(np.int32))
 
 
@@ -74,6 +85,7 @@ def test_quantize_matches_oracle(ext, cuda, m, k, kind):
     q_ref, s_ref = orc.quant_activation(x.numpy())
     _assert_codes_equal(_codes(q, m, k), q_ref, f"M={m} K={k} {kind}")
     assert np.array_equal(_words(q, m, k), orc.pack_nibbles(q_ref)), "packed words differ"
+    _assert_qcorr(q, q_ref, f"M={m} K={k}")
     assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32)), "scale bits differ"
 
 
@@ -103,6 +115,7 @@ def test_quantize_exact_ties(ext, cuda, k):
     q_ref, s_ref = orc.quant_activation(x16)
     got = _codes(q, m, k)
     _assert_codes_equal(got, q_ref, f"ties K={k}")
+    _assert_qcorr(q, q_ref, f"ties K={k}")
     assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32))
     # half-even: 2.5 -> 2, -2.5 -> -2, 0.5 -> 0, 3.5 -> 4, 1.5 -> 2, -6.5 -> -6, 4.5 -> 4
     r0_cols = np.flatnonzero(y[0])

@@ -87,8 +87,10 @@ def test_payload_and_scales_round_trip(pack):
 def test_mfma_layout_definition(pack, n, k):
     """Fragment (column block nb, 128-deep block t) is 1 KB at word (nb*KB + t)*256 made of
     64 16-byte slots; slot L holds codes 128*t + 32*(L//16) .. +31 of column 16*nb + L%16
-    (zero codes past K), so lane L's two MFMA operands are codes 0-15 and 16-31 of it and
-    the 4 lane groups cover the block's 128 codes once.  The scales follow the payload."""
+    (zero words past K), so lane L's two MFMA operands are codes 0-15 and 16-31 of it and
+    the 4 lane groups cover the block's 128 codes once.  Byte j of a word holds the code of
+    k = 2j in its high nibble (two's complement) and that of k = 2j + 1 in its low nibble
+    (offset binary).  The scales follow the payload, then wcorr = -128 * even-k code sums."""
     packed = inp.random_packed(inp.generator(n + k), n, k)
     mf = pack.pack_mfma_weight(packed, k)
     assert tuple(mf.shape) == (n, k // 8 + pack.MFMA_MARKER_WORDS)
@@ -100,18 +102,58 @@ def test_mfma_layout_definition(pack, n, k):
             seen = np.zeros((16, 128), np.int32)
             for lane in range(64):
                 w = (nb * kb + t) * 256 + 4 * lane
-                got = orc.unpack_nibbles(flat[w : w + 4][None, :], 32)[0]
+                byts = flat[w : w + 4].astype(np.uint32).view(np.uint8).astype(np.int32)
+                hi = byts >> 4
+                got = np.empty(32, np.int32)
+                got[0::2] = np.where(hi >= 8, hi - 16, hi)  # k even: two's complement
+                got[1::2] = (byts & 15) - 8                 # k odd: offset binary
                 k0 = 128 * t + 32 * (lane // 16)
-                want = np.zeros(32, np.int32)
                 seg = codes[16 * nb + lane % 16, k0 : k0 + 32]
-                want[: seg.size] = seg
-                assert np.array_equal(got, want), (nb, t, lane)
+                assert np.array_equal(got[: seg.size], seg), (nb, t, lane)
+                # pad words past K are all-zero bits (not encoded zero codes)
+                assert np.all(flat[w + seg.size // 8 : w + 4] == 0), (nb, t, lane)
                 seen[lane % 16, 32 * (lane // 16) : 32 * (lane // 16) + 32] += 1
             assert np.all(seen == 1)
     pw = n * kb * 16
     assert np.array_equal(flat[pw : pw + n], packed.numpy()[:, k // 8])
-    assert np.all(flat[pw + n :] == 0)
+    assert np.array_equal(flat[pw + n : pw + 2 * n], -128 * codes[:, 0::2].sum(axis=1))
+    assert np.all(flat[pw + 2 * n :] == 0)
     assert torch.equal(pack.unpack_mfma_weight(mf, k), packed)
+
+
+def _unpack_bytes(words: np.ndarray, mask: int) -> np.ndarray:
+    """int8 bytes of (word & mask) for every word: the GPU's one-AND unpack."""
+    return (words.astype(np.uint32) & np.uint32(mask)).view(np.uint8).view(np.int8).astype(np.int64)
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 5, 64), (16, 16, 2048), (7, 9, 16384)])
+def test_nibble_encoding_identity(pack, m, n, k):
+    """The MFMA-side algebra: unpacking encoded activation and weight words with one AND
+    each (activation: & 0x0F0F0F0F paired with the weight's & 0xF0F0F0F0, and vice versa)
+    and summing the int8 byte products gives S = 16 * acc + 128 * (odd-k activation code
+    sum) + 128 * (even-k weight code sum), so S + qcorr + wcorr = 16 * acc.  Checked with
+    extreme codes too (-8/7 weights, +-7 activations)."""
+    gen = np.random.default_rng(m * n + k)
+    a = gen.integers(-7, 8, (m, k)).astype(np.int64)
+    b = gen.integers(-8, 8, (n, k)).astype(np.int64)
+    a[0, :] = 7 if m > 1 else a[0, :]
+    b[0, :] = -8
+    if n > 1:
+        b[1, :] = 7
+    wa = pack.flip_activation_words(torch.from_numpy(orc.pack_nibbles(a.astype(np.int32)))).numpy()
+    wb = pack.encode_weight_words(torch.from_numpy(orc.pack_nibbles(b.astype(np.int32)))).numpy()
+    a_lo, a_hi = _unpack_bytes(wa, 0x0F0F0F0F), _unpack_bytes(wa, 0xF0F0F0F0)
+    b_lo, b_hi = _unpack_bytes(wb, 0x0F0F0F0F), _unpack_bytes(wb, 0xF0F0F0F0)
+    s = a_lo.reshape(m, -1) @ b_hi.reshape(n, -1).T + a_hi.reshape(m, -1) @ b_lo.reshape(n, -1).T
+    acc = a @ b.T
+    qcorr = -128 * a[:, 1::2].sum(axis=1)
+    wcorr = -128 * b[:, 0::2].sum(axis=1)
+    assert np.array_equal(s + qcorr[:, None] + wcorr[None, :], 16 * acc)
+    assert np.abs(s).max() <= 2048 * k
+    mf = pack.pack_mfma_weight(torch.from_numpy(np.concatenate(
+        [orc.pack_nibbles(b.astype(np.int32)), np.ones((n, 1), np.int32)], axis=1)), k) if n % 16 == 0 else None
+    if mf is not None:
+        assert np.array_equal(pack.mfma_weight_corrections(mf, k).numpy(), wcorr)
 
 
 @pytest.mark.parametrize("m,k", [(1, 64), (17, 128), (40, 2048)])
@@ -130,9 +172,16 @@ def test_activation_fragment_layout(pack, m, k):
         slot = row % 16 + 16 * ((kw % 16) // 4)
         assert idx[row, kw] == ((row // 16) * kb + kw // 16) * 256 + 4 * slot + kw % 4
     words = torch.randint(-(2**31), 2**31 - 1, (m, k // 8), dtype=torch.int32)
-    buf = torch.zeros(total, dtype=torch.int32)
-    buf[torch.from_numpy(idx.reshape(-1))] = words.reshape(-1)
+    buf = torch.zeros(total + m16, dtype=torch.int32)
+    buf[torch.from_numpy(idx.reshape(-1))] = pack.flip_activation_words(words).reshape(-1)
+    buf[total : total + m] = torch.arange(m, dtype=torch.int32)
     assert torch.equal(pack.codes_from_fragment_major(buf, m, k), words)
+    assert torch.equal(pack.qcorr_from_fragment_major(buf, m, k), torch.arange(m, dtype=torch.int32))
+    # activation encoding: low nibble of each byte offset binary, high nibble two's complement
+    w0 = int(orc.pack_nibbles(np.array([[-8, -1, 0, 7, 3, -3, 1, -7]], np.int32))[0, 0]) & 0xFFFFFFFF
+    e0 = int(pack.flip_activation_words(torch.tensor([w0 - (1 << 32) if w0 >= 1 << 31 else w0], dtype=torch.int32))[0]) & 0xFFFFFFFF
+    assert [(e0 >> (8 * j)) & 15 for j in range(4)] == [-8 + 8, 0 + 8, 3 + 8, 1 + 8]
+    assert [(e0 >> (8 * j + 4)) & 15 for j in range(4)] == [15, 7, 13, 9]
 
 
 def test_mfma_layout_rejects_bad_shapes(pack):
@@ -171,11 +220,11 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_library_version_and_sizes(lib):
     assert lib.pi05w4a4_version() >= 100
-    assert lib.pi05w4a4_q_words(776, 2048) == 784 * 256
-    assert lib.pi05w4a4_q_words(16, 64) == 16 * 16  # K padded to 128
+    assert lib.pi05w4a4_q_words(776, 2048) == 784 * 256 + 784  # codes, then qcorr per row
+    assert lib.pi05w4a4_q_words(16, 64) == 16 * 16 + 16  # K padded to 128
     assert lib.pi05w4a4_q_words(0, 64) == 0
-    assert lib.pi05w4a4_mfma_words(2048, 2048) == 2048 * (2048 // 8 + 1)
-    assert lib.pi05w4a4_mfma_words(32, 192) == 32 * (256 // 8 + 1)
+    assert lib.pi05w4a4_mfma_words(2048, 2048) == 2048 * (2048 // 8 + 2)  # + scale, wcorr
+    assert lib.pi05w4a4_mfma_words(32, 192) == 32 * (256 // 8 + 2)
     assert lib.pi05w4a4_mfma_words(0, 64) == 0
 
 
@@ -217,8 +266,10 @@ def test_abi_validation_without_gpu(lib):
     assert lib.pi05w4a4_gemm_multi(vp(20), vp(16), 4, 64, 1, w1, n1, y1, vp(0), 0, vp(0)) == 1
     assert lib.pi05w4a4_gemm(vp(16), vp(16), 4, 64, vp(16), 24, vp(16), vp(0), 0, vp(0)) == 1
     assert "multiple of 16" in _err(lib)
-    # accumulator readout limited to K <= 65536
-    assert lib.pi05w4a4_gemm_acc(vp(16), 4, 131072, vp(16), 16, vp(16), vp(0)) == 1
+    # K is bounded so that the int32 MFMA sum (at most 2048 K in magnitude) cannot overflow
+    assert lib.pi05w4a4_gemm_acc(vp(16), 4, 1 << 20, vp(16), 16, vp(16), vp(0)) == 1
+    assert "at most 524288" in _err(lib)
+    assert lib.pi05w4a4_gemm(vp(16), vp(16), 4, 1 << 20, vp(16), 16, vp(16), vp(0), 0, vp(0)) == 1
     # M == 0 GEMM is a no-op success
     assert lib.pi05w4a4_gemm(vp(16), vp(16), 0, 64, vp(16), 16, vp(0), vp(0), 0, vp(0)) == 0
 
