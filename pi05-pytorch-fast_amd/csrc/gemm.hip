@@ -217,8 +217,41 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
       }
     }
   };
+  // The first ring load is unconditional: with nkb == 0 it reads the clamped block
+  // kb_end - 1 >= 0 and is never used.
+  load(kb_begin, ra[0], rb[0]);
+
+  // Epilogue operands of the whole workgroup tile, fetched now so that their latency hides
+  // under the main loop: thread t holds the row scale (pre-divided by 16) and qcorr of
+  // tile row t % (16*MI), and the column scale and wcorr of tile column t % NCOL.  All
+  // indices are clamped, so every thread loads unconditionally; columns past N get zeros
+  // when staged to LDS after the loop.
+  constexpr int TROWS = 16 * MI;
+  constexpr int NCOL = 16 * NI * NW;  // GELU: the gate and the up columns of the tile
+  float e_sa;
+  int32_t e_qc;
+  float e_sw;
+  int32_t e_wc;
+  bool e_colvalid;
+  {
+    const int r = tid % TROWS;
+    // The accumulator readout (kEpiAcc) has no row scales (p.sa may be null): it reads
+    // the first M words of q instead, which always exist, and never uses the values.
+    const float* sa_src = (p.sa != nullptr) ? p.sa : reinterpret_cast<const float*>(p.q);
+    e_sa = sa_src[min(m0 + r, M - 1)];
+    e_qc = p.q[q_payload_words(p.mblocks, KB128) + min(mt * TROWS + r, p.mblocks * 16 - 1)];
+    const int f = (tid / 16) % (NI * NW);  // fragment of the tile: wave f / NI, ni = f % NI
+    const int fn = f % NI, fw = f / NI;
+    const int fcol0 = GELU ? (nt * (8 * NI * NW) + fw * (8 * NI) + (fn % (NI / 2)) * 16)
+                           : ((nt - tile_begin) * (16 * NI * NW) + fw * (16 * NI) + fn * 16);
+    const int col = fcol0 + (tid & 15);
+    e_colvalid = col < N;
+    const int32_t* cbase = ((GELU && fn >= NI / 2) ? W2 : W) + N * scale_off + min(col, N - 1);
+    e_sw = __int_as_float(cbase[0]);
+    e_wc = cbase[N];
+  }
+
   if (nkb > 0) {
-    load(kb_begin, ra[0], rb[0]);
     int i = 0;
     for (; i + 2 <= nkb; i += 2) {
       load(kb_begin + i + 1, ra[1], rb[1]);
@@ -232,6 +265,16 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
     }
     if (i < nkb) compute(ra[0], rb[0]);  // odd count: the last block is in slot 0
   }
+
+  __shared__ __align__(16) float2 epi_row[TROWS];    // (sa / 16, qcorr bits) per tile row
+  __shared__ __align__(16) float epi_sw[NCOL];       // column scales of the tile
+  __shared__ __align__(16) int32_t epi_wc[NCOL];     // column corrections of the tile
+  if (tid < TROWS) epi_row[tid] = make_float2(e_sa * 0.0625f, __int_as_float(e_qc));
+  if (tid < NCOL) {
+    epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
+    epi_wc[tid] = e_colvalid ? e_wc : 0;
+  }
+  if constexpr (KW == 1) __syncthreads();  // KW > 1: the fold below synchronises
 
   // ---- k-part reduction through LDS (KW > 1): pairs of k parts are folded until part 0
   // of every column block holds the full sum; the other waves are done after that.
@@ -267,38 +310,40 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
   auto out_col = [&](int ni) {  // first of the lane's four columns of fragment ni
     return GELU ? (wcol + (ni % (NI / 2)) * 16 + lcol) : (wcol + ni * 16 + lcol);
   };
-  // Row and column corrections (16 * acc = S + qcorr + wcorr).
-  const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
+  // Row and column operands from LDS.  16 * acc = S + qcorr + wcorr; row scales are
+  // pre-divided by 16, which folds that factor into the scale: float(16 t) * (sa / 16)
+  // rounds exactly like float(t) * sa (both rescalings are exact powers of two).
+  float sv[MI];
   int32_t qc[MI];
 #pragma unroll
-  for (int mi = 0; mi < MI; ++mi) qc[mi] = qcorr[min(mt * MI + mi, p.mblocks - 1) * 16 + lrow];
+  for (int mi = 0; mi < MI; ++mi) {
+    const float2 e = epi_row[mi * 16 + lrow];
+    sv[mi] = e.x;
+    qc[mi] = __float_as_int(e.y);
+  }
   v4i wc[NI];
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int32_t* wcorr = ((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off + N;
-    wc[ni] = bvalid[ni] ? *reinterpret_cast<const v4i*>(wcorr + out_col(ni)) : v4i{0, 0, 0, 0};
-  }
+  for (int ni = 0; ni < NI; ++ni) wc[ni] = *reinterpret_cast<const v4i*>(&epi_wc[(wn * NI + ni) * 16 + lcol]);
   if (p.mode == kEpiFp16 || p.mode == kEpiGeluUp) {
-    // Row scales are pre-multiplied by 1/16, which folds the 16 of the corrected sum into
-    // the scale: float(16 t) * (sa / 16) rounds exactly like float(t) * sa (both
-    // rescalings are exact powers of two and 16 t is at most 2^24 in magnitude).
-    float sv[MI];
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi) sv[mi] = p.sa[min(m0 + mi * 16 + lrow, M - 1)] * 0.0625f;
     float4 sw[NI];
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) {
-      const float* scales = reinterpret_cast<const float*>(((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off);
-      sw[ni] = bvalid[ni] ? *reinterpret_cast<const float4*>(scales + out_col(ni)) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    for (int ni = 0; ni < NI; ++ni) sw[ni] = *reinterpret_cast<const float4*>(&epi_sw[(wn * NI + ni) * 16 + lcol]);
+    // Each 16-row block of the wave's output is staged in LDS (8-byte writes of a lane's
+    // four columns) and written back as whole rows with 16-byte stores: a wave row of
+    // 64 (GELU: 32) fp16 columns is 128 (64) contiguous bytes.  The staging area is
+    // private to the wave.
+    constexpr int OCW = GELU ? 8 * NI : 16 * NI;  // output columns of the wave
+    constexpr int LSR = OCW + 8;                  // staged row stride in halves (pad)
+    constexpr int LPR = OCW / 8;                  // lanes per row, 16 bytes each
+    constexpr int RPI = 64 / LPR;                 // rows per store instruction
+    static_assert(16 % RPI == 0 || RPI % 16 == 0, "store rows must tile the 16-row block");
+    __shared__ __align__(16) _Float16 stage_all[NW * 16 * LSR];
+    _Float16* stage = stage_all + wn * (16 * LSR);
     _Float16* y = static_cast<_Float16*>(Y);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      const int64_t row = m0 + mi * 16 + lrow;
-      if (row >= M) continue;  // only the last row tile has such lanes
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
-        if (!bvalid[ni]) continue;
         const v4i s = acc[mi][ni] + qc[mi] + wc[ni];
         const float swv[4] = {sw[ni].x, sw[ni].y, sw[ni].z, sw[ni].w};
         half4 o;
@@ -315,8 +360,18 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = dequant(s[r], sv[mi], swv[r]);
         }
-        *reinterpret_cast<half4*>(y + row * N + out_col(ni)) = o;
+        *reinterpret_cast<half4*>(stage + lrow * LSR + ni * 16 + lcol) = o;
       }
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int j = 0; j < (16 + RPI - 1) / RPI; ++j) {
+        const int rr = j * RPI + lane / LPR;
+        const int64_t grow = m0 + mi * 16 + rr;
+        const int gcol = wcol + (lane % LPR) * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + min(rr, 15) * LSR + (lane % LPR) * 8);
+        if (rr < 16 && grow < M && gcol < N) *reinterpret_cast<uint4*>(y + grow * N + gcol) = v;
+      }
+      __builtin_amdgcn_wave_barrier();
     }
   } else {
     // kEpiPartial: raw sums S, int32 [ksplit, M, n_total] at column col_off + col (the
