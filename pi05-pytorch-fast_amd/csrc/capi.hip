@@ -127,10 +127,14 @@ int validate_gemm_common(const int32_t* q, const float* sa, int64_t m, int32_t k
   return PI05W4A4_OK;
 }
 
+// Output offsets inside one 112-row tile are 32-bit: N is bounded well below 2^31 / 224.
+constexpr int32_t kMaxN = 1 << 20;
+
 int validate_weight(const int32_t* w, int32_t n, const char* name) {
   if (w == nullptr) return fail(PI05W4A4_EINVAL, "%s is null", name);
   if (n <= 0 || n % 16 != 0)
     return fail(PI05W4A4_EINVAL, "%s: N must be a positive multiple of 16, got %d", name, n);
+  if (n > kMaxN) return fail(PI05W4A4_EINVAL, "%s: N must be at most %d, got %d", name, kMaxN, n);
   if (!aligned(w, 16)) return fail(PI05W4A4_EINVAL, "%s must be 16-byte aligned", name);
   return PI05W4A4_OK;
 }

@@ -12,8 +12,8 @@
 // the same k, so its int32 sum is
 //   S = 16 * acc + 128 * sum_{k odd} a + 128 * sum_{k even} b.
 // The row and column terms are precomputed (qcorr after the activation codes, wcorr after
-// the weight scales) and the epilogue forms 16 * acc = S + qcorr[m] + wcorr[n] exactly;
-// |S| <= 2048 K < 2^31 for any K the host accepts.  This costs 2 ALU ops per packed word
+// the weight scales) and the accumulators start at qcorr[m] + wcorr[n], so they end at
+// 16 * acc exactly; |S| <= 2048 K < 2^31 for any K the host accepts.  This costs 2 ALU ops per packed word
 // instead of the 3 of a shift-and-mask unpack, which matters: the unpack is the largest
 // non-MFMA cost of the loop.
 //
@@ -25,15 +25,17 @@
 // Both operands live in HBM in the same MFMA-fragment-major layout (frag_word_index: one
 // 1 KB fragment per 16 rows/columns x 128 k; lane L loads slot L = 32 codes of row/
 // column L%16, the operands of the block's two MFMAs), so every operand fetch is one
-// fully coalesced 16-byte-per-lane load straight into registers.  (The vector memory pipeline issues about one wave-wide load
-// per ~20 clocks per CU whatever its width, so 16-byte loads double the operand bandwidth
-// of 8-byte ones.)  The K loop walks 128-deep k blocks through a 2-deep register ring:
-// the loads of block kb + 1 are issued before block kb is multiplied.  There is no LDS
+// fully coalesced 16-byte-per-lane load straight into registers.  (The vector memory
+// pipeline issues about one wave-wide load per ~20 clocks per CU whatever its width, so
+// 16-byte loads double the operand bandwidth of 8-byte ones.)  The K loop walks 128-deep
+// k blocks through a RING-deep register ring (2 at two waves per SIMD): the loads of
+// block kb + RING - 1 are issued before block kb is multiplied.  There is no LDS
 // traffic and no barrier in the loop: the waves of a workgroup share their A fragments
 // through the L1/L2 caches only.  (Measured alternatives that lost: A staged through a
 // double-buffered LDS tile, whose per-stage barrier stalls the MFMA pipe more than the
-// shared loads save; and L2 warm-up touches of the weights a few blocks ahead, whose
-// extra load instructions cost more than the misses they avoid.)
+// shared loads save; L2 warm-up touches of the weights a few blocks ahead, whose extra
+// load instructions cost more than the misses they avoid; and deeper rings at one wave
+// per SIMD, which lose the second wave's latency hiding.)
 // Every global load in the loop is unconditional (out-of-range rows, columns and k
 // blocks are clamped to valid addresses and their results are discarded), so the
 // compiler's vmcnt bookkeeping stays exact and the prefetches overlap the MFMAs.
@@ -45,9 +47,11 @@
 // side on one XCD and read those weights from its L2.
 //
 // Epilogue.  The weights are MFMA operand A, so each lane ends with four consecutive
-// output columns of one row and writes them as one 8-byte store (16 rows x 32 bytes per
-// store instruction), with no staging.  Modes: fp16 with scales, int32 split-K partials,
-// int32 accumulators, and paired gate/up tiles finished as fp16(gelu_tanh(gate) * up).
+// output columns of one row.  The tile's row and column scales were fetched under the
+// main loop and staged in LDS; each 16-row block of a wave's fp16 output is staged in LDS
+// (one 8-byte write per lane and fragment) and written back as whole rows with 16-byte
+// non-temporal stores.  Modes: fp16 with scales, int32 split-K partials, int32
+// accumulators, and paired gate/up tiles finished as fp16(gelu_tanh(gate) * up).
 
 #include "w4a4_internal.h"
 
@@ -85,8 +89,8 @@ __device__ __forceinline__ _Float16 dequant(int32_t acc, float sa, float sw) {
   return static_cast<_Float16>(y);
 }
 
-template <int MI, int NI, int NWAVES, int KW, bool GELU>
-__global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))) void gemm_w4a4_kernel(const GemmParams p) {
+template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE>
+__global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
@@ -180,16 +184,12 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
   const int nkb = kb_end - kb_begin;
 
   v4i acc[MI][NI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = v4i{0, 0, 0, 0};
 
   // ---- main loop: A and B straight from global memory into a 2-deep register ring.
   // Each load is a scalar fragment base plus one shared unsigned 32-bit lane offset
   // (global_load_dwordx4 with an SGPR base): no per-load address arithmetic.
-  uint4 ra[2][MI];
-  uint4 rb[2][NI];
+  uint4 ra[RING][MI];
+  uint4 rb[RING][NI];
   auto load = [&](int kb, uint4 (&a)[MI], uint4 (&b)[NI]) {
     const uint32_t off = static_cast<uint32_t>(min(kb, kb_end - 1)) * 1024u + static_cast<uint32_t>(lane) * 16u;
 #pragma unroll
@@ -221,17 +221,38 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
   // kb_end - 1 >= 0 and is never used.
   load(kb_begin, ra[0], rb[0]);
 
-  // Epilogue operands of the whole workgroup tile, fetched now so that their latency hides
-  // under the main loop: thread t holds the row scale (pre-divided by 16) and qcorr of
-  // tile row t % (16*MI), and the column scale and wcorr of tile column t % NCOL.  All
-  // indices are clamped, so every thread loads unconditionally; columns past N get zeros
-  // when staged to LDS after the loop.
+  // Accumulators start at the correction terms, qcorr[row] + wcorr[col], so that they end
+  // at 16 * acc exactly (S + qcorr + wcorr).  Only the first k part of the first K slice
+  // carries them: the other parts' sums are added to it.  Lane L owns rows 16*mi + L%16
+  // and columns 16*ni + 4*(L/16) + 0..3 of its wave tile (see the epilogue).  Rows and
+  // columns past the matrix read clamped, in-bounds words and are never stored.
+  {
+    const bool first_part = (ks == 0) && (wk == 0);
+    const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
+    int32_t qc[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) qc[mi] = qcorr[min(mt * MI + mi, p.mblocks - 1) * 16 + (lane & 15)];
+    v4i wc[NI];
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const int col = GELU ? (wcol + (ni % (NI / 2)) * 16) : (wcol + ni * 16);
+      const int32_t* wcorr = ((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off + N;
+      wc[ni] = *reinterpret_cast<const v4i*>(wcorr + min(col, N - 16) + (lane >> 4) * 4);
+    }
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = first_part ? (wc[ni] + qc[mi]) : v4i{0, 0, 0, 0};
+  }
+
+  // Epilogue scales of the whole workgroup tile, fetched now so that their latency hides
+  // under the main loop: thread t holds the row scale of tile row t % (16*MI) and the
+  // column scale of tile column t % NCOL.  All indices are clamped, so every thread loads
+  // unconditionally; columns past N get zero scales when staged to LDS after the loop.
   constexpr int TROWS = 16 * MI;
   constexpr int NCOL = 16 * NI * NW;  // GELU: the gate and the up columns of the tile
   float e_sa;
-  int32_t e_qc;
   float e_sw;
-  int32_t e_wc;
   bool e_colvalid;
   {
     const int r = tid % TROWS;
@@ -239,41 +260,37 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
     // the first M words of q instead, which always exist, and never uses the values.
     const float* sa_src = (p.sa != nullptr) ? p.sa : reinterpret_cast<const float*>(p.q);
     e_sa = sa_src[min(m0 + r, M - 1)];
-    e_qc = p.q[q_payload_words(p.mblocks, KB128) + min(mt * TROWS + r, p.mblocks * 16 - 1)];
     const int f = (tid / 16) % (NI * NW);  // fragment of the tile: wave f / NI, ni = f % NI
     const int fn = f % NI, fw = f / NI;
     const int fcol0 = GELU ? (nt * (8 * NI * NW) + fw * (8 * NI) + (fn % (NI / 2)) * 16)
                            : ((nt - tile_begin) * (16 * NI * NW) + fw * (16 * NI) + fn * 16);
     const int col = fcol0 + (tid & 15);
     e_colvalid = col < N;
-    const int32_t* cbase = ((GELU && fn >= NI / 2) ? W2 : W) + N * scale_off + min(col, N - 1);
-    e_sw = __int_as_float(cbase[0]);
-    e_wc = cbase[N];
+    e_sw = __int_as_float((((GELU && fn >= NI / 2) ? W2 : W) + N * scale_off)[min(col, N - 1)]);
   }
 
-  if (nkb > 0) {
-    int i = 0;
-    for (; i + 2 <= nkb; i += 2) {
-      load(kb_begin + i + 1, ra[1], rb[1]);
+  // Step s multiplies block kb_begin + s from ring slot s % RING and first prefetches
+  // block s + RING - 1 into the slot freed by step s - 1.  The loop runs whole
+  // iterations of RING steps; steps past nkb only load (clamped, in bounds) and skip
+  // their multiply, so no memory instruction is conditional and the compiler's vmcnt
+  // bookkeeping stays exact.
+#pragma unroll
+  for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
+  for (int i = 0; i < nkb; i += RING) {
+#pragma unroll
+    for (int j = 0; j < RING; ++j) {
+      load(kb_begin + i + j + RING - 1, ra[(j + RING - 1) % RING], rb[(j + RING - 1) % RING]);
       // Keep each prefetch at the top of its step: under register pressure the
       // scheduler would otherwise sink the loads next to their use.
       __builtin_amdgcn_sched_barrier(0);
-      compute(ra[0], rb[0]);
-      load(kb_begin + i + 2, ra[0], rb[0]);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(ra[1], rb[1]);
+      if (j == 0 || i + j < nkb) compute(ra[j], rb[j]);
     }
-    if (i < nkb) compute(ra[0], rb[0]);  // odd count: the last block is in slot 0
   }
 
-  __shared__ __align__(16) float2 epi_row[TROWS];    // (sa / 16, qcorr bits) per tile row
-  __shared__ __align__(16) float epi_sw[NCOL];       // column scales of the tile
-  __shared__ __align__(16) int32_t epi_wc[NCOL];     // column corrections of the tile
-  if (tid < TROWS) epi_row[tid] = make_float2(e_sa * 0.0625f, __int_as_float(e_qc));
-  if (tid < NCOL) {
-    epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
-    epi_wc[tid] = e_colvalid ? e_wc : 0;
-  }
+  __shared__ __align__(16) float epi_sa[TROWS];  // row scales / 16 of the tile
+  __shared__ __align__(16) float epi_sw[NCOL];   // column scales of the tile
+  if (tid < TROWS) epi_sa[tid] = e_sa * 0.0625f;
+  if (tid < NCOL) epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
   if constexpr (KW == 1) __syncthreads();  // KW > 1: the fold below synchronises
 
   // ---- k-part reduction through LDS (KW > 1): pairs of k parts are folded until part 0
@@ -310,21 +327,13 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
   auto out_col = [&](int ni) {  // first of the lane's four columns of fragment ni
     return GELU ? (wcol + (ni % (NI / 2)) * 16 + lcol) : (wcol + ni * 16 + lcol);
   };
-  // Row and column operands from LDS.  16 * acc = S + qcorr + wcorr; row scales are
-  // pre-divided by 16, which folds that factor into the scale: float(16 t) * (sa / 16)
-  // rounds exactly like float(t) * sa (both rescalings are exact powers of two).
-  float sv[MI];
-  int32_t qc[MI];
-#pragma unroll
-  for (int mi = 0; mi < MI; ++mi) {
-    const float2 e = epi_row[mi * 16 + lrow];
-    sv[mi] = e.x;
-    qc[mi] = __float_as_int(e.y);
-  }
-  v4i wc[NI];
-#pragma unroll
-  for (int ni = 0; ni < NI; ++ni) wc[ni] = *reinterpret_cast<const v4i*>(&epi_wc[(wn * NI + ni) * 16 + lcol]);
+  // The accumulators hold 16 * acc.  Row scales come from LDS pre-divided by 16, which
+  // folds that factor into the scale: float(16 t) * (sa / 16) rounds exactly like
+  // float(t) * sa (both rescalings are exact powers of two).
   if (p.mode == kEpiFp16 || p.mode == kEpiGeluUp) {
+    float sv[MI];
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) sv[mi] = epi_sa[mi * 16 + lrow];
     float4 sw[NI];
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) sw[ni] = *reinterpret_cast<const float4*>(&epi_sw[(wn * NI + ni) * 16 + lcol]);
@@ -339,16 +348,18 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
     static_assert(16 % RPI == 0 || RPI % 16 == 0, "store rows must tile the 16-row block");
     __shared__ __align__(16) _Float16 stage_all[NW * 16 * LSR];
     _Float16* stage = stage_all + wn * (16 * LSR);
-    _Float16* y = static_cast<_Float16*>(Y);
+    // Stores address the wave's output block through a scalar base and a 32-bit lane
+    // offset (the block spans at most 16*MI rows of N columns).
+    char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
-        const v4i s = acc[mi][ni] + qc[mi] + wc[ni];
+        const v4i s = acc[mi][ni];
         const float swv[4] = {sw[ni].x, sw[ni].y, sw[ni].z, sw[ni].w};
         half4 o;
         if (GELU) {
-          const v4i su = acc[mi][ni + NI / 2] + qc[mi] + wc[ni + NI / 2];
+          const v4i su = acc[mi][ni + NI / 2];
           const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
@@ -366,17 +377,21 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
 #pragma unroll
       for (int j = 0; j < (16 + RPI - 1) / RPI; ++j) {
         const int rr = j * RPI + lane / LPR;
-        const int64_t grow = m0 + mi * 16 + rr;
-        const int gcol = wcol + (lane % LPR) * 8;
-        const uint4 v = *reinterpret_cast<const uint4*>(stage + min(rr, 15) * LSR + (lane % LPR) * 8);
-        if (rr < 16 && grow < M && gcol < N) *reinterpret_cast<uint4*>(y + grow * N + gcol) = v;
+        const int trow = mi * 16 + rr;  // row within the tile
+        const int tcol = (lane % LPR) * 8;
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + min(rr, 15) * LSR + tcol);
+        // Non-temporal: the outputs are not re-read by this kernel, so they should not
+        // displace the weights streaming through L2 (measured 1-3% faster).
+        if (rr < 16 && m0 + trow < M && wcol + tcol < N)
+          __builtin_nontemporal_store(v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)},
+                                      reinterpret_cast<v4i*>(yw + static_cast<uint32_t>(trow * N + tcol) * 2u));
       }
       __builtin_amdgcn_wave_barrier();
     }
   } else {
-    // kEpiPartial: raw sums S, int32 [ksplit, M, n_total] at column col_off + col (the
-    // corrections are added once after the K slices are summed);
-    // kEpiAcc:     int32 [M, N] accumulators of the group, (S + qcorr + wcorr) / 16.
+    // kEpiPartial: partial sums of 16 * acc, int32 [ksplit, M, n_total] at column
+    // col_off + col (slice 0 carries the corrections);
+    // kEpiAcc:     int32 [M, N] accumulators of the group, (16 * acc) / 16.
     int32_t* out;
     int64_t ld;
     if (p.mode == kEpiPartial) {
@@ -396,7 +411,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(2))
         // partial columns in GELU mode: gate block [0, N), up block [N, 2N)
         const int col = out_col(ni) + ((GELU && ni >= NI / 2) ? N : 0);
         v4i v = acc[mi][ni];
-        if (p.mode == kEpiAcc) v = (v + qc[mi] + wc[ni]) >> 4;  // exact: a multiple of 16
+        if (p.mode == kEpiAcc) v = v >> 4;  // exact: a multiple of 16
         *reinterpret_cast<v4i*>(out + row * ld + col) = v;
       }
     }
@@ -417,7 +432,6 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   const int64_t scale_off = static_cast<int64_t>(kblocks128(p.k)) * 16;
   const int64_t plane = M * p.n_total;
   const float sav = p.sa[row] * 0.0625f;  // the sums below are 16 * acc
-  const int32_t qc = p.q[q_payload_words(p.mblocks, kblocks128(p.k)) + row];
   if (GELU) {
     const int N = p.gelu_pair_n;
     int4 g = make_int4(0, 0, 0, 0), u = make_int4(0, 0, 0, 0);
@@ -430,10 +444,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
     }
     const float* swg = reinterpret_cast<const float*>(p.g[0].w + N * scale_off);
     const float* swu = reinterpret_cast<const float*>(p.g[1].w + N * scale_off);
-    const int32_t* wcg = p.g[0].w + N * scale_off + N;
-    const int32_t* wcu = p.g[1].w + N * scale_off + N;
-    const int gv[4] = {g.x + qc + wcg[c], g.y + qc + wcg[c + 1], g.z + qc + wcg[c + 2], g.w + qc + wcg[c + 3]};
-    const int uv[4] = {u.x + qc + wcu[c], u.y + qc + wcu[c + 1], u.z + qc + wcu[c + 2], u.w + qc + wcu[c + 3]};
+    const int gv[4] = {g.x, g.y, g.z, g.w};
+    const int uv[4] = {u.x, u.y, u.z, u.w};
     _Float16* y = static_cast<_Float16*>(p.g[0].y) + row * N + c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -466,21 +478,20 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   }
   const int col = c - off;
   const float* sw = reinterpret_cast<const float*>(W + N * scale_off);
-  const int32_t* wc = W + N * scale_off + N + col;
   _Float16* y = static_cast<_Float16*>(Y) + row * N + col;
-  const int sv[4] = {s.x + qc + wc[0], s.y + qc + wc[1], s.z + qc + wc[2], s.w + qc + wc[3]};
+  const int sv[4] = {s.x, s.y, s.z, s.w};
 #pragma unroll
   for (int e = 0; e < 4; ++e) y[e] = dequant(sv[e], sav, sw[col + e]);
 }
 
-template <int MI, int NI, int NWAVES, int KW>
+template <int MI, int NI, int NWAVES, int KW, int RING = 2, int WPE = 2>
 hipError_t launch_cfg(const GemmParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles),
                   static_cast<unsigned>(p.ksplit));
   if (p.mode == kEpiGeluUp || (p.mode == kEpiPartial && p.gelu_pair_n > 0))
-    gemm_w4a4_kernel<MI, NI, NWAVES, KW, true><<<grid, 64 * NWAVES, 0, stream>>>(p);
+    gemm_w4a4_kernel<MI, NI, NWAVES, KW, true, RING, WPE><<<grid, 64 * NWAVES, 0, stream>>>(p);
   else
-    gemm_w4a4_kernel<MI, NI, NWAVES, KW, false><<<grid, 64 * NWAVES, 0, stream>>>(p);
+    gemm_w4a4_kernel<MI, NI, NWAVES, KW, false, RING, WPE><<<grid, 64 * NWAVES, 0, stream>>>(p);
   return hipGetLastError();
 }
 
