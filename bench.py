@@ -12,10 +12,13 @@ embeddings, all resident in HBM.  Timed region: K replays of the whole forward c
 in one HIP graph, bracketed by device synchronisation; `value` = ms per forward.
 
 Per-kernel figures (`gemms`, `roofline`): each W4A4 kernel of the forward is launched
-back to back through the C ABI with preallocated buffers at the forward's shapes; HIP
-events recorded on the launching stream (torch's current stream, which the library
-uses) bracket the launches, giving the average kernel duration, int8 TOPS and the
-fraction of the MI355X dense int8 MFMA peak (GEMMs) or of HBM bandwidth (quantizers).
+through the C ABI with preallocated buffers at the forward's shapes.  After a warm-up of
+about 0.3 s of back-to-back launches (clocks settle), `--kernel-iters` launches are
+captured in one HIP graph; HIP events recorded on the launching stream (torch's current
+stream, which the library uses) bracket each of 5 replays, and the median per-launch
+time gives the kernel duration, int8 TOPS and the fraction of the MI355X dense int8 MFMA
+peak (GEMMs) or of HBM bandwidth (quantizers).  The graph removes host launch gaps
+between the back-to-back kernels.
 The dominant kernel of the forward (gate/up GEMM) is the `roofline` object; its `traffic`
 (HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed
 under profiles/ when present.
@@ -53,11 +56,12 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--tokens", type=int, default=776)
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--layers", type=int, default=18)
-    ap.add_argument("--kernel-iters", type=int, default=30, help="back-to-back launches per kernel")
+    ap.add_argument("--kernel-iters", type=int, default=100, help="launches per timed graph replay")
+    ap.add_argument("--kernel-warmup-s", type=float, default=0.3, help="eager warm-up per kernel (s)")
     ap.add_argument("--no-graph", action="store_true", help="time eager forwards instead of graph replays")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
@@ -72,26 +76,42 @@ class KernelBench:
     """Back-to-back launches of one W4A4 kernel through the C ABI, timed with HIP events
     recorded on the launching stream."""
 
-    def __init__(self, torch, ext, dev, iters):
+    def __init__(self, torch, ext, dev, iters, warm_s=0.3, reps=5):
         self.torch, self.ext, self.dev, self.iters = torch, ext, dev, iters
+        self.warm_s, self.reps = warm_s, reps
         self.lib = ext.load_int4_gemm()
 
     def _stream(self):
         return ctypes.c_void_p(self.torch.cuda.current_stream(self.dev).cuda_stream)
 
     def _time(self, fn) -> float:
+        """Median microseconds per launch of `fn` over `reps` replays of a graph holding
+        `iters` launches, after an eager warm-up of about `warm_s` seconds."""
         torch = self.torch
-        for _ in range(3):
-            fn()
+        fn()
         torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(self.iters):
-            fn()
-        e1.record()
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < self.warm_s:
+            for _ in range(20):
+                fn()
+            torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(self.iters):
+                fn()
+        graph.replay()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / self.iters
+        per_launch = []
+        for _ in range(self.reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            per_launch.append(e0.elapsed_time(e1) * 1e3 / self.iters)
+        del graph
+        return statistics.median(per_launch)
 
     def _check(self, rc):
         if rc != 0:
@@ -257,7 +277,7 @@ def main() -> int:
     torch.cuda.set_device(dev)
     ext.preload()
     m = args.tokens * args.batch
-    kb = KernelBench(torch, ext, dev, args.kernel_iters)
+    kb = KernelBench(torch, ext, dev, args.kernel_iters, args.kernel_warmup_s)
     if args.only_kernel:
         print(json.dumps(kernel_table(kb, m, args.only_kernel)), flush=True)
         return 0

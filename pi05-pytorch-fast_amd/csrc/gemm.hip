@@ -202,20 +202,32 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // element r of lane L is output row 16*mi + L%16, column 16*ni + 4*(L/16) + r: four
   // consecutive columns of one row per lane.  Pad codes of a K that is not a multiple
   // of 128 multiply zero weight words: no guard.
-  auto compute = [&](const uint4 (&a)[MI], const uint4 (&b)[NI]) {
+  // The operands of a block's first MFMAs (all weight fragments of half 0 and activation
+  // fragment 0) are unpacked at the end of the previous block, among its last MFMAs, so
+  // that a block starts multiplying at once (nb0 / na0 carry them across blocks).
+  v4i nb0[NI];
+  v4i na0;
+  auto unpack_first = [&](const uint4 (&a)[MI], const uint4 (&b)[NI]) {
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) nb0[ni] = unpack_w(b[ni].x, b[ni].y);
+    na0 = unpack_a(a[0].x, a[0].y);
+  };
+  auto compute = [&](const uint4 (&a)[MI], const uint4 (&b)[NI], const uint4 (&an)[MI],
+                     const uint4 (&bn)[NI]) {
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       v4i bop[NI];
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) bop[ni] = h ? unpack_w(b[ni].z, b[ni].w) : unpack_w(b[ni].x, b[ni].y);
+      for (int ni = 0; ni < NI; ++ni) bop[ni] = h ? unpack_w(b[ni].z, b[ni].w) : nb0[ni];
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi) {
-        const v4i aop = h ? unpack_a(a[mi].z, a[mi].w) : unpack_a(a[mi].x, a[mi].y);
+        const v4i aop = h ? unpack_a(a[mi].z, a[mi].w) : (mi == 0 ? na0 : unpack_a(a[mi].x, a[mi].y));
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni)
           acc[mi][ni] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bop[ni], aop, acc[mi][ni], 0, 0, 0);
       }
     }
+    unpack_first(an, bn);  // the next block (loaded one step ago)
   };
   // The first ring load is unconditional: with nkb == 0 it reads the clamped block
   // kb_end - 1 >= 0 and is never used.
@@ -276,6 +288,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // bookkeeping stays exact.
 #pragma unroll
   for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
+  unpack_first(ra[0], rb[0]);
   for (int i = 0; i < nkb; i += RING) {
 #pragma unroll
     for (int j = 0; j < RING; ++j) {
@@ -283,7 +296,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       // Keep each prefetch at the top of its step: under register pressure the
       // scheduler would otherwise sink the loads next to their use.
       __builtin_amdgcn_sched_barrier(0);
-      if (j == 0 || i + j < nkb) compute(ra[j], rb[j]);
+      if (j == 0 || i + j < nkb) compute(ra[j], rb[j], ra[(j + 1) % RING], rb[(j + 1) % RING]);
     }
   }
 
