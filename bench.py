@@ -65,7 +65,8 @@ def parse_args():
     ap.add_argument("--no-graph", action="store_true", help="time eager forwards instead of graph replays")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0, help="budget of the CPU baseline")
-    ap.add_argument("--fuse-gelu", action="store_true", help="gate/up with the fused GELU*up epilogue")
+    ap.add_argument("--unfused-gelu", action="store_true",
+                    help="gate/up as two fp16 outputs + eager gelu*up instead of the fused epilogue")
     ap.add_argument("--only-kernel", default="",
                     help="skip the forward; launch only this kernel class (for rocprofv3 --pmc runs)")
     return ap.parse_args()
@@ -284,8 +285,7 @@ def main() -> int:
 
     from pi05_fast.w4a4.prefix_lm import build_prefix_lm, prefix_inputs, prefix_ops
 
-    if args.fuse_gelu:
-        os.environ["PI05_W4A4_FUSE_GELU"] = "1"
+    os.environ["PI05_W4A4_FUSE_GELU"] = "0" if args.unfused_gelu else "1"
     model, _ = build_prefix_lm(dev, num_layers=args.layers)
     x = prefix_inputs(args.batch, args.tokens, dev)
     s = args.tokens
@@ -360,11 +360,11 @@ def main() -> int:
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
     calls = {"quant_k2048": 3, "quant_k16384": 1, "qkv": 1, "o": 1, "down": 1,
-             "gate_up": 0 if args.fuse_gelu else 1, "gate_up_gelu": 1 if args.fuse_gelu else 0}
+             "gate_up": 1 if args.unfused_gelu else 0, "gate_up_gelu": 0 if args.unfused_gelu else 1}
     for name, c in calls.items():
         kernels[name]["calls_per_layer"] = c
     w4a4_us_per_layer = sum(kernels[n]["avg_us"] * c for n, c in calls.items())
-    dk = kernels["gate_up_gelu" if args.fuse_gelu else "gate_up"]
+    dk = kernels["gate_up"]
     traffic, traffic_src = read_traffic()
     roofline = {
         "bound": "mfma",
@@ -401,7 +401,7 @@ def main() -> int:
             "batch": args.batch,
             "layers": args.layers,
             "timed": "hip-graph replay" if not args.no_graph else "eager",
-            "fused_gelu_up": bool(args.fuse_gelu),
+            "fused_gelu_up": not args.unfused_gelu,
             "graph_replay_bit_exact_vs_eager": graph_exact,
         },
         "eager_ms_per_forward": round(eager_ms, 3),

@@ -51,7 +51,8 @@
 // main loop and staged in LDS; each 16-row block of a wave's fp16 output is staged in LDS
 // (one 8-byte write per lane and fragment) and written back as whole rows with 16-byte
 // non-temporal stores.  Modes: fp16 with scales, int32 split-K partials, int32
-// accumulators, and paired gate/up tiles finished as fp16(gelu_tanh(gate) * up).
+// accumulators, and paired gate/up tiles finished exactly as the eager
+// `gelu(gate, approximate="tanh") * up` on the fp16 gate and up (apply.py:135-138).
 
 #include "w4a4_internal.h"
 
@@ -73,10 +74,28 @@ __device__ __forceinline__ v4i unpack_w(uint32_t x, uint32_t y) {
              static_cast<int>(y & kHiNib), static_cast<int>(y & kLoNib)};
 }
 
-__device__ __forceinline__ float gelu_tanh(float x) {
-  // 0.5 * x * (1 + tanh(sqrt(2/pi) * (x + 0.044715 * x^3)))
-  const float inner = 0.7978845608028654f * (x + 0.044715f * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
+// torch.nn.functional.gelu(x, approximate="tanh") of an fp16 value, evaluated the way
+// PyTorch's elementwise GELU is (fp32: x^3 = (x*x)*x, inner = kBeta * fma(kKappa, x^3, x),
+// (0.5*x) * (1 + tanhf(inner))) and rounded to fp16.  Contraction is off so that only the
+// one FMA is formed, and the empty asm keeps the fp32 result in a register: otherwise the
+// backend folds the last multiply and the fp16 conversion into one v_fma_mix, which rounds
+// once and differs from the fp32-then-fp16 rounding on about a fifth of all fp16 inputs.
+// Compared with torch's eager GELU on the same GPU for every finite fp16 input: identical.
+__device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh) {
+#pragma clang fp contract(off)
+  const float x = static_cast<float>(xh);
+  const float x3 = (x * x) * x;
+  const float inner = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
+  float y = (0.5f * x) * (1.0f + tanhf(inner));
+  asm volatile("" : "+v"(y));
+  return static_cast<_Float16>(y);
+}
+
+// fp16 * fp16 as torch's eager mul: one fp32 product rounded to fp16.
+__device__ __forceinline__ _Float16 mul_f16(_Float16 a, _Float16 b) {
+  float y = static_cast<float>(a) * static_cast<float>(b);
+  asm volatile("" : "+v"(y));
+  return static_cast<_Float16>(y);
 }
 
 // fp16((float(acc) * sa) * sw) with both products rounded to fp32 first.  The empty asm
@@ -376,9 +395,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
           const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float g = static_cast<float>(dequant(s[r], sv[mi], swv[r]));
-            const float u = static_cast<float>(dequant(su[r], sv[mi], swu[r]));
-            o[r] = static_cast<_Float16>(gelu_tanh(g) * u);
+            o[r] = mul_f16(gelu_tanh_f16(dequant(s[r], sv[mi], swv[r])), dequant(su[r], sv[mi], swu[r]));
           }
         } else {
 #pragma unroll
@@ -462,9 +479,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
     _Float16* y = static_cast<_Float16*>(p.g[0].y) + row * N + c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const float gf = static_cast<float>(dequant(gv[e], sav, swg[c + e]));
-      const float uf = static_cast<float>(dequant(uv[e], sav, swu[c + e]));
-      y[e] = static_cast<_Float16>(gelu_tanh(gf) * uf);
+      y[e] = mul_f16(gelu_tanh_f16(dequant(gv[e], sav, swg[c + e])), dequant(uv[e], sav, swu[c + e]));
     }
     return;
   }

@@ -7,13 +7,16 @@ not only gate/up -- runs the fast layout.  With ``PI05_W4A4_MFMA=0`` the referen
 load-time layouts are kept (row padding ``PI05_W4A4_ROW_PAD_WORDS``, WMMA preshuffle of
 gate/up ``PI05_W4A4_GATE_PRESHUFFLE``) and the ops convert them on every call.
 
-``PI05_W4A4_FUSE_GELU=1`` (default 0) routes gate/up through ``int4_gemm2_gelu``, which
-applies GELU-tanh(gate) * up in the GEMM epilogue (one fp16 rounding fewer than the
-reference's eager ``act_fn(gate) * up``).
+``PI05_W4A4_FUSE_GELU`` (default 1) routes gate/up through ``int4_gemm2_gelu`` when the
+MLP's activation is torch's GELU-tanh: the GEMM epilogue computes
+``gelu(gate, approximate="tanh") * up`` with the same fp16 roundings as the reference's
+eager ``act_fn(gate) * up`` (bit-identical outputs), without writing gate and up.
+``PI05_W4A4_FUSE_GELU=0`` keeps the eager form.
 """
 
 from __future__ import annotations
 
+import functools
 import json
 import os
 import types
@@ -227,11 +230,24 @@ def _fused_attn_forward(
     return attn_output, attn_weights
 
 
+def _is_torch_gelu_tanh(act) -> bool:
+    """True iff ``act`` evaluates ``torch.nn.functional.gelu(x, approximate="tanh")`` (the
+    default of transformers' GELUTanh, Gemma's ``gelu_pytorch_tanh``): the function whose
+    fp16 results the fused gate/up epilogue reproduces bit for bit."""
+    fn = getattr(act, "act", act)
+    return (
+        isinstance(fn, functools.partial)
+        and fn.func is torch.nn.functional.gelu
+        and not fn.args
+        and fn.keywords == {"approximate": "tanh"}
+    )
+
+
 def fuse_shared_activation_quant(model: nn.Module) -> int:
     """One activation quant for QKV and one for gate/up (apply.py:194-213)."""
     if os.environ.get("PI05_W4A4_FUSE_QUANT", "1") == "0":
         return 0
-    fuse_gelu = os.environ.get("PI05_W4A4_FUSE_GELU", "0") == "1"
+    fuse_gelu = os.environ.get("PI05_W4A4_FUSE_GELU", "1") == "1"
     n = 0
     for mod in model.modules():
         qkv = (getattr(mod, "q_proj", None), getattr(mod, "k_proj", None), getattr(mod, "v_proj", None))
@@ -245,7 +261,11 @@ def fuse_shared_activation_quant(model: nn.Module) -> int:
             getattr(mod, "down_proj", None),
         )
         if all(isinstance(p, W4A4Linear) for p in gate_up) and hasattr(mod, "act_fn"):
-            mod._w4a4_fuse_gelu = fuse_gelu and gate_up[0].packed.shape == gate_up[1].packed.shape
+            mod._w4a4_fuse_gelu = (
+                fuse_gelu
+                and gate_up[0].packed.shape == gate_up[1].packed.shape
+                and _is_torch_gelu_tanh(mod.act_fn)
+            )
             mod.forward = types.MethodType(_fused_mlp_forward, mod)
             n += 1
     return n

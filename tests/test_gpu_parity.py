@@ -238,9 +238,10 @@ def test_int4_gemm2_gelu_matches_unfused(ext, cuda, m):
     torch.cuda.synchronize()
     h64 = orc.gelu_tanh(inp.to_np(g).astype(np.float64)) * inp.to_np(u).astype(np.float64)
     err_fused = orc.rel_l2(inp.to_np(h), h64)
-    err_eager = orc.rel_l2(inp.to_np(h_eager), h64)
-    assert err_fused <= 1e-3, f"fused rel_l2 {err_fused:.3e} (eager {err_eager:.3e})"
-    assert orc.rel_l2(inp.to_np(h), inp.to_np(h_eager)) <= 1e-3
+    assert err_fused <= 1e-3, f"fused rel_l2 {err_fused:.3e} against the float64 closed form"
+    # The fused epilogue evaluates gelu and the product exactly as the eager ops do.
+    nbad = int((h.view(torch.int16) != h_eager.view(torch.int16)).sum())
+    assert nbad == 0, f"{nbad}/{h.numel()} fused outputs differ from eager gelu(gate) * up"
 
 
 # ----------------------------------------------------------------------------- reference tests
