@@ -163,6 +163,19 @@ int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* 
                        int32_t n, void* y_fp16, int32_t* qbuf, float* sabuf, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/*
+ * RMSNorm of fp16 rows, the input norm of every attention and MLP block ahead of the QKV
+ * and gate/up activation quant.  No counterpart in the reference's W4A4 code: it replaces
+ * transformers' GemmaRMSNorm module (modeling_gemma.py:64-78), which the reference runs
+ * eagerly between its W4A4 ops, with one kernel of the same fp32 operation order:
+ *   y = fp16((float(x) * rsqrt(mean(float(x)^2) + eps)) * (unit_offset + float(w))).
+ * x, y fp16 [M, K] (may alias), w fp16 [K]; K % 8 == 0, K <= 16384; 16-byte aligned.
+ * The sum of squares is reduced in another order than torch's, so a few outputs can
+ * differ from the eager module's by one fp16 ulp.
+ */
+int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                     int64_t m, int32_t k, void* y_fp16, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

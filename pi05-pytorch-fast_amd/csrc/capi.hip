@@ -315,6 +315,22 @@ int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_m
                   static_cast<hipStream_t>(stream));
 }
 
+int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                      int64_t m, int32_t k, void* y_fp16, void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k <= 0 || k % 8 != 0 || k > 16384)
+    return fail(PI05W4A4_EINVAL, "RMSNorm width must be a multiple of 8 up to 16384, got %d", k);
+  if (m == 0) return ok();
+  if (x_fp16 == nullptr || w_fp16 == nullptr || y_fp16 == nullptr)
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!aligned(x_fp16, 16) || !aligned(w_fp16, 16) || !aligned(y_fp16, 16))
+    return fail(PI05W4A4_EINVAL, "x, w and y must be 16-byte aligned");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  return hip_status(w4a4::launch_rmsnorm(x_fp16, w_fp16, eps, unit_offset != 0, m, k, y_fp16,
+                                         static_cast<hipStream_t>(stream)),
+                    "rmsnorm launch");
+}
+
 int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
                        int32_t n, void* y_fp16, int32_t* qbuf, float* sabuf, void* workspace,
                        size_t workspace_bytes, void* stream) {

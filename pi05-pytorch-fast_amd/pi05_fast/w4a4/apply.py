@@ -145,11 +145,14 @@ def apply_w4a4_from_dir(model: nn.Module, pack_dir: str | Path) -> int:
     preload()
     n = replace_linears_from_packed(model, packed, meta["layers"], device=device)
     n_fuse = fuse_shared_activation_quant(model)
+    from pi05_fast.w4a4.norm import fuse_rmsnorm
+
+    n_norm = fuse_rmsnorm(model)
     n_mfma = sum(isinstance(m, W4A4Linear) and m.mfma for m in model.modules())
     n_pre = sum(isinstance(m, W4A4Linear) and m.preshuffled for m in model.modules())
     print(
         f"w4a4: replaced {n} Linear modules from {pack_dir}; "
-        f"shared-quant fused {n_fuse} QKV/MLP groups; "
+        f"shared-quant fused {n_fuse} QKV/MLP groups; one-kernel RMSNorm {n_norm}; "
         f"MFMA-fragment-major {n_mfma}; WMMA-preshuffled gate/up {n_pre}",
         flush=True,
     )

@@ -72,6 +72,7 @@ def load_int4_gemm():
         "pi05w4a4_gemm_gelu_up": (ctypes.c_int, [vp, vp, i64, i32, vp, vp, i32, vp, vp, sz, vp]),
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
+        "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -265,13 +266,32 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
         return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), x.device, kind, gelu=gelu)
 
 
+def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool) -> torch.Tensor:
+    if not x.is_cuda or not weight.is_cuda:
+        raise RuntimeError("rms_norm expects CUDA/HIP tensors")
+    if x.dtype != torch.float16 or weight.dtype != torch.float16:
+        raise RuntimeError("rms_norm expects float16 activations and weight")
+    k = int(x.size(-1))
+    if weight.dim() != 1 or int(weight.numel()) != k:
+        raise RuntimeError(f"rms_norm weight must be [{k}], got {tuple(weight.shape)}")
+    xc = x if x.is_contiguous() else x.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
+    y = torch.empty_like(xc)
+    m = xc.numel() // k if k else 0
+    lib = load_int4_gemm()
+    with torch.cuda.device(x.device):
+        _check(lib.pi05w4a4_rmsnorm(_ptr(xc), _ptr(w), float(eps), 1 if unit_offset else 0, m, k,
+                                    _ptr(y), _stream(x.device)), "pi05w4a4_rmsnorm")
+    return y
+
+
 # ----------------------------------------------------------------------------- custom ops
 def _register_custom_op() -> None:
     global _op_registered
     if _op_registered:
         return
     try:
-        torch.ops.pi05_w4a4.int4_gemm2_gelu
+        torch.ops.pi05_w4a4.rms_norm
         _op_registered = True
         return
     except (AttributeError, RuntimeError):
@@ -340,6 +360,15 @@ def _register_custom_op() -> None:
     def _int4_gemm2_gelu_fake(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor):
         return _fake_out(x, w_gate)
 
+    # Not in the reference: the decoder's RMSNorm (transformers GemmaRMSNorm) in one kernel.
+    @torch.library.custom_op("pi05_w4a4::rms_norm", mutates_args=())
+    def _rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool) -> torch.Tensor:
+        return _rms_norm_impl(x, weight, eps, unit_offset)
+
+    @_rms_norm.register_fake
+    def _rms_norm_fake(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool):
+        return torch.empty_like(x)
+
     _op_registered = True
 
 
@@ -392,6 +421,13 @@ def int4_gemm_acc(x: torch.Tensor, packed_w: torch.Tensor) -> tuple[torch.Tensor
         _check(lib.pi05w4a4_gemm_acc(_ptr(q), m, k, _ptr(w), int(w.size(0)), _ptr(acc),
                                      _stream(x.device)), "pi05w4a4_gemm_acc")
     return acc[:, :n_true], q, sa
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool = True) -> torch.Tensor:
+    """RMSNorm over the last dim in one kernel: fp16((x * rsqrt(mean(x^2) + eps)) *
+    (unit_offset + weight)), fp32 inside (transformers GemmaRMSNorm semantics when
+    ``unit_offset``)."""
+    return torch.ops.pi05_w4a4.rms_norm(x, weight, float(eps), bool(unit_offset))
 
 
 def preload() -> None:

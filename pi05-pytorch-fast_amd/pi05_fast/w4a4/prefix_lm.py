@@ -6,7 +6,8 @@ forwards patched to the shared-quant fused versions (rocm_pi05_optim.py:204-237 
 apply.py:91-213).  LeRobot is not available here, so this module assembles the same
 stack from transformers' Gemma decoder layers: 18 layers, hidden 2048, 8 heads x 256,
 1 KV head, intermediate 16384, RMSNorm (1 + w), RoPE, GELU-tanh, fp16, and installs the
-same hooks (``apply.fuse_shared_activation_quant``).  Attention stays fp16 eager.
+same hooks (``apply.fuse_shared_activation_quant``); on the GPU the RMSNorms run as one
+kernel each (``norm.fuse_rmsnorm``).  Attention stays fp16 eager.
 
 Layers are constructed on the meta device (no fp32 weights are ever materialised); the
 seven projections are W4A4Linear modules holding packed weights, the norms are real.
@@ -21,6 +22,7 @@ import torch.nn as nn
 
 from pi05_fast.w4a4.apply import fuse_shared_activation_quant, load_time_weight
 from pi05_fast.w4a4.linear import W4A4Linear
+from pi05_fast.w4a4.norm import fuse_rmsnorm
 
 PALIGEMMA_2B_LM = dict(
     hidden_size=2048,
@@ -159,6 +161,7 @@ def build_prefix_lm(
     model = PrefixLM(cfg, layers, norm, rotary).eval()
     if fuse:
         fuse_shared_activation_quant(model)
+        fuse_rmsnorm(model)
     return model, weights
 
 

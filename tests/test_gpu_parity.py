@@ -287,3 +287,27 @@ def test_op_errors(ext, cuda):
         ext.int4_gemm(torch.randn(2, 4096, device=cuda).half(), w)
     with pytest.raises(RuntimeError, match="must be int32"):
         ext.int4_gemm(torch.randn(2, 2048, device=cuda).half(), w.float())
+
+
+# ----------------------------------------------------------------------------- decoder RMSNorm
+@pytest.mark.parametrize("m,k", [(776, 2048), (5, 2048), (33, 16384), (7, 64)])
+def test_rms_norm_matches_gemma_module(ext, cuda, m, k):
+    """The one-kernel RMSNorm against transformers' eager GemmaRMSNorm on the same fp16
+    inputs: identical except where the sum of squares, reduced in another order, moves the
+    result across an fp16 rounding boundary (one ulp, on a small fraction of elements)."""
+    from transformers.models.gemma.modeling_gemma import GemmaRMSNorm
+
+    gen = torch.Generator().manual_seed(m * 7 + k)
+    x = (torch.randn(m, k, generator=gen) * 3.0).to(torch.float16).to(cuda)
+    norm = GemmaRMSNorm(k, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(k, generator=gen) * 0.05)
+    norm = norm.to(device=cuda, dtype=torch.float16)
+    with torch.no_grad():
+        want = norm(x)
+        got = ext.rms_norm(x, norm.weight, 1e-6)
+    torch.cuda.synchronize()
+    ulps = (got.view(torch.int16).int() - want.view(torch.int16).int()).abs()
+    assert int(ulps.max()) <= 1, f"max difference {int(ulps.max())} fp16 ulps"
+    frac = float((ulps > 0).float().mean())
+    assert frac <= 5e-3, f"{100 * frac:.3f}% of outputs differ by one ulp"

@@ -11,9 +11,10 @@ shared-quant fused QKV and gate/up forwards, fused GELU*up epilogue), every W4A4
 is recorded with its actual input, and each output must equal the oracle's W4A4 semantics
 (`int4_gemm_ref`: FWHT + INT4 quant, exact integer matmul, `(acc*s_a)*s_w` to fp16) on
 that input bit for bit.  The fused GELU*up output must equal torch's eager
-`gelu(g, approximate="tanh") * u` of the oracle's g and u, bit for bit.  The decoder ops
-around the projections (RMSNorm, RoPE, attention) are transformers' modules; no reference
-test pins them (parity unpinned there).
+`gelu(g, approximate="tanh") * u` of the oracle's g and u, bit for bit.  The decoder's
+RMSNorms run as the one-kernel ``pi05_w4a4::rms_norm`` (checked against transformers'
+module in test_gpu_parity.py); RoPE and attention are transformers' modules, which no
+reference test pins (parity unpinned there).
 """
 
 from __future__ import annotations
@@ -93,6 +94,9 @@ def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens):
         y = model(x, mask)
     torch.cuda.synchronize()
     assert torch.isfinite(y).all()
+    from pi05_fast.w4a4.norm import FusedRMSNorm
+
+    assert isinstance(model.layers[0].input_layernorm, FusedRMSNorm)
     kinds = [c[0] for c in rec.calls]
     assert kinds.count("int4_gemm3") == layers  # QKV
     assert kinds.count("int4_gemm2_gelu") == layers  # gate/up + GELU*up
