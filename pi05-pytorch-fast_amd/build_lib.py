@@ -19,7 +19,7 @@ from pathlib import Path
 
 PKG_ROOT = Path(__file__).resolve().parent
 CSRC = PKG_ROOT / "csrc"
-SOURCES = ["quant_rot.hip", "repack.hip", "gemm.hip", "rmsnorm.hip", "capi.hip"]
+SOURCES = ["quant_rot.hip", "repack.hip", "gemm.hip", "rmsnorm.hip", "attention.hip", "capi.hip"]
 OUT = PKG_ROOT / "pi05_fast" / "w4a4" / "_lib" / "libpi05_w4a4.so"
 
 

@@ -186,6 +186,17 @@ int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroup
   return hip_status(w4a4::launch_gemm(p, pl.cfg.id, stream), "gemm launch");
 }
 
+// Shape checks shared by the two attention entry points.
+int validate_attention(int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d) {
+  if (d != w4a4::kAttnHeadDim)
+    return fail(PI05W4A4_EINVAL, "head_dim must be %d, got %d", w4a4::kAttnHeadDim, d);
+  if (b < 1 || b > 65535) return fail(PI05W4A4_EINVAL, "batch must be in [1, 65535], got %lld", (long long)b);
+  if (s < 1 || s > w4a4::kAttnMaxKeys)
+    return fail(PI05W4A4_EINVAL, "sequence length must be in [1, %d], got %d", w4a4::kAttnMaxKeys, s);
+  if (kvh < 1 || kvh > 65535 || h < kvh || h % kvh != 0)
+    return fail(PI05W4A4_EINVAL, "query heads (%d) must be a multiple of KV heads (%d)", h, kvh);
+  return ok();
+}
 }  // namespace
 
 extern "C" {
@@ -329,6 +340,86 @@ int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t 
   return hip_status(w4a4::launch_rmsnorm(x_fp16, w_fp16, eps, unit_offset != 0, m, k, y_fp16,
                                          static_cast<hipStream_t>(stream)),
                     "rmsnorm launch");
+}
+
+
+size_t pi05w4a4_attn_vt_elems(int64_t b, int32_t s, int32_t kvh, int32_t d) {
+  if (b < 1 || s < 1 || kvh < 1 || d < 1) return 0;
+  return static_cast<size_t>(b) * kvh * d * static_cast<size_t>(w4a4::attn_s_pad(s));
+}
+
+int pi05w4a4_attn_kv_prep(const void* k, const void* v, int64_t ld_kv, const void* cos_fp16,
+                          const void* sin_fp16, int64_t b, int32_t s, int32_t kvh, int32_t d,
+                          void* k_rope, void* v_t, void* stream) {
+  int rc = validate_attention(b, s, kvh, kvh, d);
+  if (rc) return rc;
+  if (!k || !v || !cos_fp16 || !sin_fp16 || !k_rope || !v_t) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (ld_kv < static_cast<int64_t>(kvh) * d || ld_kv % 8 != 0)
+    return fail(PI05W4A4_EINVAL, "K/V token stride must be a multiple of 8 and >= KVH*head_dim, got %lld",
+                (long long)ld_kv);
+  if (!aligned(k, 16) || !aligned(v, 16) || !aligned(cos_fp16, 16) || !aligned(sin_fp16, 16) ||
+      !aligned(k_rope, 16) || !aligned(v_t, 16))
+    return fail(PI05W4A4_EINVAL, "k, v, cos, sin, k_rope and v_t must be 16-byte aligned");
+  w4a4::AttnParams p{};
+  p.k = static_cast<const _Float16*>(k);
+  p.v = static_cast<const _Float16*>(v);
+  p.ld_kv = ld_kv;
+  p.cosb = static_cast<const _Float16*>(cos_fp16);
+  p.sinb = static_cast<const _Float16*>(sin_fp16);
+  p.b = static_cast<int32_t>(b);
+  p.s = s;
+  p.h = kvh;
+  p.kvh = kvh;
+  p.s_pad = static_cast<int32_t>(w4a4::attn_s_pad(s));
+  p.k_rope = static_cast<_Float16*>(k_rope);
+  p.v_t = static_cast<_Float16*>(v_t);
+  return hip_status(w4a4::launch_attn_kv_prep(p, static_cast<hipStream_t>(stream)), "attention K/V prep launch");
+}
+
+int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* k_rope, const void* v_t,
+                              const void* cos_fp16, const void* sin_fp16, const void* mask,
+                              int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
+                              int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
+                              int64_t ld_out, void* stream) {
+  int rc = validate_attention(b, s, h, kvh, d);
+  if (rc) return rc;
+  if (!q || !k_rope || !v_t || !cos_fp16 || !sin_fp16 || !out) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (ld_q < static_cast<int64_t>(h) * d || ld_q % 8 != 0)
+    return fail(PI05W4A4_EINVAL, "query token stride must be a multiple of 8 and >= H*head_dim, got %lld",
+                (long long)ld_q);
+  if (ld_out < static_cast<int64_t>(h) * d || ld_out % 4 != 0)
+    return fail(PI05W4A4_EINVAL, "output token stride must be a multiple of 4 and >= H*head_dim, got %lld",
+                (long long)ld_out);
+  if (!aligned(q, 16) || !aligned(k_rope, 16) || !aligned(v_t, 16) || !aligned(cos_fp16, 16) ||
+      !aligned(sin_fp16, 16) || !aligned(out, 8))
+    return fail(PI05W4A4_EINVAL, "q, k_rope, v_t, cos and sin must be 16-byte aligned, out 8-byte aligned");
+  if (mask != nullptr) {
+    if (mask_len < s || mask_len % 4 != 0)
+      return fail(PI05W4A4_EINVAL, "mask rows must hold a multiple of 4 keys >= S, got %d", mask_len);
+    if (mask_bs < 0 || mask_bs % 4 != 0 || mask_rs < mask_len || mask_rs % 4 != 0)
+      return fail(PI05W4A4_EINVAL, "mask strides must be multiples of 4 (row stride >= row length)");
+    if (!aligned(mask, 8)) return fail(PI05W4A4_EINVAL, "mask must be 8-byte aligned");
+  }
+  w4a4::AttnParams p{};
+  p.q = static_cast<const _Float16*>(q);
+  p.ld_q = ld_q;
+  p.cosb = static_cast<const _Float16*>(cos_fp16);
+  p.sinb = static_cast<const _Float16*>(sin_fp16);
+  p.mask = static_cast<const _Float16*>(mask);
+  p.mask_bs = mask_bs;
+  p.mask_rs = mask_rs;
+  p.mask_len = mask_len;
+  p.scaling = scaling;
+  p.b = static_cast<int32_t>(b);
+  p.s = s;
+  p.h = h;
+  p.kvh = kvh;
+  p.s_pad = static_cast<int32_t>(w4a4::attn_s_pad(s));
+  p.k_rope = const_cast<_Float16*>(static_cast<const _Float16*>(k_rope));
+  p.v_t = const_cast<_Float16*>(static_cast<const _Float16*>(v_t));
+  p.out = static_cast<_Float16*>(out);
+  p.ld_out = ld_out;
+  return hip_status(w4a4::launch_prefix_attention(p, static_cast<hipStream_t>(stream)), "prefix attention launch");
 }
 
 int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,

@@ -102,6 +102,31 @@ enum TileCfg : int {
   kCfg7x4K8 = 6,  // MI 7, NI 4, 8 waves along K (2 per SIMD): 112 x 64, for very long K
 };
 
+// Prefix attention (attention.hip): head_dim 256, grouped-query heads, fp16.
+constexpr int kAttnHeadDim = 256;
+constexpr int kAttnMaxKeys = 1024;
+struct AttnParams {
+  const _Float16* q;      // [B, S, H, 256], token stride ld_q (elements)
+  int64_t ld_q;
+  const _Float16* k;      // [B, S, KVH, 256] before RoPE, token stride ld_kv
+  const _Float16* v;      // [B, S, KVH, 256], token stride ld_kv
+  int64_t ld_kv;
+  const _Float16* cosb;   // [B, S, 256]
+  const _Float16* sinb;   // [B, S, 256]
+  const _Float16* mask;   // additive, element (b, sq, sk) at b*mask_bs + sq*mask_rs + sk; or null
+  int64_t mask_bs;
+  int64_t mask_rs;
+  int32_t mask_len;       // keys per mask row (>= S, multiple of 4)
+  float scaling;
+  int32_t b, s, h, kvh;
+  int32_t s_pad;          // keys rounded up to a multiple of 64
+  _Float16* k_rope;       // [B, KVH, S, 256] with RoPE
+  _Float16* v_t;          // [B, KVH, 256, s_pad], zero past S
+  _Float16* out;          // [B, S, H, 256], token stride ld_out
+  int64_t ld_out;
+};
+int64_t attn_s_pad(int32_t s);
+
 // Launchers (return hipError_t of the launch).
 hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, float* sa,
                            float inv_sqrt_k, hipStream_t stream);
@@ -112,5 +137,7 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t stream);
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int unit_offset, int64_t m,
                           int32_t k, void* y, hipStream_t stream);
+hipError_t launch_attn_kv_prep(const AttnParams& p, hipStream_t stream);
+hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream);
 
 }  // namespace w4a4

@@ -183,6 +183,40 @@ def _fused_mlp_forward(self, x: torch.Tensor) -> torch.Tensor:
     return y if y.dtype == x.dtype else y.to(dtype=x.dtype)
 
 
+_EAGER_ATTENTION = ("eager", "w4a4_eager")
+
+
+def _prefix_attention_fits(self, q: torch.Tensor, k: torch.Tensor, attention_mask, past_key_values) -> bool:
+    """Whether RoPE + attention of this call can run as ``extension.prefix_attention``:
+    an eager attention implementation (bidirectional unless the additive mask says
+    otherwise), head_dim 256, fp16 on the GPU, at most 1024 tokens, no dropout, logit
+    softcap or sliding window, an fp16 [B|1, 1, S, >=S] mask or none, and an empty cache
+    (a prefix forward).  ``PI05_W4A4_FUSE_ATTN=0`` keeps transformers' path."""
+    if os.environ.get("PI05_W4A4_FUSE_ATTN", "1") == "0":
+        return False
+    cfg = self.config
+    if getattr(cfg, "_attn_implementation", "eager") not in _EAGER_ATTENTION:
+        return False
+    if self.training and getattr(self, "attention_dropout", 0.0):
+        return False
+    if getattr(cfg, "attn_logit_softcapping", None) or getattr(self, "sliding_window", None):
+        return False
+    if self.head_dim != 256 or q.dtype != torch.float16 or not q.is_cuda or q.dim() != 3:
+        return False
+    b, s = int(q.size(0)), int(q.size(1))
+    if s > 1024 or k.size(-1) % 256 or q.size(-1) % k.size(-1):
+        return False
+    if attention_mask is not None:
+        m = attention_mask
+        if m.dtype != torch.float16 or m.dim() != 4 or m.size(1) != 1 or m.size(0) not in (1, b):
+            return False
+        if m.size(2) != s or m.size(3) < s:
+            return False
+    if past_key_values is not None and past_key_values.get_seq_length(self.layer_idx) != 0:
+        return False
+    return True
+
+
 def _fused_attn_forward(
     self,
     hidden_states: torch.Tensor,
@@ -191,7 +225,9 @@ def _fused_attn_forward(
     past_key_values=None,
     **kwargs,
 ):
-    """Gemma attention with QKV from one int4_gemm3 call (apply.py:145-191)."""
+    """Gemma attention with QKV from one int4_gemm3 call (apply.py:145-191).  When the call
+    fits (``_prefix_attention_fits``), RoPE and the attention run as the two kernels of
+    ``extension.prefix_attention``; otherwise transformers' RoPE and attention interface."""
     from transformers.modeling_utils import ALL_ATTENTION_FUNCTIONS
     from transformers.models.gemma.modeling_gemma import apply_rotary_pos_emb, eager_attention_forward
 
@@ -205,11 +241,23 @@ def _fused_attn_forward(
         self.k_proj.packed,
         self.v_proj.packed,
     )
+    cos, sin = position_embeddings
+    if _prefix_attention_fits(self, q, k, attention_mask, past_key_values):
+        from pi05_fast.w4a4.extension import prefix_attention
+
+        out, key_states = prefix_attention(
+            q, k, v, cos, sin, attention_mask, float(self.scaling),
+            q.size(-1) // self.head_dim, k.size(-1) // self.head_dim,
+        )
+        if past_key_values is not None:
+            value_states = v.view(hidden_shape).transpose(1, 2)
+            past_key_values.update(key_states, value_states, self.layer_idx)
+        return self.o_proj(out.reshape(*input_shape, -1)), None
+
     query_states = q.view(hidden_shape).transpose(1, 2)
     key_states = k.view(hidden_shape).transpose(1, 2)
     value_states = v.view(hidden_shape).transpose(1, 2)
 
-    cos, sin = position_embeddings
     query_states, key_states = apply_rotary_pos_emb(query_states, key_states, cos, sin)
 
     if past_key_values is not None:

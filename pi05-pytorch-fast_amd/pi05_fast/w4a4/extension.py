@@ -73,6 +73,12 @@ def load_int4_gemm():
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
+        "pi05w4a4_attn_vt_elems": (sz, [i64, i32, i32, i32]),
+        "pi05w4a4_attn_kv_prep": (ctypes.c_int, [vp, vp, i64, vp, vp, i64, i32, i32, i32, vp, vp, vp]),
+        "pi05w4a4_prefix_attention": (
+            ctypes.c_int,
+            [vp, i64, vp, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp],
+        ),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -285,13 +291,76 @@ def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offse
     return y
 
 
+ATTN_HEAD_DIM = 256
+ATTN_MAX_KEYS = 1024
+
+
+def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int):
+    """(tensor, batch stride, row stride, row length) of an additive fp16 mask [B|1, 1, S, >=S]
+    in the form the kernel reads (row length a multiple of 4 >= S, strides multiples of 4,
+    8-byte aligned); a padded copy is made only when the given tensor does not fit."""
+    if mask is None:
+        return None, 0, 0, 0
+    if mask.dtype != torch.float16 or mask.dim() != 4 or mask.size(1) != 1:
+        raise RuntimeError("prefix_attention mask must be an additive float16 [B, 1, S, Sk] tensor")
+    if mask.size(0) not in (1, b) or mask.size(2) != s or mask.size(3) < s:
+        raise RuntimeError(f"prefix_attention mask shape {tuple(mask.shape)} does not fit B={b}, S={s}")
+    m = mask[:, 0, :, :]
+    s4 = (s + 3) // 4 * 4
+    fits = (
+        m.size(2) >= s4
+        and m.stride(2) == 1
+        and m.stride(1) % 4 == 0
+        and (m.size(0) == 1 or m.stride(0) % 4 == 0)
+        and m.data_ptr() % 8 == 0
+    )
+    if not fits:
+        m = torch.nn.functional.pad(m[:, :, :s], (0, s4 - s)).contiguous()
+    bs = 0 if m.size(0) == 1 else m.stride(0)
+    return m, bs, m.stride(1), s4
+
+
+def _prefix_attention_impl(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+    mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    d = ATTN_HEAD_DIM
+    for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
+        if not t.is_cuda:
+            raise RuntimeError(f"prefix_attention: {name} must be on CUDA/HIP")
+        if t.dtype != torch.float16:
+            raise RuntimeError(f"prefix_attention: {name} must be float16")
+    if q.dim() != 3 or k.dim() != 3 or v.shape != k.shape:
+        raise RuntimeError("prefix_attention expects q [B, S, H*256], k and v [B, S, KVH*256]")
+    b, s = int(q.size(0)), int(q.size(1))
+    h, kvh = int(num_heads), int(num_kv_heads)
+    if q.size(2) != h * d or k.size(2) != kvh * d or tuple(k.shape[:2]) != (b, s):
+        raise RuntimeError(f"prefix_attention: q {tuple(q.shape)} / k {tuple(k.shape)} do not match "
+                           f"{h} query and {kvh} KV heads of {d}")
+    qc, kc, vc = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
+    cs = [t.expand(b, s, d).contiguous() if t.dim() == 3 else t.reshape(b, s, d).contiguous() for t in (cos, sin)]
+    m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s)
+    lib = load_int4_gemm()
+    k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
+    v_t = torch.empty(int(lib.pi05w4a4_attn_vt_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
+    out = torch.empty((b, s, h * d), dtype=torch.float16, device=q.device)
+    with torch.cuda.device(q.device):
+        st = _stream(q.device)
+        _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
+                                         _ptr(k_rope), _ptr(v_t), st), "pi05w4a4_attn_kv_prep")
+        _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(k_rope), _ptr(v_t), _ptr(cs[0]), _ptr(cs[1]),
+                                             _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
+                                             _ptr(out), h * d, st), "pi05w4a4_prefix_attention")
+    return out, k_rope
+
+
 # ----------------------------------------------------------------------------- custom ops
 def _register_custom_op() -> None:
     global _op_registered
     if _op_registered:
         return
     try:
-        torch.ops.pi05_w4a4.rms_norm
+        torch.ops.pi05_w4a4.prefix_attention
         _op_registered = True
         return
     except (AttributeError, RuntimeError):
@@ -369,6 +438,20 @@ def _register_custom_op() -> None:
     def _rms_norm_fake(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool):
         return torch.empty_like(x)
 
+    # Not in the reference: RoPE + attention between int4_gemm3 and o_proj in two kernels.
+    @torch.library.custom_op("pi05_w4a4::prefix_attention", mutates_args=())
+    def _prefix_attention(
+        q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+        mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        return _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads)
+
+    @_prefix_attention.register_fake
+    def _prefix_attention_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads):
+        b, s = q.shape[0], q.shape[1]
+        out = q.new_empty((b, s, num_heads * ATTN_HEAD_DIM))
+        return out, q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM))
+
     _op_registered = True
 
 
@@ -428,6 +511,21 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: boo
     (unit_offset + weight)), fp32 inside (transformers GemmaRMSNorm semantics when
     ``unit_offset``)."""
     return torch.ops.pi05_w4a4.rms_norm(x, weight, float(eps), bool(unit_offset))
+
+
+def prefix_attention(
+    q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+    mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """RoPE + attention of the prefix LM (head_dim 256, fp16, at most 1024 tokens).
+
+    q [B, S, H*256], k and v [B, S, KVH*256] as int4_gemm3 returns them (before RoPE),
+    cos/sin [B, S, 256] (the decoder's position embeddings), mask None or additive fp16
+    [B|1, 1, S, >=S].  Returns (attention output [B, S, H*256], key states with RoPE
+    [B, KVH, S, 256]): transformers' apply_rotary_pos_emb + eager_attention_forward, the
+    key states bit-identical to the eager ones."""
+    return torch.ops.pi05_w4a4.prefix_attention(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
+                                                int(num_kv_heads))
 
 
 def preload() -> None:

@@ -7,7 +7,9 @@ apply.py:91-213).  LeRobot is not available here, so this module assembles the s
 stack from transformers' Gemma decoder layers: 18 layers, hidden 2048, 8 heads x 256,
 1 KV head, intermediate 16384, RMSNorm (1 + w), RoPE, GELU-tanh, fp16, and installs the
 same hooks (``apply.fuse_shared_activation_quant``); on the GPU the RMSNorms run as one
-kernel each (``norm.fuse_rmsnorm``).  Attention stays fp16 eager.
+kernel each (``norm.fuse_rmsnorm``) and RoPE + attention as the two kernels of
+``extension.prefix_attention`` (``PI05_W4A4_FUSE_ATTN=0``: transformers' RoPE and the
+fp16 eager attention below).
 
 Layers are constructed on the meta device (no fp32 weights are ever materialised); the
 seven projections are W4A4Linear modules holding packed weights, the norms are real.

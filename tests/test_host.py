@@ -274,6 +274,33 @@ def test_abi_validation_without_gpu(lib):
     assert lib.pi05w4a4_gemm(vp(16), vp(16), 0, 64, vp(16), 16, vp(0), vp(0), 0, vp(0)) == 0
 
 
+def test_attention_abi_validation_without_gpu(lib):
+    vp = ctypes.c_void_p
+    p = vp(256)  # aligned, never dereferenced: every call below fails validation first
+
+    def prep(b=1, s=776, kvh=1, d=256, ld=256, k=p):
+        return lib.pi05w4a4_attn_kv_prep(k, p, ld, p, p, b, s, kvh, d, p, p, vp(0))
+
+    def attn(b=1, s=776, h=8, kvh=1, d=256, mask=vp(0), mlen=0, mbs=0, mrs=0, ld_q=2048, out=p):
+        return lib.pi05w4a4_prefix_attention(p, ld_q, p, p, p, p, mask, mbs, mrs, mlen, 0.0625,
+                                             b, s, h, kvh, d, out, 2048, vp(0))
+
+    assert lib.pi05w4a4_attn_vt_elems(1, 776, 1, 256) == 256 * 832  # keys padded to 64
+    assert lib.pi05w4a4_attn_vt_elems(2, 64, 2, 256) == 2 * 2 * 256 * 64
+    assert prep(d=128) == 1 and "head_dim must be 256" in _err(lib)
+    assert prep(s=1025) == 1 and "sequence length" in _err(lib)
+    assert prep(s=0) == 1
+    assert prep(ld=200) == 1 and "token stride" in _err(lib)
+    assert prep(k=vp(258)) == 1 and "aligned" in _err(lib)
+    assert attn(h=6, kvh=4) == 1 and "multiple of KV heads" in _err(lib)
+    assert attn(ld_q=1024) == 1 and "token stride" in _err(lib)
+    assert attn(out=vp(0)) == 1 and "null" in _err(lib)
+    # mask rows: a multiple of 4 keys, at least S, strides multiples of 4
+    assert attn(mask=p, mlen=775, mrs=776) == 1 and "mask rows" in _err(lib)
+    assert attn(mask=p, mlen=776, mrs=776, mbs=2) == 1 and "mask strides" in _err(lib)
+    assert attn(mask=vp(260), mlen=776, mrs=776) == 1 and "8-byte" in _err(lib)
+
+
 # ----------------------------------------------------------------------------- op surface
 def test_custom_ops_registered_with_fakes():
     from pi05_fast.w4a4 import extension  # noqa: F401
