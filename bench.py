@@ -6,7 +6,7 @@
 Workload (`value`): one forward of the 18-layer Gemma-2B-shaped prefix LM (hidden 2048,
 8x256 heads, 1 KV head, intermediate 16384) over a 776-token prefix, batch 1, every
 q/k/v/o/gate/up/down projection running the W4A4 path (FWHT + INT4 quant, int8-MFMA
-GEMM) and attention fp16 eager.  Weights are synthetic packed INT4 (random codes with the
+GEMM), RoPE + attention as the two prefix-attention kernels and each RMSNorm as one kernel.  Weights are synthetic packed INT4 (random codes with the
 statistics of a packed N(0, 0.02) weight), inputs synthetic N(0, 1/sqrt(2048)) prefix
 embeddings, all resident in HBM.  Timed region: K replays of the whole forward captured
 in one HIP graph, bracketed by device synchronisation; `value` = ms per forward.
@@ -18,7 +18,8 @@ captured in one HIP graph; HIP events recorded on the launching stream (torch's 
 stream, which the library uses) bracket each of 5 replays, and the median per-launch
 time gives the kernel duration, int8 TOPS and the fraction of the MI355X dense int8 MFMA
 peak (GEMMs) or of HBM bandwidth (quantizers).  The graph removes host launch gaps
-between the back-to-back kernels.
+between the back-to-back kernels.  The non-W4A4 kernels of the forward (prefix attention,
+its K/V prep, RMSNorm) are timed the same way under `other_kernels`.
 The dominant kernel of the forward (gate/up GEMM) is the `roofline` object; its `traffic`
 (HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed
 under profiles/ when present.
@@ -48,6 +49,7 @@ for _p in (ROOT / "pi05-pytorch-fast_amd", ROOT):
 
 METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X)"
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
+FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
 TRAFFIC_FILE = ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md"
 
@@ -168,6 +170,57 @@ class KernelBench:
         return {"m": m, "k": k, "n": n, "avg_us": round(us, 3), "ops": ops, "tops": round(tops, 1),
                 "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "bytes": nbytes,
                 "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb}
+
+
+    def attention(self, b, s, h=8, kvh=1):
+        """The two prefix-attention kernels (K RoPE + V transpose, then attention) at one
+        decoder layer's shapes, zero additive mask."""
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        d = 256
+        gen = torch.Generator(device=self.dev).manual_seed(7)
+        q = torch.randn(b, s, h * d, device=self.dev, generator=gen).half()
+        k = torch.randn(b, s, kvh * d, device=self.dev, generator=gen).half()
+        v = torch.randn(b, s, kvh * d, device=self.dev, generator=gen).half()
+        ang = torch.rand(b, s, d, device=self.dev, generator=gen) * 6.28
+        cos, sin = ang.cos().half(), ang.sin().half()
+        s4 = (s + 3) // 4 * 4
+        mask = torch.zeros(b, s, s4, dtype=torch.float16, device=self.dev)
+        k_rope = torch.empty(b, kvh, s, d, dtype=torch.float16, device=self.dev)
+        kvm = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=self.dev)
+        out = torch.empty(b, s, h * d, dtype=torch.float16, device=self.dev)
+        prep = lambda: self._check(lib.pi05w4a4_attn_kv_prep(  # noqa: E731
+            P(k), P(v), kvh * d, P(cos), P(sin), b, s, kvh, d, P(k_rope), P(kvm), self._stream()))
+        attn = lambda: self._check(lib.pi05w4a4_prefix_attention(  # noqa: E731
+            P(q), h * d, P(kvm), P(cos), P(sin), P(mask), s * s4, s4, s4, d**-0.5,
+            b, s, h, kvh, d, P(out), h * d, self._stream()))
+        prep()
+        us_prep = self._time(prep)
+        us_attn = self._time(attn)
+        flops = 4.0 * b * h * s * s * d
+        s_pad = (s + 63) // 64 * 64
+        # Bytes that cross each workgroup's vector-memory path: every workgroup streams all
+        # of K and V (keys x 2 x 512 B) plus its 32 query rows (and cos/sin) once per wave.
+        wgs = b * kvh * -(-(s * h // kvh) // 32)
+        per_wg = 2.0 * s_pad * d * 2 + 4 * 32 * d * 2 * 3 + 4 * 32 * s_pad * 2 / 4
+        tflops = flops / (us_attn * 1e-6) / 1e12
+        return {
+            "attention": {"b": b, "s": s, "h": h, "kvh": kvh, "avg_us": round(us_attn, 3), "flops": flops,
+                          "tflops": round(tflops, 2), "frac_fp16_peak": round(tflops / FP16_PEAK_TFLOPS, 4),
+                          "workgroups": wgs, "bytes_per_workgroup": per_wg,
+                          "l2_to_cu_gbs": round(wgs * per_wg / (us_attn * 1e-6) / 1e9, 1)},
+            "attn_kv_prep": {"avg_us": round(us_prep, 3),
+                             "bytes": 2.0 * b * s * kvh * d * 2 * 2 + 2.0 * b * s * d * 2},
+        }
+
+    def rmsnorm(self, m, k=2048):
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16)
+        w = torch.randn(k, device=self.dev, dtype=torch.float16)
+        y = torch.empty_like(x)
+        us = self._time(lambda: self._check(lib.pi05w4a4_rmsnorm(P(x), P(w), 1e-6, 1, m, k, P(y), self._stream())))
+        nbytes = 4.0 * m * k + 2 * k
+        return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes,
+                "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
@@ -356,6 +409,8 @@ def main() -> int:
         del graph
 
         kernels = kernel_table(kb, m)
+        others = kb.attention(args.batch, args.tokens)
+        others["rmsnorm"] = kb.rmsnorm(m)
 
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
@@ -408,6 +463,7 @@ def main() -> int:
         "w4a4_gop_per_forward": round(total_ops / 1e9, 1),
         "w4a4_kernel_ms_per_forward": round(w4a4_us_per_layer * args.layers / 1e3, 3),
         "gemms": kernels,
+        "other_kernels": others,
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:

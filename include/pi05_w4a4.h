@@ -184,27 +184,30 @@ int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t 
  * eager_attention_forward) with two kernels of the same fp16/fp32 operation order:
  *   q', k' = fp16(fp16(x * cos) + fp16(rotate_half(x) * sin))          (bit-exact)
  *   s = fp16(fp16(fp16(q' . k') * scaling) + mask); p = fp16(softmax_fp32(s)); o = fp16(p v)
- * Only the order of the fp32 sums inside q'.k', the softmax row sum and p v differs from
- * torch's.  S (keys = queries) is at most 1024.
+ * The fp32 sums run in another order than torch's and exp uses the hardware exp2, so o
+ * agrees with the eager output to fp16 rounding.  S (keys = queries) is at most 1024.
  *
  * pi05w4a4_attn_kv_prep: k, v fp16 [B, S, KVH, 256] with token stride ld_kv (elements,
  * multiple of 8), cos/sin fp16 [B, S, 256] ->
  *   k_rope fp16 [B, KVH, S, 256] (RoPE applied: the key states a KV cache stores) and
- *   v_t fp16 [B, KVH, 256, s_pad] (V transposed, keys zero-padded to s_pad = S rounded up
- *   to 64; pi05w4a4_attn_vt_elems(B, S, KVH, 256) elements).
+ *   kv_mfma, pi05w4a4_attn_kv_mfma_elems(B, S, KVH, 256) fp16 elements: per (b, KV head),
+ *   K with RoPE and then V^T in MFMA-fragment-major order with the keys zero-padded to
+ *   s_pad = S rounded up to 64 (K fragment (j, t), 512 elements at (8j + t) * 512: lane L
+ *   holds K[16j + L%16][32t + 8(L/16) + 0..7]; V^T fragment (db, t) at
+ *   s_pad*256 + (db*s_pad/32 + t) * 512: lane L holds V[32t + 8(L/16) + 0..7][16db + L%16]).
  * pi05w4a4_prefix_attention: q fp16 [B, S, H, 256] (token stride ld_q, the QKV GEMM's q
- * output; RoPE is applied inside), k_rope and v_t from kv_prep, the same cos/sin, an
+ * output; RoPE is applied inside), kv_mfma from kv_prep, the same cos/sin, an
  * optional additive fp16 mask (element (b, sq, sk) at mask[b*mask_bs + sq*mask_rs + sk];
  * mask_bs = 0 broadcasts one mask; mask_len >= S keys per row, a multiple of 4, strides
  * multiples of 4, 8-byte aligned; null for none) and `scaling` ->
  *   out fp16 [B, S, H, 256] with token stride ld_out (multiple of 4).
  * All other pointers 16-byte aligned (out 8-byte).
  */
-size_t pi05w4a4_attn_vt_elems(int64_t b, int32_t s, int32_t kvh, int32_t d);
+size_t pi05w4a4_attn_kv_mfma_elems(int64_t b, int32_t s, int32_t kvh, int32_t d);
 int pi05w4a4_attn_kv_prep(const void* k, const void* v, int64_t ld_kv, const void* cos_fp16,
                           const void* sin_fp16, int64_t b, int32_t s, int32_t kvh, int32_t d,
-                          void* k_rope, void* v_t, void* stream);
-int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* k_rope, const void* v_t,
+                          void* k_rope, void* kv_mfma, void* stream);
+int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               const void* cos_fp16, const void* sin_fp16, const void* mask,
                               int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
                               int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,

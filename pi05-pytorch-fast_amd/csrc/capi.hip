@@ -343,23 +343,23 @@ int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t 
 }
 
 
-size_t pi05w4a4_attn_vt_elems(int64_t b, int32_t s, int32_t kvh, int32_t d) {
+size_t pi05w4a4_attn_kv_mfma_elems(int64_t b, int32_t s, int32_t kvh, int32_t d) {
   if (b < 1 || s < 1 || kvh < 1 || d < 1) return 0;
-  return static_cast<size_t>(b) * kvh * d * static_cast<size_t>(w4a4::attn_s_pad(s));
+  return static_cast<size_t>(b) * kvh * 2 * d * static_cast<size_t>(w4a4::attn_s_pad(s));
 }
 
 int pi05w4a4_attn_kv_prep(const void* k, const void* v, int64_t ld_kv, const void* cos_fp16,
                           const void* sin_fp16, int64_t b, int32_t s, int32_t kvh, int32_t d,
-                          void* k_rope, void* v_t, void* stream) {
+                          void* k_rope, void* kv_mfma, void* stream) {
   int rc = validate_attention(b, s, kvh, kvh, d);
   if (rc) return rc;
-  if (!k || !v || !cos_fp16 || !sin_fp16 || !k_rope || !v_t) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!k || !v || !cos_fp16 || !sin_fp16 || !k_rope || !kv_mfma) return fail(PI05W4A4_EINVAL, "null pointer argument");
   if (ld_kv < static_cast<int64_t>(kvh) * d || ld_kv % 8 != 0)
     return fail(PI05W4A4_EINVAL, "K/V token stride must be a multiple of 8 and >= KVH*head_dim, got %lld",
                 (long long)ld_kv);
   if (!aligned(k, 16) || !aligned(v, 16) || !aligned(cos_fp16, 16) || !aligned(sin_fp16, 16) ||
-      !aligned(k_rope, 16) || !aligned(v_t, 16))
-    return fail(PI05W4A4_EINVAL, "k, v, cos, sin, k_rope and v_t must be 16-byte aligned");
+      !aligned(k_rope, 16) || !aligned(kv_mfma, 16))
+    return fail(PI05W4A4_EINVAL, "k, v, cos, sin, k_rope and kv_mfma must be 16-byte aligned");
   w4a4::AttnParams p{};
   p.k = static_cast<const _Float16*>(k);
   p.v = static_cast<const _Float16*>(v);
@@ -372,27 +372,27 @@ int pi05w4a4_attn_kv_prep(const void* k, const void* v, int64_t ld_kv, const voi
   p.kvh = kvh;
   p.s_pad = static_cast<int32_t>(w4a4::attn_s_pad(s));
   p.k_rope = static_cast<_Float16*>(k_rope);
-  p.v_t = static_cast<_Float16*>(v_t);
+  p.kv_mfma = static_cast<_Float16*>(kv_mfma);
   return hip_status(w4a4::launch_attn_kv_prep(p, static_cast<hipStream_t>(stream)), "attention K/V prep launch");
 }
 
-int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* k_rope, const void* v_t,
+int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               const void* cos_fp16, const void* sin_fp16, const void* mask,
                               int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
                               int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
                               int64_t ld_out, void* stream) {
   int rc = validate_attention(b, s, h, kvh, d);
   if (rc) return rc;
-  if (!q || !k_rope || !v_t || !cos_fp16 || !sin_fp16 || !out) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!q || !kv_mfma || !cos_fp16 || !sin_fp16 || !out) return fail(PI05W4A4_EINVAL, "null pointer argument");
   if (ld_q < static_cast<int64_t>(h) * d || ld_q % 8 != 0)
     return fail(PI05W4A4_EINVAL, "query token stride must be a multiple of 8 and >= H*head_dim, got %lld",
                 (long long)ld_q);
   if (ld_out < static_cast<int64_t>(h) * d || ld_out % 4 != 0)
     return fail(PI05W4A4_EINVAL, "output token stride must be a multiple of 4 and >= H*head_dim, got %lld",
                 (long long)ld_out);
-  if (!aligned(q, 16) || !aligned(k_rope, 16) || !aligned(v_t, 16) || !aligned(cos_fp16, 16) ||
+  if (!aligned(q, 16) || !aligned(kv_mfma, 16) || !aligned(cos_fp16, 16) ||
       !aligned(sin_fp16, 16) || !aligned(out, 8))
-    return fail(PI05W4A4_EINVAL, "q, k_rope, v_t, cos and sin must be 16-byte aligned, out 8-byte aligned");
+    return fail(PI05W4A4_EINVAL, "q, kv_mfma, cos and sin must be 16-byte aligned, out 8-byte aligned");
   if (mask != nullptr) {
     if (mask_len < s || mask_len % 4 != 0)
       return fail(PI05W4A4_EINVAL, "mask rows must hold a multiple of 4 keys >= S, got %d", mask_len);
@@ -415,8 +415,7 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* k_rope, c
   p.h = h;
   p.kvh = kvh;
   p.s_pad = static_cast<int32_t>(w4a4::attn_s_pad(s));
-  p.k_rope = const_cast<_Float16*>(static_cast<const _Float16*>(k_rope));
-  p.v_t = const_cast<_Float16*>(static_cast<const _Float16*>(v_t));
+  p.kv_mfma = const_cast<_Float16*>(static_cast<const _Float16*>(kv_mfma));
   p.out = static_cast<_Float16*>(out);
   p.ld_out = ld_out;
   return hip_status(w4a4::launch_prefix_attention(p, static_cast<hipStream_t>(stream)), "prefix attention launch");

@@ -121,7 +121,7 @@ struct AttnParams {
   int32_t b, s, h, kvh;
   int32_t s_pad;          // keys rounded up to a multiple of 64
   _Float16* k_rope;       // [B, KVH, S, 256] with RoPE
-  _Float16* v_t;          // [B, KVH, 256, s_pad], zero past S
+  _Float16* kv_mfma;      // per (b, KV head): K then V^T in MFMA-fragment-major order
   _Float16* out;          // [B, S, H, 256], token stride ld_out
   int64_t ld_out;
 };

@@ -73,11 +73,11 @@ def load_int4_gemm():
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
-        "pi05w4a4_attn_vt_elems": (sz, [i64, i32, i32, i32]),
+        "pi05w4a4_attn_kv_mfma_elems": (sz, [i64, i32, i32, i32]),
         "pi05w4a4_attn_kv_prep": (ctypes.c_int, [vp, vp, i64, vp, vp, i64, i32, i32, i32, vp, vp, vp]),
         "pi05w4a4_prefix_attention": (
             ctypes.c_int,
-            [vp, i64, vp, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp],
+            [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp],
         ),
     }
     for name, (res, args) in sig.items():
@@ -342,13 +342,13 @@ def _prefix_attention_impl(
     m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s)
     lib = load_int4_gemm()
     k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
-    v_t = torch.empty(int(lib.pi05w4a4_attn_vt_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
+    kv_mfma = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
     out = torch.empty((b, s, h * d), dtype=torch.float16, device=q.device)
     with torch.cuda.device(q.device):
         st = _stream(q.device)
         _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
-                                         _ptr(k_rope), _ptr(v_t), st), "pi05w4a4_attn_kv_prep")
-        _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(k_rope), _ptr(v_t), _ptr(cs[0]), _ptr(cs[1]),
+                                         _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
+        _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
                                              _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
                                              _ptr(out), h * d, st), "pi05w4a4_prefix_attention")
     return out, k_rope

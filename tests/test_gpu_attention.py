@@ -2,7 +2,8 @@
 o_proj of the fused attention forward (apply.py:167-188).
 
 - Key states with RoPE must equal transformers' ``apply_rotary_pos_emb`` on the same fp16
-  tensors bit for bit, and V^T must be V transposed with zero key padding.
+  tensors bit for bit, and the MFMA-fragment-major K / V^T copies must hold exactly those
+  keys and V (zero key padding) at the positions the C ABI header states.
 - The attention output is floating point: it is checked against a float32 torch
   reference of the same op (RoPE'd q/k from torch, fp32 scores + mask, fp32 softmax, fp32
   PV) with rel-L2 <= 2e-3, next to transformers' eager fp16 path, whose own error
@@ -99,27 +100,47 @@ def _rel_l2(a, b):
     return float((a.float() - b.float()).norm() / b.float().norm())
 
 
+def _fragments_k(kp: torch.Tensor) -> torch.Tensor:
+    """[s_pad, 256] keys -> K fragments [s_pad/16, 8, 64, 8]: fragment (j, t), lane
+    L = 16*(L/16) + L%16 holds K[16j + L%16][32t + 8(L/16) + 0..7]."""
+    nj = kp.size(0) // 16
+    return kp.view(nj, 16, 8, 4, 8).permute(0, 2, 3, 1, 4).reshape(nj, 8, 64, 8)
+
+
+def _fragments_vt(vp: torch.Tensor) -> torch.Tensor:
+    """[s_pad, 256] values -> V^T fragments [16, s_pad/32, 64, 8]: fragment (db, t), lane L
+    holds V[32t + 8(L/16) + 0..7][16db + L%16]."""
+    nst = vp.size(0) // 32
+    return vp.view(nst, 4, 8, 16, 16).permute(3, 0, 1, 4, 2).reshape(16, nst, 64, 8)
+
+
 @pytest.mark.parametrize("b,s,kvh", [(1, 776, 1), (2, 100, 1), (1, 1, 1), (1, 1024, 1), (1, 64, 2)])
-def test_key_rope_and_value_transpose(ext, cuda, b, s, kvh):
+def test_key_rope_and_mfma_layouts(ext, cuda, b, s, kvh):
     h = 8
     q, k, v, cos, sin = _inputs(b, s, h, kvh, cuda, seed=s + b)
     lib = ext.load_int4_gemm()
     s_pad = (s + 63) // 64 * 64
     k_rope = torch.empty(b, kvh, s, D, dtype=torch.float16, device=cuda)
-    v_t = torch.full((b, kvh, D, s_pad), 7.0, dtype=torch.float16, device=cuda)
-    assert lib.pi05w4a4_attn_vt_elems(b, s, kvh, D) == v_t.numel()
+    kvm = torch.full((b, kvh, 2, s_pad * D), 7.0, dtype=torch.float16, device=cuda)
+    assert lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, D) == kvm.numel()
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     rc = lib.pi05w4a4_attn_kv_prep(
         ctypes.c_void_p(k.data_ptr()), ctypes.c_void_p(v.data_ptr()), kvh * D,
         ctypes.c_void_p(cos.contiguous().data_ptr()), ctypes.c_void_p(sin.contiguous().data_ptr()),
-        b, s, kvh, D, ctypes.c_void_p(k_rope.data_ptr()), ctypes.c_void_p(v_t.data_ptr()), stream)
+        b, s, kvh, D, ctypes.c_void_p(k_rope.data_ptr()), ctypes.c_void_p(kvm.data_ptr()), stream)
     assert rc == 0, lib.pi05w4a4_last_error()
     torch.cuda.synchronize()
     _, k_want = _torch_rope(q, k, cos, sin, h, kvh)
     assert torch.equal(k_rope, k_want.contiguous())
-    v_want = v.view(b, s, kvh, D).permute(0, 2, 3, 1)
-    assert torch.equal(v_t[..., :s], v_want)
-    assert not v_t[..., s:].any()
+    vs = v.view(b, s, kvh, D)
+    for bi in range(b):
+        for g in range(kvh):
+            kp = torch.zeros(s_pad, D, dtype=torch.float16, device=cuda)
+            kp[:s] = k_want[bi, g]
+            vp = torch.zeros(s_pad, D, dtype=torch.float16, device=cuda)
+            vp[:s] = vs[bi, :, g]
+            assert torch.equal(kvm[bi, g, 0].view(s_pad // 16, 8, 64, 8), _fragments_k(kp))
+            assert torch.equal(kvm[bi, g, 1].view(16, s_pad // 32, 64, 8), _fragments_vt(vp))
 
 
 CASES = [

@@ -282,11 +282,11 @@ def test_attention_abi_validation_without_gpu(lib):
         return lib.pi05w4a4_attn_kv_prep(k, p, ld, p, p, b, s, kvh, d, p, p, vp(0))
 
     def attn(b=1, s=776, h=8, kvh=1, d=256, mask=vp(0), mlen=0, mbs=0, mrs=0, ld_q=2048, out=p):
-        return lib.pi05w4a4_prefix_attention(p, ld_q, p, p, p, p, mask, mbs, mrs, mlen, 0.0625,
+        return lib.pi05w4a4_prefix_attention(p, ld_q, p, p, p, mask, mbs, mrs, mlen, 0.0625,
                                              b, s, h, kvh, d, out, 2048, vp(0))
 
-    assert lib.pi05w4a4_attn_vt_elems(1, 776, 1, 256) == 256 * 832  # keys padded to 64
-    assert lib.pi05w4a4_attn_vt_elems(2, 64, 2, 256) == 2 * 2 * 256 * 64
+    assert lib.pi05w4a4_attn_kv_mfma_elems(1, 776, 1, 256) == 2 * 256 * 832  # K, V^T; keys padded to 64
+    assert lib.pi05w4a4_attn_kv_mfma_elems(2, 64, 2, 256) == 2 * 2 * 2 * 256 * 64
     assert prep(d=128) == 1 and "head_dim must be 256" in _err(lib)
     assert prep(s=1025) == 1 and "sequence length" in _err(lib)
     assert prep(s=0) == 1
