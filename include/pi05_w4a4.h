@@ -148,6 +148,32 @@ int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t 
                           void* h_fp16, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * GEMM with a residual add in the epilogue: y = fp16(fp16((acc * sa[m]) * sw[n]) + r[m, n])
+ * for residual r fp16 [M, N] (16-byte aligned; y may alias r).  The second rounding is
+ * that of the decoder's fp16 `residual + hidden_states` (modeling_gemma.py
+ * GemmaDecoderLayer.forward), which it replaces for o_proj and down_proj: the reference
+ * runs int4_gemm (int4_gemm.cu:618-624) and then the add as a separate elementwise op.
+ */
+int pi05w4a4_gemm_residual(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                           const int32_t* w_mfma, int32_t n, const void* residual_fp16,
+                           void* y_fp16, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RMSNorm fused into the K = 2048 activation quant: the codes and scales of
+ * pi05w4a4_quantize applied to h = fp16((x * r) * (unit_offset + w)),
+ * r = 1 / sqrt(sum(x^2) / K + eps), the input norm of every attention and MLP block of
+ * the prefix LM.  Replaces the reference's GemmaRMSNorm (modeling_gemma.py:64-78) plus the
+ * quantize_x of the following int4_gemm3 / int4_gemm2 (int4_gemm.cu:496-531).  The fp32
+ * sum of squares runs per lane over 32 consecutive elements (lane l: elements 32l ..
+ * 32l + 31, in order), then across the 64 lanes by the xor butterfly 32, 16, .., 1; sqrt
+ * and the division are correctly rounded.  h differs from the eager module's output by at
+ * most one fp16 ulp on a few elements (torch sums in another order and uses rsqrt).
+ */
+int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
+                              int32_t unit_offset, int64_t m, int32_t k, int32_t* q, float* sa,
+                              void* stream);
+
+/*
  * Raw int32 accumulators acc[m, n] (row-major [M, N]) for bit-exact checks; no dequant.
  * Debug counterpart of the int32 accumulation inside gemm_iu4 (int4_gemm.cu:114-178).
  */

@@ -20,6 +20,10 @@ Pinning (each function is checked by ``tests/test_oracle.py``):
   * ``int4_gemm_ref`` / ``gemm_acc_int32``  golden vectors + int64 brute force.
   * ``dequant_fp16``        golden vectors through ``int4_gemm_ref``.
   * ``gelu_tanh_up``        float64 closed form of GELU-tanh (tolerance only).
+  * ``rms_norm_lanes``      transformers' GemmaRMSNorm (torch fp32 on the CPU) to one fp16
+                            ulp; constant rows (closed form); the wave-order sum against
+                            float64 (it is a restatement of an fp32 summation order, so
+                            only its order, not its arithmetic, is ours).
 """
 
 from __future__ import annotations
@@ -211,6 +215,35 @@ def gelu_tanh_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
     sequence ``act_fn(gate) * up`` of apply.py:138 rounds (values in float64 math)."""
     g = gelu_tanh(np.asarray(gate, np.float16).astype(np.float64)).astype(np.float16)
     return (g.astype(np.float64) * np.asarray(up, np.float16).astype(np.float64)).astype(np.float16)
+
+
+def rms_norm_lanes(x: np.ndarray, weight: np.ndarray, eps: float, unit_offset: bool = True,
+                   lanes: int = 64) -> np.ndarray:
+    """GemmaRMSNorm (transformers modeling_gemma.py:64-78: fp32 inside, (1 + w), fp16
+    out) in the fp32 summation order of the fused RMSNorm + quant kernel, so that the fp16
+    rows it returns are the ones that kernel rotates and quantizes, bit for bit:
+    lane l sums x^2 over elements l*K/lanes .. (l+1)*K/lanes - 1 in order, the lanes are
+    combined by the butterfly p[l] += p[l ^ o] for o = lanes/2, .., 1, and
+    h = fp16((x * r) * g) with r = 1 / sqrt(ss * (1/K) + eps) (each op one fp32 rounding)
+    and g = 1 + w (unit_offset) or w.  x fp16 [M, K], weight fp16 [K]."""
+    v = np.asarray(x, dtype=np.float16).astype(np.float32)
+    m, k = v.shape
+    r_len = k // lanes
+    sq = v * v
+    part = np.zeros((m, lanes), dtype=np.float32)
+    per_lane = sq.reshape(m, lanes, r_len)
+    for j in range(r_len):
+        part = part + per_lane[:, :, j]
+    idx = np.arange(lanes)
+    o = lanes // 2
+    while o >= 1:
+        part = part + part[:, idx ^ o]
+        o //= 2
+    ss = part[:, 0]
+    r = np.float32(1.0) / np.sqrt(ss * np.float32(1.0 / k) + np.float32(eps))
+    w = np.asarray(weight, dtype=np.float16).astype(np.float32)
+    g = (np.float32(1.0) + w) if unit_offset else w
+    return ((v * r[:, None]) * g[None, :]).astype(np.float16)
 
 
 def rel_l2(a: np.ndarray, b: np.ndarray) -> float:

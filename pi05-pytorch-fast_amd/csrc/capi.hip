@@ -141,7 +141,8 @@ int validate_weight(const int32_t* w, int32_t n, const char* name) {
 
 int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroups,
              const int32_t* const* w, const int32_t* n, void* const* y, int mode,
-             void* workspace, size_t workspace_bytes, hipStream_t stream) {
+             void* workspace, size_t workspace_bytes, hipStream_t stream,
+             const void* residual = nullptr) {
   const bool gelu = mode == w4a4::kEpiGeluUp;
   const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc);
   if (pl.mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
@@ -168,6 +169,7 @@ int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroup
   p.mblocks = static_cast<int32_t>(cdiv(m, 16));
   p.n_total = static_cast<int32_t>(n_total);
   p.gelu_pair_n = gelu ? n[0] : 0;
+  p.res = static_cast<const _Float16*>(residual);
   if (pl.ksplit > 1) {
     const size_t need = static_cast<size_t>(pl.ksplit) * static_cast<size_t>(m) *
                         static_cast<size_t>(n_total) * sizeof(int32_t);
@@ -288,6 +290,39 @@ int pi05w4a4_gemm_multi(const int32_t* q, const float* sa, int64_t m, int32_t k,
   if (m == 0) return ok();
   return run_gemm(q, sa, m, k, ngroups, w_mfma, n, y_fp16, w4a4::kEpiFp16, workspace,
                   workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
+int pi05w4a4_gemm_residual(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                           const int32_t* w_mfma, int32_t n, const void* residual_fp16,
+                           void* y_fp16, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = validate_gemm_common(q, sa, m, k);
+  if (rc) return rc;
+  rc = validate_weight(w_mfma, n, "weight");
+  if (rc) return rc;
+  if (m == 0) return ok();
+  if (y_fp16 == nullptr || residual_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null output or residual");
+  if (!aligned(y_fp16, 16) || !aligned(residual_fp16, 16))
+    return fail(PI05W4A4_EINVAL, "output and residual must be 16-byte aligned");
+  const int32_t* ws[1] = {w_mfma};
+  const int32_t ns[1] = {n};
+  void* ys[1] = {y_fp16};
+  return run_gemm(q, sa, m, k, 1, ws, ns, ys, w4a4::kEpiFp16, workspace, workspace_bytes,
+                  static_cast<hipStream_t>(stream), residual_fp16);
+}
+
+int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
+                              int32_t unit_offset, int64_t m, int32_t k, int32_t* q, float* sa,
+                              void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k != 2048) return fail(PI05W4A4_EINVAL, "the fused RMSNorm quantizer takes K = 2048, got %d", k);
+  if (m == 0) return ok();
+  if (!x_fp16 || !w_fp16 || !q || !sa) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!aligned(x_fp16, 16) || !aligned(w_fp16, 16) || !aligned(q, 16) || !aligned(sa, 4))
+    return fail(PI05W4A4_EINVAL, "x, w and q must be 16-byte aligned, sa 4-byte aligned");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  return hip_status(w4a4::launch_rmsnorm_quantize(x_fp16, w_fp16, eps, unit_offset != 0, m, k, q, sa,
+                                                  static_cast<float>(1.0 / std::sqrt(2048.0)), static_cast<hipStream_t>(stream)),
+                    "rmsnorm quantize launch");
 }
 
 int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t k,

@@ -62,6 +62,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
 // Activation operand bytes: (a[2j] + 8, 16 a[2j+1]) for the 8 codes of word x, then y.
 __device__ __forceinline__ v4i unpack_a(uint32_t x, uint32_t y) {
@@ -383,6 +384,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // Stores address the wave's output block through a scalar base and a 32-bit lane
     // offset (the block spans at most 16*MI rows of N columns).
     char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
+    // Residual (one-group fp16 mode): y = fp16(y + res), the rounding of torch's fp16 add.
+    const char* rw = (!GELU && p.res != nullptr) ? reinterpret_cast<const char*>(p.res + m0 * N + wcol) : nullptr;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
@@ -409,12 +412,19 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         const int rr = j * RPI + lane / LPR;
         const int trow = mi * 16 + rr;  // row within the tile
         const int tcol = (lane % LPR) * 8;
-        const uint4 v = *reinterpret_cast<const uint4*>(stage + min(rr, 15) * LSR + tcol);
+        uint4 v = *reinterpret_cast<const uint4*>(stage + min(rr, 15) * LSR + tcol);
         // Non-temporal: the outputs are not re-read by this kernel, so they should not
         // displace the weights streaming through L2 (measured 1-3% faster).
-        if (rr < 16 && m0 + trow < M && wcol + tcol < N)
+        if (rr < 16 && m0 + trow < M && wcol + tcol < N) {
+          const uint32_t off = static_cast<uint32_t>(trow * N + tcol) * 2u;
+          if (rw != nullptr) {
+            half8 o8 = __builtin_bit_cast(half8, v);
+            o8 += *reinterpret_cast<const half8*>(rw + off);
+            v = __builtin_bit_cast(uint4, o8);
+          }
           __builtin_nontemporal_store(v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)},
-                                      reinterpret_cast<v4i*>(yw + static_cast<uint32_t>(trow * N + tcol) * 2u));
+                                      reinterpret_cast<v4i*>(yw + off));
+        }
       }
       __builtin_amdgcn_wave_barrier();
     }
@@ -508,8 +518,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   const float* sw = reinterpret_cast<const float*>(W + N * scale_off);
   _Float16* y = static_cast<_Float16*>(Y) + row * N + col;
   const int sv[4] = {s.x, s.y, s.z, s.w};
+  const _Float16* res = p.res != nullptr ? p.res + row * N + col : nullptr;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) y[e] = dequant(sv[e], sav, sw[col + e]);
+  for (int e = 0; e < 4; ++e) {
+    const _Float16 o = dequant(sv[e], sav, sw[col + e]);
+    y[e] = res != nullptr ? static_cast<_Float16>(o + res[e]) : o;
+  }
 }
 
 template <int MI, int NI, int NWAVES, int KW, int RING = 2, int WPE = 2>

@@ -36,6 +36,12 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
@@ -241,10 +247,18 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
 // of pass 0 and the per-lane reads of later passes are (nearly) bank-conflict free.
 // ROWS rows per workgroup; with T = 64 every row belongs to one wave and the passes
 // need no workgroup barrier.
-template <int LOGK, int LOGT, int ROWS>
+// NORM: the row is first replaced by its RMSNorm (transformers' GemmaRMSNorm,
+// modeling_gemma.py:64-78, with weight nw and the (1 + w) offset when unit_offset):
+//   h = fp16((x * r) * g),  r = 1 / sqrt(ss / K + eps) (correctly rounded sqrt and
+//   division),  g = unit_offset + w,
+// with ss summed per lane over its R consecutive elements in order, then over the 64
+// lanes by the xor butterfly 32, 16, .., 1 (the oracle restates this order exactly), and
+// the fp16 h is what gets rotated and quantized, as if the norm's output had been stored.
+template <int LOGK, int LOGT, int ROWS, bool NORM = false>
 __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     const _Float16* __restrict__ x, int64_t m, int32_t* __restrict__ q, float* __restrict__ sa,
-    int32_t* __restrict__ qcorr, float inv_sqrt_k) {
+    int32_t* __restrict__ qcorr, float inv_sqrt_k, const _Float16* __restrict__ nw = nullptr,
+    float eps = 0.0f, int unit_offset = 0) {
   constexpr int K = 1 << LOGK;
   constexpr int T = 1 << LOGT;
   constexpr int r = LOGK - LOGT;
@@ -286,6 +300,27 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     const half8 h = *reinterpret_cast<const half8*>(xr + 8 * c);
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
+  }
+  if constexpr (NORM) {
+#pragma clang fp contract(off)
+    static_assert(T == 64, "the fused RMSNorm reduces over one wave");
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < R; ++j) ss = ss + v[j] * v[j];
+    ss = wave_sum_f(ss);
+    const float rr = 1.0f / __builtin_sqrtf(ss * (1.0f / K) + eps);
+    const _Float16* wr = nw + t * R;
+#pragma unroll
+    for (int c = 0; c < R / 8; ++c) {
+      const half8 wv = *reinterpret_cast<const half8*>(wr + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float g = unit_offset ? 1.0f + static_cast<float>(wv[e]) : static_cast<float>(wv[e]);
+        float y = (v[8 * c + e] * rr) * g;
+        asm volatile("" : "+v"(y));  // keep the fp32 product (no v_fma_mix into fp16)
+        v[8 * c + e] = static_cast<float>(static_cast<_Float16>(y));
+      }
+    }
   }
 
 #pragma unroll
@@ -439,6 +474,18 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
       quant_rows_kernel<<<grid, 256, 0, stream>>>(xh, m, k, q, sa, qcorr);
       break;
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int unit_offset,
+                                  int64_t m, int32_t k, int32_t* q, float* sa, float inv_sqrt_k,
+                                  hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  if (k != 2048) return hipErrorInvalidValue;
+  int32_t* qcorr = q + q_payload_words((m + 15) / 16, kblocks128(k));
+  fwht_quant_kernel<11, 6, 4, true><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
+      static_cast<const _Float16*>(x), m, q, sa, qcorr, inv_sqrt_k, static_cast<const _Float16*>(w),
+      eps, unit_offset);
   return hipGetLastError();
 }
 

@@ -41,6 +41,7 @@ struct GemmParams {
   int32_t* partial;   // workspace for kEpiPartial: [ksplit, M, n_total]
   int32_t n_total;
   int32_t gelu_pair_n;  // for kEpiGeluUp: columns of the gate (= up) weight
+  const _Float16* res;  // kEpiFp16, one group: fp16 [M, N] added to the output (or null)
 };
 
 // MFMA-fragment-major layout of packed INT4 codes, shared by the weights (r = output
@@ -137,6 +138,10 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t stream);
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int unit_offset, int64_t m,
                           int32_t k, void* y, hipStream_t stream);
+// RMSNorm fused into the K = 2048 activation quant (hipErrorInvalidValue for other K).
+hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int unit_offset,
+                                  int64_t m, int32_t k, int32_t* q, float* sa, float inv_sqrt_k,
+                                  hipStream_t stream);
 hipError_t launch_attn_kv_prep(const AttnParams& p, hipStream_t stream);
 hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream);
 

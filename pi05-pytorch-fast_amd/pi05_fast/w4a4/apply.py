@@ -148,11 +148,13 @@ def apply_w4a4_from_dir(model: nn.Module, pack_dir: str | Path) -> int:
     from pi05_fast.w4a4.norm import fuse_rmsnorm
 
     n_norm = fuse_rmsnorm(model)
+    n_layer = fuse_decoder_layers(model)
     n_mfma = sum(isinstance(m, W4A4Linear) and m.mfma for m in model.modules())
     n_pre = sum(isinstance(m, W4A4Linear) and m.preshuffled for m in model.modules())
     print(
         f"w4a4: replaced {n} Linear modules from {pack_dir}; "
         f"shared-quant fused {n_fuse} QKV/MLP groups; one-kernel RMSNorm {n_norm}; "
+        f"fused decoder layers {n_layer}; "
         f"MFMA-fragment-major {n_mfma}; WMMA-preshuffled gate/up {n_pre}",
         flush=True,
     )
@@ -192,6 +194,14 @@ def _prefix_attention_fits(self, q: torch.Tensor, k: torch.Tensor, attention_mas
     otherwise), head_dim 256, fp16 on the GPU, at most 1024 tokens, no dropout, logit
     softcap or sliding window, an fp16 [B|1, 1, S, >=S] mask or none, and an empty cache
     (a prefix forward).  ``PI05_W4A4_FUSE_ATTN=0`` keeps transformers' path."""
+    if q.dim() != 3:
+        return False
+    return _attention_call_fits(self, q.shape, int(k.size(-1)), q.dtype, q.is_cuda, attention_mask,
+                                past_key_values)
+
+
+def _attention_call_fits(self, q_shape, k_width: int, dtype, is_cuda: bool, attention_mask,
+                         past_key_values) -> bool:
     if os.environ.get("PI05_W4A4_FUSE_ATTN", "1") == "0":
         return False
     cfg = self.config
@@ -201,10 +211,10 @@ def _prefix_attention_fits(self, q: torch.Tensor, k: torch.Tensor, attention_mas
         return False
     if getattr(cfg, "attn_logit_softcapping", None) or getattr(self, "sliding_window", None):
         return False
-    if self.head_dim != 256 or q.dtype != torch.float16 or not q.is_cuda or q.dim() != 3:
+    if self.head_dim != 256 or dtype != torch.float16 or not is_cuda or len(q_shape) != 3:
         return False
-    b, s = int(q.size(0)), int(q.size(1))
-    if s > 1024 or k.size(-1) % 256 or q.size(-1) % k.size(-1):
+    b, s, q_width = int(q_shape[0]), int(q_shape[1]), int(q_shape[2])
+    if s > 1024 or k_width % 256 or q_width % k_width:
         return False
     if attention_mask is not None:
         m = attention_mask
@@ -279,6 +289,99 @@ def _fused_attn_forward(
     attn_output = attn_output.reshape(*input_shape, -1).contiguous()
     attn_output = self.o_proj(attn_output)
     return attn_output, attn_weights
+
+
+def _norm_parts(norm) -> tuple[torch.Tensor, float, bool] | None:
+    """(fp16 weight, eps, unit_offset) of a Gemma RMSNorm module (transformers'
+    GemmaRMSNorm or norm.FusedRMSNorm), or None."""
+    from pi05_fast.w4a4.norm import FusedRMSNorm
+
+    w = getattr(norm, "weight", None)
+    if not isinstance(w, torch.Tensor) or w.dtype != torch.float16 or not w.is_cuda or w.dim() != 1:
+        return None
+    if isinstance(norm, FusedRMSNorm):
+        return w, norm.eps, norm.unit_offset
+    if type(norm).__name__ == "GemmaRMSNorm":
+        return w, float(norm.eps), True
+    return None
+
+
+def _decoder_layer_fits(layer) -> bool:
+    """A Gemma decoder layer whose seven projections are bias-free MFMA-layout W4A4 layers,
+    whose MLP uses the fused GELU-tanh*up epilogue and whose norms are Gemma RMSNorms over
+    2048 features."""
+    attn, mlp = getattr(layer, "self_attn", None), getattr(layer, "mlp", None)
+    if attn is None or mlp is None or not getattr(mlp, "_w4a4_fuse_gelu", False):
+        return False
+    projs = [getattr(attn, n, None) for n in ("q_proj", "k_proj", "v_proj", "o_proj")]
+    projs += [getattr(mlp, n, None) for n in ("gate_proj", "up_proj", "down_proj")]
+    if not all(isinstance(p, W4A4Linear) and p.mfma and p.bias is None for p in projs):
+        return False
+    norms = [_norm_parts(getattr(layer, n, None)) for n in ("input_layernorm", "post_attention_layernorm")]
+    return all(n is not None and n[0].numel() == 2048 for n in norms) and projs[0].in_features == 2048
+
+
+def _fused_decoder_layer_forward(
+    self,
+    hidden_states: torch.Tensor,
+    attention_mask: torch.Tensor | None = None,
+    position_ids=None,
+    past_key_values=None,
+    use_cache: bool | None = False,
+    position_embeddings: tuple[torch.Tensor, torch.Tensor] | None = None,
+    **kwargs,
+):
+    """GemmaDecoderLayer.forward (modeling_gemma.py) with the edges of the W4A4 ops fused:
+    input_layernorm into the QKV activation quant, RoPE + attention as
+    ``extension.prefix_attention``, the attention residual add into the o_proj epilogue,
+    post_attention_layernorm into the gate/up activation quant (GELU-tanh*up epilogue) and
+    the MLP residual add into the down_proj epilogue.  Calls that do not fit the fused
+    attention run the layer's original forward."""
+    from pi05_fast.w4a4 import extension as ext
+
+    attn, mlp = self.self_attn, self.mlp
+    x = hidden_states
+    if not (
+        x.dtype == torch.float16
+        and x.dim() == 3
+        and x.is_contiguous()
+        and position_embeddings is not None
+        and _attention_call_fits(attn, (x.size(0), x.size(1), attn.q_proj.out_features),
+                                 attn.k_proj.out_features, x.dtype, x.is_cuda, attention_mask, past_key_values)
+    ):
+        return self._w4a4_layer_forward(hidden_states, attention_mask=attention_mask, position_ids=position_ids,
+                                        past_key_values=past_key_values, use_cache=use_cache,
+                                        position_embeddings=position_embeddings, **kwargs)
+    w1, eps1, off1 = _norm_parts(self.input_layernorm)
+    w2, eps2, off2 = _norm_parts(self.post_attention_layernorm)
+    q, k, v = ext.rms_norm_int4_gemm3(x, w1, eps1, attn.q_proj.packed, attn.k_proj.packed, attn.v_proj.packed,
+                                      unit_offset=off1)
+    cos, sin = position_embeddings
+    hd = attn.head_dim
+    out, key_states = ext.prefix_attention(q, k, v, cos, sin, attention_mask, float(attn.scaling),
+                                           q.size(-1) // hd, k.size(-1) // hd)
+    if past_key_values is not None:
+        value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
+        past_key_values.update(key_states, value_states, attn.layer_idx)
+    x2 = ext.int4_gemm_residual(out, attn.o_proj.packed, x)
+    h = ext.rms_norm_int4_gemm2_gelu(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, unit_offset=off2)
+    return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2)
+
+
+def fuse_decoder_layers(model: nn.Module) -> int:
+    """Install ``_fused_decoder_layer_forward`` on every decoder layer that fits
+    (``_decoder_layer_fits``); the original forward stays reachable for calls that do not.
+    ``PI05_W4A4_FUSE_LAYER=0`` keeps the per-module forwards.  Returns the layers fused."""
+    if os.environ.get("PI05_W4A4_FUSE_LAYER", "1") == "0":
+        return 0
+    n = 0
+    for mod in model.modules():
+        if hasattr(mod, "input_layernorm") and hasattr(mod, "self_attn") and _decoder_layer_fits(mod):
+            if not hasattr(mod, "_w4a4_layer_forward"):
+                mod._w4a4_layer_forward = mod.forward
+            mod.forward = types.MethodType(_fused_decoder_layer_forward, mod)
+            n += 1
+    return n
 
 
 def _is_torch_gelu_tanh(act) -> bool:

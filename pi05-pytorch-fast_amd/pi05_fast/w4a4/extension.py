@@ -73,6 +73,8 @@ def load_int4_gemm():
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
+        "pi05w4a4_gemm_residual": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, sz, vp]),
+        "pi05w4a4_rmsnorm_quantize": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
         "pi05w4a4_attn_kv_mfma_elems": (sz, [i64, i32, i32, i32]),
         "pi05w4a4_attn_kv_prep": (ctypes.c_int, [vp, vp, i64, vp, vp, i64, i32, i32, i32, vp, vp, vp]),
         "pi05w4a4_prefix_attention": (
@@ -224,11 +226,24 @@ def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
     return repack_weight(w, k, tiled=False), n
 
 
-def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
-    """Shared-activation GEMMs of 1..3 MFMA-layout weights (one launch)."""
+def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, residual=None):
+    """Shared-activation GEMMs of 1..3 MFMA-layout weights (one launch); with ``residual``
+    (one weight) the epilogue adds it: fp16(fp16(y) + residual)."""
     lib = load_int4_gemm()
     m = int(sa.size(0))
     ns = [int(w.size(0)) for (w, _) in weights]
+    if residual is not None:
+        (w0, n_true), = weights
+        if n_true != ns[0] or tuple(residual.shape) != (*out_shape_prefix, n_true):
+            raise RuntimeError(f"residual must be [{', '.join(map(str, out_shape_prefix))}, {n_true}] "
+                               f"with N a multiple of 16, got {tuple(residual.shape)}")
+        res = residual if residual.is_contiguous() and residual.data_ptr() % 16 == 0 else residual.contiguous().clone()
+        out = torch.empty((m, n_true), dtype=torch.float16, device=device)
+        ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, 1, (ctypes.c_int32 * 1)(n_true), 0)
+        ws = _workspace(device, ws_bytes)
+        _check(lib.pi05w4a4_gemm_residual(_ptr(q), _ptr(sa), m, k, _ptr(w0), n_true, _ptr(res), _ptr(out),
+                                          _ptr(ws), ws_bytes, _stream(device)), "pi05w4a4_gemm_residual")
+        return [out.view(*out_shape_prefix, n_true)]
     if gelu:
         n = ns[0]
         outs = [torch.empty((m, n), dtype=torch.float16, device=device)]
@@ -259,9 +274,34 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False):
     return results
 
 
-def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False):
+def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
+                      unit_offset: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+    """``quantize`` of ``rms_norm(x, weight, eps, unit_offset)`` in one kernel (K = 2048):
+    the norm's fp16 output is rotated and quantized without being stored."""
     k = _check_x(x)
-    q, sa = quantize(x)  # the reference quantizes before checking the weights
+    if k != 2048:
+        raise RuntimeError(f"the fused RMSNorm quantizer takes K = 2048, got {k}")
+    if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 1 or weight.numel() != k:
+        raise RuntimeError(f"RMSNorm weight must be a float16 CUDA/HIP tensor [{k}]")
+    x2 = x.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    w = weight.contiguous()
+    m = x2.numel() // k
+    lib = load_int4_gemm()
+    q = torch.empty((int(lib.pi05w4a4_q_words(m, k)),), dtype=torch.int32, device=x2.device)
+    sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
+    with torch.cuda.device(x2.device):
+        _check(lib.pi05w4a4_rmsnorm_quantize(_ptr(x2), _ptr(w), float(eps), 1 if unit_offset else 0, m, k,
+                                             _ptr(q), _ptr(sa), _stream(x2.device)), "pi05w4a4_rmsnorm_quantize")
+    return q, sa
+
+
+def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False,
+         norm=None, residual=None):
+    k = _check_x(x)
+    # the reference quantizes before checking the weights
+    q, sa = quantize(x) if norm is None else rms_norm_quantize(x, *norm)
     conv = []
     for w in ws:
         _check_packed(w, k)
@@ -269,7 +309,8 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
             _check_tiled(w, k)
         conv.append(_as_mfma(w, k, tiled))
     with torch.cuda.device(x.device):
-        return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), x.device, kind, gelu=gelu)
+        return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), x.device, kind, gelu=gelu,
+                            residual=residual)
 
 
 def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool) -> torch.Tensor:
@@ -438,6 +479,40 @@ def _register_custom_op() -> None:
     def _rms_norm_fake(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool):
         return torch.empty_like(x)
 
+    # Not in the reference: the decoder's RMSNorm fused into the QKV / gate-up activation
+    # quant, and the residual add fused into the o / down GEMM epilogue.
+    @torch.library.custom_op("pi05_w4a4::rms_norm_int4_gemm3", mutates_args=())
+    def _rms_norm_int4_gemm3(
+        x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
+        w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        a, b, c = _run(x, [w0, w1, w2], tiled=False, kind="int4_gemm3", norm=(norm_weight, eps, unit_offset))
+        return a, b, c
+
+    @_rms_norm_int4_gemm3.register_fake
+    def _rms_norm_int4_gemm3_fake(x, norm_weight, eps, unit_offset, w0, w1, w2):
+        return _fake_out(x, w0), _fake_out(x, w1), _fake_out(x, w2)
+
+    @torch.library.custom_op("pi05_w4a4::rms_norm_int4_gemm2_gelu", mutates_args=())
+    def _rms_norm_int4_gemm2_gelu(
+        x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
+        w_gate: torch.Tensor, w_up: torch.Tensor,
+    ) -> torch.Tensor:
+        return _run(x, [w_gate, w_up], tiled=False, kind="int4_gemm2_gelu", gelu=True,
+                    norm=(norm_weight, eps, unit_offset))[0]
+
+    @_rms_norm_int4_gemm2_gelu.register_fake
+    def _rms_norm_int4_gemm2_gelu_fake(x, norm_weight, eps, unit_offset, w_gate, w_up):
+        return _fake_out(x, w_gate)
+
+    @torch.library.custom_op("pi05_w4a4::int4_gemm_residual", mutates_args=())
+    def _int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+        return _run(x, [packed_w], tiled=False, kind="int4_gemm", residual=residual)[0]
+
+    @_int4_gemm_residual.register_fake
+    def _int4_gemm_residual_fake(x, packed_w, residual):
+        return _fake_out(x, packed_w)
+
     # Not in the reference: RoPE + attention between int4_gemm3 and o_proj in two kernels.
     @torch.library.custom_op("pi05_w4a4::prefix_attention", mutates_args=())
     def _prefix_attention(
@@ -511,6 +586,25 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: boo
     (unit_offset + weight)), fp32 inside (transformers GemmaRMSNorm semantics when
     ``unit_offset``)."""
     return torch.ops.pi05_w4a4.rms_norm(x, weight, float(eps), bool(unit_offset))
+
+
+def rms_norm_int4_gemm3(x, norm_weight, eps, w0, w1, w2, unit_offset=True):
+    """int4_gemm3 of rms_norm(x): the decoder's input norm fused into the QKV activation
+    quant (K = 2048)."""
+    return torch.ops.pi05_w4a4.rms_norm_int4_gemm3(x, norm_weight, float(eps), bool(unit_offset), w0, w1, w2)
+
+
+def rms_norm_int4_gemm2_gelu(x, norm_weight, eps, w_gate, w_up, unit_offset=True):
+    """int4_gemm2_gelu of rms_norm(x): the post-attention norm fused into the gate/up
+    activation quant (K = 2048)."""
+    return torch.ops.pi05_w4a4.rms_norm_int4_gemm2_gelu(x, norm_weight, float(eps), bool(unit_offset),
+                                                        w_gate, w_up)
+
+
+def int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+    """residual + int4_gemm(x, packed_w), the add done in the GEMM epilogue with the
+    rounding of the eager fp16 add (MFMA-layout or row-major weights, N % 16 == 0)."""
+    return torch.ops.pi05_w4a4.int4_gemm_residual(x, packed_w, residual)
 
 
 def prefix_attention(

@@ -7,9 +7,11 @@ apply.py:91-213).  LeRobot is not available here, so this module assembles the s
 stack from transformers' Gemma decoder layers: 18 layers, hidden 2048, 8 heads x 256,
 1 KV head, intermediate 16384, RMSNorm (1 + w), RoPE, GELU-tanh, fp16, and installs the
 same hooks (``apply.fuse_shared_activation_quant``); on the GPU the RMSNorms run as one
-kernel each (``norm.fuse_rmsnorm``) and RoPE + attention as the two kernels of
+kernel each (``norm.fuse_rmsnorm``), RoPE + attention as the two kernels of
 ``extension.prefix_attention`` (``PI05_W4A4_FUSE_ATTN=0``: transformers' RoPE and the
-fp16 eager attention below).
+fp16 eager attention below), and each decoder layer runs ``apply.fuse_decoder_layers``'
+forward: norms fused into the activation quants, residual adds into the o/down GEMM
+epilogues (``PI05_W4A4_FUSE_LAYER=0``: the per-module forwards).
 
 Layers are constructed on the meta device (no fp32 weights are ever materialised); the
 seven projections are W4A4Linear modules holding packed weights, the norms are real.
@@ -22,7 +24,7 @@ import math
 import torch
 import torch.nn as nn
 
-from pi05_fast.w4a4.apply import fuse_shared_activation_quant, load_time_weight
+from pi05_fast.w4a4.apply import fuse_decoder_layers, fuse_shared_activation_quant, load_time_weight
 from pi05_fast.w4a4.linear import W4A4Linear
 from pi05_fast.w4a4.norm import fuse_rmsnorm
 
@@ -164,6 +166,7 @@ def build_prefix_lm(
     if fuse:
         fuse_shared_activation_quant(model)
         fuse_rmsnorm(model)
+        fuse_decoder_layers(model)
     return model, weights
 
 

@@ -1,0 +1,97 @@
+"""The fused edges of the W4A4 ops on the GPU (through the C ABI), checked bit for bit
+against the oracle:
+
+- ``pi05w4a4_rmsnorm_quantize``: codes, scales and row corrections equal the oracle's
+  ``quant_activation`` of ``rms_norm_lanes(x)`` (GemmaRMSNorm restated in the kernel's fp32
+  summation order; the fp16 norm output is what gets quantized);
+- ``pi05w4a4_gemm_residual``: y equals fp16(int4_gemm_ref(x, W) + residual), the rounding
+  of the decoder's eager fp16 residual add, also through the split-K path (small M).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w4a4_oracle as orc
+from tests import w4a4_inputs as inp
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ext(cuda):
+    from pi05_fast.w4a4 import extension
+
+    extension.preload()
+    return extension
+
+
+def _codes(q: torch.Tensor, m: int, k: int) -> np.ndarray:
+    from pi05_fast.w4a4.pack import codes_from_fragment_major
+
+    return orc.unpack_nibbles(inp.to_np(codes_from_fragment_major(q.cpu(), m, k)), k)
+
+
+@pytest.mark.parametrize("m,scale,offset", [(776, 1.0, True), (1, 1.0, True), (37, 40.0, True), (64, 0.05, False)])
+def test_rmsnorm_quantize_matches_oracle(ext, cuda, m, scale, offset):
+    k = 2048
+    gen = inp.generator(m)
+    x = (inp.activations(gen, m, k).float() * scale).half()
+    w = (torch.randn(k, generator=gen) * (0.1 if offset else 1.0)).half()
+    q, sa = ext.rms_norm_quantize(x.to(cuda), w.to(cuda), 1e-6, unit_offset=offset)
+    torch.cuda.synchronize()
+    h = orc.rms_norm_lanes(x.numpy(), w.numpy(), 1e-6, unit_offset=offset)
+    q_ref, s_ref = orc.quant_activation(h)
+    got = _codes(q, m, k)
+    nbad = int(np.count_nonzero(got != q_ref))
+    assert nbad == 0, f"{nbad}/{got.size} codes differ"
+    assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32)), "scale bits differ"
+    from pi05_fast.w4a4.pack import qcorr_from_fragment_major
+
+    qc = inp.to_np(qcorr_from_fragment_major(q.cpu(), m, k))
+    assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
+
+
+def test_rmsnorm_quantize_equals_norm_then_quantize_when_norm_matches(ext, cuda):
+    """When the standalone norm kernel's output equals the lane-order restatement (most
+    rows), the fused quant equals quantize(rms_norm(x)) exactly."""
+    m, k = 64, 2048
+    gen = inp.generator(5)
+    x = inp.activations(gen, m, k).to(cuda)
+    w = (torch.randn(k, generator=gen) * 0.1).half().to(cuda)
+    h = ext.rms_norm(x, w, 1e-6)
+    q1, s1 = ext.quantize(h)
+    q2, s2 = ext.rms_norm_quantize(x, w, 1e-6)
+    torch.cuda.synchronize()
+    same_rows = (h.cpu().numpy().view(np.int16) ==
+                 orc.rms_norm_lanes(x.cpu().numpy(), w.cpu().numpy(), 1e-6).view(np.int16)).all(axis=1)
+    assert same_rows.mean() > 0.5
+    c1, c2 = _codes(q1, m, k), _codes(q2, m, k)
+    assert np.array_equal(c1[same_rows], c2[same_rows])
+    assert np.array_equal(inp.to_np(s1)[same_rows].view(np.int32), inp.to_np(s2)[same_rows].view(np.int32))
+
+
+@pytest.mark.parametrize("m,k,n", [(776, 2048, 2048), (776, 16384, 2048), (1, 16384, 2048), (64, 2048, 2048),
+                                   (5, 2048, 256)])
+def test_gemm_residual_matches_oracle(ext, cuda, m, k, n):
+    gen = inp.generator(m + k + n)
+    x = inp.activations(gen, m, k) if k == 2048 else inp.geglu_activations(gen, m, k)
+    w = inp.packed_weight(gen, n, k)
+    res = (torch.randn(m, n, generator=gen) * 2.0).half()
+    w_mfma = ext.repack_weight(w.to(cuda), k=k)
+    y = ext.int4_gemm_residual(x.to(cuda), w_mfma, res.to(cuda))
+    torch.cuda.synchronize()
+    ref = orc.int4_gemm_ref(x.numpy(), w.numpy())
+    want = (ref.astype(np.float32) + res.numpy().astype(np.float32)).astype(np.float16)
+    got = inp.to_np(y)
+    nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
+    assert nbad == 0, f"{nbad}/{got.size} outputs differ"
+
+
+def test_gemm_residual_rejects_bad_residual(ext, cuda):
+    x = torch.zeros(4, 2048, dtype=torch.float16, device=cuda)
+    w = ext.repack_weight(inp.random_packed(inp.generator(1), 256, 2048).to(cuda), k=2048)
+    with pytest.raises(RuntimeError, match="residual must be"):
+        ext.int4_gemm_residual(x, w, torch.zeros(4, 128, dtype=torch.float16, device=cuda))

@@ -11,10 +11,12 @@ shared-quant fused QKV and gate/up forwards, fused GELU*up epilogue), every W4A4
 is recorded with its actual input, and each output must equal the oracle's W4A4 semantics
 (`int4_gemm_ref`: FWHT + INT4 quant, exact integer matmul, `(acc*s_a)*s_w` to fp16) on
 that input bit for bit.  The fused GELU*up output must equal torch's eager
-`gelu(g, approximate="tanh") * u` of the oracle's g and u, bit for bit.  The decoder's
-RMSNorms run as the one-kernel ``pi05_w4a4::rms_norm`` (checked against transformers'
-module in test_gpu_parity.py); RoPE and attention are transformers' modules, which no
-reference test pins (parity unpinned there).
+`gelu(g, approximate="tanh") * u` of the oracle's g and u, bit for bit.  With the fused
+decoder layers (the default) the recorded ops also carry the input norms (the oracle's
+`rms_norm_lanes` of the recorded input is what gets quantized) and the residual adds
+(fp16(y + residual)).  RoPE + attention run as ``prefix_attention``, checked against an
+fp32 reference in test_gpu_attention.py; no reference test pins the decoder around the
+W4A4 ops (parity unpinned there).
 """
 
 from __future__ import annotations
@@ -30,24 +32,27 @@ from oracle import w4a4_oracle as orc
 pytestmark = pytest.mark.gpu
 
 
-def _build(cuda, layers: int, fuse_gelu: bool):
+def _build(cuda, layers: int, fuse_gelu: bool, fuse_layer: bool = True):
     from pi05_fast.w4a4.prefix_lm import build_prefix_lm
 
-    old = os.environ.get("PI05_W4A4_FUSE_GELU")
-    os.environ["PI05_W4A4_FUSE_GELU"] = "1" if fuse_gelu else "0"
+    env = {"PI05_W4A4_FUSE_GELU": "1" if fuse_gelu else "0", "PI05_W4A4_FUSE_LAYER": "1" if fuse_layer else "0"}
+    old = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
     try:
         return build_prefix_lm(cuda, num_layers=layers)
     finally:
-        if old is None:
-            del os.environ["PI05_W4A4_FUSE_GELU"]
-        else:
-            os.environ["PI05_W4A4_FUSE_GELU"] = old
+        for k, v in old.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
 
 
 class _Recorder:
     """Wraps the extension ops (and the name linear.py imported) to record every call."""
 
-    NAMES = ("int4_gemm", "int4_gemm2", "int4_gemm3", "int4_gemm2_gelu")
+    NAMES = ("int4_gemm", "int4_gemm2", "int4_gemm3", "int4_gemm2_gelu", "rms_norm_int4_gemm3",
+             "rms_norm_int4_gemm2_gelu", "int4_gemm_residual")
 
     def __init__(self, monkeypatch):
         from pi05_fast.w4a4 import extension, linear
@@ -61,10 +66,11 @@ class _Recorder:
                 monkeypatch.setattr(linear, name, wrapped)
 
     def _wrap(self, name, fn):
-        def run(x, *ws):
-            out = fn(x, *ws)
+        def run(*args, **kwargs):
+            out = fn(*args, **kwargs)
             outs = out if isinstance(out, tuple) else (out,)
-            self.calls.append((name, x.detach().clone(), [w for w in ws], [o.detach().clone() for o in outs]))
+            keep = [a.detach().clone() if isinstance(a, torch.Tensor) else a for a in args]
+            self.calls.append((name, keep, dict(kwargs), [o.detach().clone() for o in outs]))
             return out
 
         return run
@@ -77,16 +83,46 @@ def _row_major(w: torch.Tensor, k: int) -> np.ndarray:
     return pack.unpack_mfma_weight(w.cpu(), k).numpy()
 
 
-def _oracle(x: torch.Tensor, w: torch.Tensor) -> np.ndarray:
+def _oracle_h(x: np.ndarray, w: torch.Tensor, k: int) -> np.ndarray:
+    """The oracle's W4A4 output for fp16 rows x [M, K] and an MFMA-layout weight."""
+    return orc.int4_gemm_ref(x, _row_major(w, k))
+
+
+def _check_call(cuda, i, call) -> None:
+    """One recorded W4A4 op against the oracle, bit for bit."""
+    name, args, kwargs, outs = call
+    x = args[0]
     k = x.shape[-1]
-    return orc.int4_gemm_ref(x.reshape(-1, k).cpu().numpy(), _row_major(w, k))
+    what = f"call {i} ({name}, K={k})"
+    xn = x.reshape(-1, k).cpu().numpy()
+    if name.startswith("rms_norm_"):
+        norm_w, eps, ws = args[1], args[2], args[3:]
+        xn = orc.rms_norm_lanes(xn, norm_w.cpu().numpy(), eps, unit_offset=kwargs.get("unit_offset", True))
+    elif name == "int4_gemm_residual":
+        ws = args[1:2]
+    else:
+        ws = args[1:]
+    if name.endswith("gelu"):
+        g = torch.from_numpy(_oracle_h(xn, ws[0], k)).to(cuda)
+        u = torch.from_numpy(_oracle_h(xn, ws[1], k)).to(cuda)
+        wants = [(torch.nn.functional.gelu(g, approximate="tanh") * u).cpu().numpy()]
+    else:
+        wants = [_oracle_h(xn, w, k) for w in ws]
+        if name == "int4_gemm_residual":
+            res = args[2].reshape(wants[0].shape).cpu().numpy()
+            wants = [(wants[0].astype(np.float32) + res.astype(np.float32)).astype(np.float16)]
+    for want, o in zip(wants, outs):
+        got = o.reshape(want.shape).cpu().numpy()
+        nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
+        assert nbad == 0, f"{what}: {nbad}/{got.size} fp16 outputs differ from the oracle"
 
 
+@pytest.mark.parametrize("fuse_layer", [True, False])
 @pytest.mark.parametrize("layers,tokens", [(2, 776), (18, 128)])
-def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens):
+def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, fuse_layer):
     from pi05_fast.w4a4.prefix_lm import prefix_inputs
 
-    model, _ = _build(cuda, layers, fuse_gelu=True)
+    model, _ = _build(cuda, layers, fuse_gelu=True, fuse_layer=fuse_layer)
     rec = _Recorder(monkeypatch)
     x = prefix_inputs(1, tokens, cuda)
     mask = torch.zeros(1, 1, tokens, tokens, dtype=torch.float16, device=cuda)
@@ -98,24 +134,17 @@ def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens):
 
     assert isinstance(model.layers[0].input_layernorm, FusedRMSNorm)
     kinds = [c[0] for c in rec.calls]
-    assert kinds.count("int4_gemm3") == layers  # QKV
-    assert kinds.count("int4_gemm2_gelu") == layers  # gate/up + GELU*up
-    assert kinds.count("int4_gemm") == 2 * layers  # o and down
-    for i, (name, xin, ws, outs) in enumerate(rec.calls):
-        what = f"call {i} ({name}, K={xin.shape[-1]})"
-        if name == "int4_gemm2_gelu":
-            g = torch.from_numpy(_oracle(xin, ws[0])).to(cuda)
-            u = torch.from_numpy(_oracle(xin, ws[1])).to(cuda)
-            want = (torch.nn.functional.gelu(g, approximate="tanh") * u).cpu().numpy()
-            got = outs[0].reshape(want.shape).cpu().numpy()
-            nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
-            assert nbad == 0, f"{what}: {nbad}/{got.size} fused GELU*up outputs differ"
-            continue
-        for w, o in zip(ws, outs):
-            want = _oracle(xin, w)
-            got = o.reshape(want.shape).cpu().numpy()
-            nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
-            assert nbad == 0, f"{what}: {nbad}/{got.size} fp16 outputs differ from the oracle"
+    if fuse_layer:
+        assert kinds.count("rms_norm_int4_gemm3") == layers  # input norm + QKV
+        assert kinds.count("rms_norm_int4_gemm2_gelu") == layers  # post norm + gate/up + GELU*up
+        assert kinds.count("int4_gemm_residual") == 2 * layers  # o and down + residual adds
+    else:
+        assert kinds.count("int4_gemm3") == layers  # QKV
+        assert kinds.count("int4_gemm2_gelu") == layers  # gate/up + GELU*up
+        assert kinds.count("int4_gemm") == 2 * layers  # o and down
+    assert len(kinds) == 4 * layers
+    for i, call in enumerate(rec.calls):
+        _check_call(cuda, i, call)
 
 
 def test_prefix_lm_fused_gelu_is_bit_exact(cuda):
@@ -123,8 +152,8 @@ def test_prefix_lm_fused_gelu_is_bit_exact(cuda):
     act_fn(gate) * up between two fp16 GEMM outputs."""
     from pi05_fast.w4a4.prefix_lm import prefix_inputs
 
-    fused, _ = _build(cuda, 2, fuse_gelu=True)
-    eager, _ = _build(cuda, 2, fuse_gelu=False)
+    fused, _ = _build(cuda, 2, fuse_gelu=True, fuse_layer=False)
+    eager, _ = _build(cuda, 2, fuse_gelu=False, fuse_layer=False)
     assert fused.layers[0].mlp._w4a4_fuse_gelu and not eager.layers[0].mlp._w4a4_fuse_gelu
     x = prefix_inputs(1, 776, cuda)
     mask = torch.zeros(1, 1, 776, 776, dtype=torch.float16, device=cuda)

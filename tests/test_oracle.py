@@ -232,3 +232,61 @@ def test_checks_catch_planted_mistakes(golden):
     y_bad = orc.dequant_fp16(orc.gemm_acc_int32(qa, q_w[:, ::-1]), sa, s_w)
     assert np.array_equal(_bits(y), _bits(golden["gemm_y_8x16x2048"]))
     assert not np.array_equal(_bits(y_bad), _bits(golden["gemm_y_8x16x2048"]))
+
+
+# ----------------------------------------------------------------------------- RMSNorm
+def _torch_gemma_rms_norm(x16: np.ndarray, w16: np.ndarray, eps: float) -> np.ndarray:
+    """transformers' GemmaRMSNorm on the CPU (fp32 inside, (1 + w), fp16 out)."""
+    import torch
+    from transformers.models.gemma.modeling_gemma import GemmaRMSNorm
+
+    k = x16.shape[-1]
+    mod = GemmaRMSNorm(k, eps=eps)
+    with torch.no_grad():
+        mod.weight.copy_(torch.from_numpy(w16.astype(np.float32)))
+        return mod(torch.from_numpy(x16)).numpy()  # fp16 in -> fp16 out (type_as)
+
+
+@pytest.mark.parametrize("m,k,scale", [(64, 2048, 1.0), (16, 2048, 30.0), (8, 1024, 0.01)])
+def test_rms_norm_lanes_matches_gemma_module(m, k, scale):
+    """Within one fp16 ulp of transformers' module (only the fp32 summation order and
+    rsqrt vs 1/sqrt differ), on a small fraction of elements."""
+    rng = np.random.default_rng(m + k)
+    x = (rng.standard_normal((m, k)) * scale).astype(np.float16)
+    w = (rng.standard_normal(k) * 0.1).astype(np.float16)
+    got = orc.rms_norm_lanes(x, w, 1e-6)
+    want = _torch_gemma_rms_norm(x, w, 1e-6)
+    ulps = np.abs(got.view(np.int16).astype(np.int32) - want.view(np.int16).astype(np.int32))
+    assert int(ulps.max()) <= 1
+    assert float((ulps > 0).mean()) <= 5e-3
+
+
+def test_rms_norm_lanes_closed_forms():
+    """Rows of one repeated value c: mean(x^2) = c^2 exactly, so h = fp16(c * r * g) with
+    r = 1 / sqrt(c^2 + eps) computed in float64 and rounded like the fp32 steps; zero rows
+    give zeros; the unit offset is (1 + w)."""
+    k = 2048
+    eps = 1e-6
+    for c in (1.0, -2.0, 0.5, 3.0):
+        x = np.full((1, k), c, np.float16)
+        w = np.zeros(k, np.float16)
+        got = orc.rms_norm_lanes(x, w, eps).astype(np.float64)
+        assert np.allclose(got, c / math.sqrt(c * c + eps), rtol=2**-10)
+        w_half = np.full(k, -0.5, np.float16)  # g = 1 + w = 0.5
+        got_half = orc.rms_norm_lanes(x, w_half, eps).astype(np.float64)
+        assert np.allclose(got_half, 0.5 * c / math.sqrt(c * c + eps), rtol=2**-10)
+        got_plain = orc.rms_norm_lanes(x, np.full(k, 2.0, np.float16), eps, unit_offset=False)
+        assert np.allclose(got_plain.astype(np.float64), 2.0 * c / math.sqrt(c * c + eps), rtol=2**-10)
+    assert not orc.rms_norm_lanes(np.zeros((2, k), np.float16), np.ones(k, np.float16), eps).any()
+
+
+def test_rms_norm_lanes_sum_order():
+    """The lane-order sum of squares stays within fp32 summation error of float64 (a
+    dropped lane or a wrong butterfly partner would be off by a whole lane's share)."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((32, 2048)).astype(np.float16)
+    v = x.astype(np.float64)
+    w = np.zeros(2048, np.float16)
+    h = orc.rms_norm_lanes(x, w, 0.0).astype(np.float64)
+    r = 1.0 / np.sqrt((v * v).mean(axis=1))
+    assert np.allclose(h, v * r[:, None], rtol=2**-10, atol=2**-14)
