@@ -71,6 +71,9 @@ def parse_args():
                     help="gate/up as two fp16 outputs + eager gelu*up instead of the fused epilogue")
     ap.add_argument("--only-kernel", default="",
                     help="skip the forward; launch only this kernel class (for rocprofv3 --pmc runs)")
+    ap.add_argument("--forward-only", action="store_true",
+                    help="time the graph-replayed forward only (no per-kernel table, no CPU baseline): "
+                         "for a kernel trace of the real forward")
     return ap.parse_args()
 
 
@@ -138,7 +141,20 @@ class KernelBench:
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
-    def gemm(self, m, k, ns, gelu=False):
+    def rmsnorm_quant(self, m, k=2048):
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16)
+        w = torch.randn(k, device=self.dev, dtype=torch.float16) * 0.1
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        us = self._time(lambda: self._check(lib.pi05w4a4_rmsnorm_quantize(
+            P(x), P(w), 1e-6, 1, m, k, P(q), P(sa), self._stream())))
+        nbytes = 2.0 * m * k + 2 * k + m * k / 2 + 4 * m
+        gbs = nbytes / (us * 1e-6) / 1e9
+        return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
+                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+
+    def gemm(self, m, k, ns, gelu=False, residual=False):
         torch, lib, P = self.torch, self.lib, self.ext._ptr
         gen = torch.Generator(device=self.dev).manual_seed(20260923 + k + sum(ns))
         x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
@@ -155,6 +171,12 @@ class KernelBench:
             fn = lambda: self._check(lib.pi05w4a4_gemm_gelu_up(  # noqa: E731
                 P(q), P(sa), m, k, P(ws[0]), P(ws[1]), ns[0], P(out), P(work), wsb, self._stream()))
             out_bytes = 2.0 * m * ns[0]
+        elif residual:
+            res = torch.randn(m, ns[0], device=self.dev, dtype=torch.float16)
+            out = torch.empty(m, ns[0], dtype=torch.float16, device=self.dev)
+            fn = lambda: self._check(lib.pi05w4a4_gemm_residual(  # noqa: E731
+                P(q), P(sa), m, k, P(ws[0]), ns[0], P(res), P(out), P(work), wsb, self._stream()))
+            out_bytes = 4.0 * m * ns[0]
         else:
             outs = [torch.empty(m, n, dtype=torch.float16, device=self.dev) for n in ns]
             w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for w in ws])
@@ -233,6 +255,9 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "gate_up": lambda: kb.gemm(m, h, [inter, inter]),
         "gate_up_gelu": lambda: kb.gemm(m, h, [inter, inter], gelu=True),
         "down": lambda: kb.gemm(m, inter, [h]),
+        "o_residual": lambda: kb.gemm(m, h, [2048], residual=True),
+        "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
+        "rmsnorm_quant_k2048": lambda: kb.rmsnorm_quant(m),
     }
     if only == "copy":  # calibration for the HBM traffic counters: a plain 64 MiB copy
         src = kb.torch.empty(64 << 20, dtype=kb.torch.uint8, device=kb.dev).fill_(1)
@@ -407,6 +432,10 @@ def main() -> int:
         torch.cuda.synchronize()
         ms = (time.perf_counter() - t0) * 1e3 / args.steps
         del graph
+        if args.forward_only:
+            print(json.dumps({"forward_only": True, "ms_per_forward": round(ms, 4), "steps": args.steps,
+                              "graph_replay_bit_exact_vs_eager": graph_exact}), flush=True)
+            return 0
 
         kernels = kernel_table(kb, m)
         others = kb.attention(args.batch, args.tokens)
@@ -414,8 +443,13 @@ def main() -> int:
 
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
-    calls = {"quant_k2048": 3, "quant_k16384": 1, "qkv": 1, "o": 1, "down": 1,
-             "gate_up": 1 if args.unfused_gelu else 0, "gate_up_gelu": 0 if args.unfused_gelu else 1}
+    # The kernels one decoder layer launches (fused layer: RMSNorm in the QKV and gate/up
+    # quants, residual adds in the o and down epilogues).
+    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 1, "quant_k16384": 1, "qkv": 1, "o_residual": 1,
+             "down_residual": 1, "gate_up_gelu": 1, "gate_up": 0, "o": 0, "down": 0}
+    if args.unfused_gelu:
+        calls.update({"rmsnorm_quant_k2048": 0, "quant_k2048": 3, "o_residual": 0, "down_residual": 0,
+                      "gate_up_gelu": 0, "gate_up": 1, "o": 1, "down": 1})
     for name, c in calls.items():
         kernels[name]["calls_per_layer"] = c
     w4a4_us_per_layer = sum(kernels[n]["avg_us"] * c for n, c in calls.items())

@@ -326,6 +326,30 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   if (tid < NCOL) epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
   if constexpr (KW == 1) __syncthreads();  // KW > 1: the fold below synchronises
 
+  // Residual (fp16 mode, one group): the 16-byte row pieces this wave's epilogue stores
+  // (see the store loop below) are loaded now, so that their latency hides under the k
+  // fold and the staging instead of stalling every store.  Addresses are clamped into the
+  // matrix; pieces outside it are never stored.
+  constexpr int ROCW = 16 * NI;
+  constexpr int RLPR = ROCW / 8;
+  constexpr int RRPI = 64 / RLPR;
+  constexpr int RJ = (16 + RRPI - 1) / RRPI;
+  uint4 resv[GELU ? 1 : MI][GELU ? 1 : RJ];
+  const bool has_res = !GELU && p.res != nullptr && p.mode == kEpiFp16;
+  if constexpr (!GELU) {
+    if (has_res && wk == 0) {
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int j = 0; j < RJ; ++j) {
+          const int rr = min(j * RRPI + lane / RLPR, 15);
+          const int64_t row = min(m0 + mi * 16 + rr, M - 1);
+          const int col = min(wcol + (lane % RLPR) * 8, N - 8);
+          resv[mi][j] = *reinterpret_cast<const uint4*>(p.res + row * N + col);
+        }
+    }
+  }
+
   // ---- k-part reduction through LDS (KW > 1): pairs of k parts are folded until part 0
   // of every column block holds the full sum; the other waves are done after that.
   if constexpr (KW > 1) {
@@ -385,7 +409,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // offset (the block spans at most 16*MI rows of N columns).
     char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
     // Residual (one-group fp16 mode): y = fp16(y + res), the rounding of torch's fp16 add.
-    const char* rw = (!GELU && p.res != nullptr) ? reinterpret_cast<const char*>(p.res + m0 * N + wcol) : nullptr;
+    static_assert(GELU || (LPR == RLPR && RPI == RRPI), "residual pieces follow the store layout");
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
 #pragma unroll
@@ -417,10 +441,12 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         // displace the weights streaming through L2 (measured 1-3% faster).
         if (rr < 16 && m0 + trow < M && wcol + tcol < N) {
           const uint32_t off = static_cast<uint32_t>(trow * N + tcol) * 2u;
-          if (rw != nullptr) {
-            half8 o8 = __builtin_bit_cast(half8, v);
-            o8 += *reinterpret_cast<const half8*>(rw + off);
-            v = __builtin_bit_cast(uint4, o8);
+          if constexpr (!GELU) {
+            if (has_res) {
+              half8 o8 = __builtin_bit_cast(half8, v);
+              o8 += __builtin_bit_cast(half8, resv[mi][j]);
+              v = __builtin_bit_cast(uint4, o8);
+            }
           }
           __builtin_nontemporal_store(v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)},
                                       reinterpret_cast<v4i*>(yw + off));
