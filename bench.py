@@ -214,7 +214,7 @@ class KernelBench:
             P(k), P(v), kvh * d, P(cos), P(sin), b, s, kvh, d, P(k_rope), P(kvm), self._stream()))
         attn = lambda: self._check(lib.pi05w4a4_prefix_attention(  # noqa: E731
             P(q), h * d, P(kvm), P(cos), P(sin), P(mask), s * s4, s4, s4, d**-0.5,
-            b, s, h, kvh, d, P(out), h * d, self._stream()))
+            b, s, h, kvh, d, P(out), h * d, None, None, self._stream()))
         prep()
         us_prep = self._time(prep)
         us_attn = self._time(attn)
@@ -443,9 +443,10 @@ def main() -> int:
 
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
-    # The kernels one decoder layer launches (fused layer: RMSNorm in the QKV and gate/up
-    # quants, residual adds in the o and down epilogues).
-    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 1, "quant_k16384": 1, "qkv": 1, "o_residual": 1,
+    # The W4A4 kernels one decoder layer launches (fused layer: RMSNorm in the QKV and
+    # gate/up quants, the o-proj quant inside the attention kernel, residual adds in the o
+    # and down epilogues).
+    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 0, "quant_k16384": 1, "qkv": 1, "o_residual": 1,
              "down_residual": 1, "gate_up_gelu": 1, "gate_up": 0, "o": 0, "down": 0}
     if args.unfused_gelu:
         calls.update({"rmsnorm_quant_k2048": 0, "quant_k2048": 3, "o_residual": 0, "down_residual": 0,

@@ -226,7 +226,11 @@ int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t 
  * optional additive fp16 mask (element (b, sq, sk) at mask[b*mask_bs + sq*mask_rs + sk];
  * mask_bs = 0 broadcasts one mask; mask_len >= S keys per row, a multiple of 4, strides
  * multiples of 4, 8-byte aligned; null for none) and `scaling` ->
- *   out fp16 [B, S, H, 256] with token stride ld_out (multiple of 4).
+ *   out fp16 [B, S, H, 256] with token stride ld_out (multiple of 4), or null, and
+ *   with KVH == 1 and H == 8 optionally q_codes / q_scales: the o-proj input's K = 2048
+ *   activation quant of the output rows (M = B * S, pi05w4a4_q_words(M, 2048) words and M
+ *   scales, exactly what pi05w4a4_quantize writes for them), which replaces the
+ *   quantize_x of the following int4_gemm (int4_gemm.cu:496-531); null for none.
  * All other pointers 16-byte aligned (out 8-byte).
  */
 size_t pi05w4a4_attn_kv_mfma_elems(int64_t b, int32_t s, int32_t kvh, int32_t d);
@@ -237,7 +241,7 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               const void* cos_fp16, const void* sin_fp16, const void* mask,
                               int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
                               int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
-                              int64_t ld_out, void* stream);
+                              int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream);
 
 #ifdef __cplusplus
 }

@@ -42,7 +42,7 @@
 // memory path, about 64 B per clock, ~13k clocks at 776 keys; the softmax is VALU work
 // (a wave64 VALU instruction occupies its SIMD for 4 clocks).
 
-#include "w4a4_internal.h"
+#include "quant_row.h"
 
 namespace w4a4 {
 namespace {
@@ -56,6 +56,8 @@ constexpr int kRows = 32;           // query rows per workgroup
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQld = kD + 8;        // LDS row stride of the query tile (halves)
+constexpr int kOld = 2048 + 8;      // LDS row stride of the output rows quantized in phase 4
+constexpr int kQRow = 2048 + 4 * (2048 / 32);  // FWHT scratch floats per quantized row
 
 __device__ __forceinline__ half8 ld8(const _Float16* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ __forceinline__ void st8(_Float16* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
@@ -344,17 +346,53 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     }
   }
 
+  if (p.out != nullptr) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int rr = row0 + 16 * qb + lr;
-    if (rr >= rows) continue;
-    _Float16* orow = p.out + (b * S + rr / n_rep) * p.ld_out + (g * n_rep + rr % n_rep) * kD + 32 * w + 4 * lg;
+    for (int qb = 0; qb < 2; ++qb) {
+      const int rr = row0 + 16 * qb + lr;
+      if (rr >= rows) continue;
+      _Float16* orow = p.out + (b * S + rr / n_rep) * p.ld_out + (g * n_rep + rr % n_rep) * kD + 32 * w + 4 * lg;
 #pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      half4 v;
+      for (int db = 0; db < 2; ++db) {
+        half4 v;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(o[db][qb][i]);
-      *reinterpret_cast<half4*>(orow + 16 * db) = v;
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(o[db][qb][i]);
+        *reinterpret_cast<half4*>(orow + 16 * db) = v;
+      }
+    }
+  }
+
+  // ---- phase 4 (one KV head of 8 query heads): the workgroup's 32 rows are 4 whole
+  // tokens of the o-proj input (8 heads x 256 = 2048), so it quantizes them itself, as the
+  // K = 2048 activation quant would: the fp16 rows are staged in LDS over the
+  // probabilities and waves 0-3 each rotate and quantize one token (fwht_quant_row).
+  if (p.qcodes != nullptr) {
+    __syncthreads();  // every wave is done reading P
+    _Float16* otile = sc;                                   // [4][kOld] fp16
+    float* scratch = reinterpret_cast<float*>(sc + 4 * kOld);  // [4][kQRow] fp32
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      const int r = 16 * qb + lr;  // n_rep == 8: token r / 8, head r % 8
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        half4 v;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = static_cast<_Float16>(o[db][qb][i]);
+        *reinterpret_cast<half4*>(otile + (r >> 3) * kOld + (r & 7) * kD + 32 * w + 16 * db + 4 * lg) = v;
+      }
+    }
+    __syncthreads();
+    const int tok = (row0 >> 3) + w;
+    if (w < 4 && tok < S) {
+      float v[32];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const half8 h = ld8(otile + w * kOld + 32 * lane + 8 * c);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
+      }
+      fwht_quant_row<11, 6>(v, scratch + w * kQRow, nullptr, nullptr, lane, b * S + tok, p.qcodes, p.qscales,
+                            p.qcorr, p.inv_sqrt_k);
     }
   }
 }
@@ -374,7 +412,12 @@ hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(p.s) * (p.h / p.kvh);
   const dim3 grid(static_cast<unsigned>((rows + kRows - 1) / kRows), static_cast<unsigned>(p.kvh),
                   static_cast<unsigned>(p.b));
-  const size_t lds = static_cast<size_t>(kRows) * (kQld + p.s_pad + 8) * sizeof(_Float16);
+  size_t sc_bytes = static_cast<size_t>(kRows) * (p.s_pad + 8) * sizeof(_Float16);
+  if (p.qcodes != nullptr) {
+    const size_t q_bytes = 4 * kOld * sizeof(_Float16) + 4 * kQRow * sizeof(float);
+    if (q_bytes > sc_bytes) sc_bytes = q_bytes;
+  }
+  const size_t lds = static_cast<size_t>(kRows) * kQld * sizeof(_Float16) + sc_bytes;
   if (p.s_pad <= 256)
     prefix_attention_kernel<2><<<grid, kThreads, lds, stream>>>(p);
   else if (p.s_pad <= 512)

@@ -415,18 +415,25 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               const void* cos_fp16, const void* sin_fp16, const void* mask,
                               int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
                               int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
-                              int64_t ld_out, void* stream) {
+                              int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream) {
   int rc = validate_attention(b, s, h, kvh, d);
   if (rc) return rc;
-  if (!q || !kv_mfma || !cos_fp16 || !sin_fp16 || !out) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!q || !kv_mfma || !cos_fp16 || !sin_fp16 || (!out && !q_codes))
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (q_codes != nullptr) {
+    if (kvh != 1 || h * d != 2048)
+      return fail(PI05W4A4_EINVAL, "the fused output quant takes one KV head and H * head_dim = 2048");
+    if (!q_scales || !aligned(q_codes, 16) || !aligned(q_scales, 4))
+      return fail(PI05W4A4_EINVAL, "q_codes must be 16-byte aligned and q_scales non-null");
+  }
   if (ld_q < static_cast<int64_t>(h) * d || ld_q % 8 != 0)
     return fail(PI05W4A4_EINVAL, "query token stride must be a multiple of 8 and >= H*head_dim, got %lld",
                 (long long)ld_q);
-  if (ld_out < static_cast<int64_t>(h) * d || ld_out % 4 != 0)
+  if (out != nullptr && (ld_out < static_cast<int64_t>(h) * d || ld_out % 4 != 0))
     return fail(PI05W4A4_EINVAL, "output token stride must be a multiple of 4 and >= H*head_dim, got %lld",
                 (long long)ld_out);
   if (!aligned(q, 16) || !aligned(kv_mfma, 16) || !aligned(cos_fp16, 16) ||
-      !aligned(sin_fp16, 16) || !aligned(out, 8))
+      !aligned(sin_fp16, 16) || (out != nullptr && !aligned(out, 8)))
     return fail(PI05W4A4_EINVAL, "q, kv_mfma, cos and sin must be 16-byte aligned, out 8-byte aligned");
   if (mask != nullptr) {
     if (mask_len < s || mask_len % 4 != 0)
@@ -453,6 +460,13 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
   p.kv_mfma = const_cast<_Float16*>(static_cast<const _Float16*>(kv_mfma));
   p.out = static_cast<_Float16*>(out);
   p.ld_out = ld_out;
+  if (q_codes != nullptr) {
+    const int64_t rows = b * s;
+    p.qcodes = q_codes;
+    p.qscales = q_scales;
+    p.qcorr = q_codes + w4a4::q_payload_words((rows + 15) / 16, w4a4::kblocks128(2048));
+    p.inv_sqrt_k = static_cast<float>(1.0 / std::sqrt(2048.0));
+  }
   return hip_status(w4a4::launch_prefix_attention(p, static_cast<hipStream_t>(stream)), "prefix attention launch");
 }
 

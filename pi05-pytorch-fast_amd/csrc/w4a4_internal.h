@@ -123,8 +123,12 @@ struct AttnParams {
   int32_t s_pad;          // keys rounded up to a multiple of 64
   _Float16* k_rope;       // [B, KVH, S, 256] with RoPE
   _Float16* kv_mfma;      // per (b, KV head): K then V^T in MFMA-fragment-major order
-  _Float16* out;          // [B, S, H, 256], token stride ld_out
+  _Float16* out;          // [B, S, H, 256], token stride ld_out (or null)
   int64_t ld_out;
+  int32_t* qcodes;        // KVH == 1, H == 8: the output rows' K = 2048 quant (or null):
+  float* qscales;         //   codes, scales and row corrections as pi05w4a4_quantize writes
+  int32_t* qcorr;         //   them for M = B * S rows
+  float inv_sqrt_k;
 };
 int64_t attn_s_pad(int32_t s);
 

@@ -332,8 +332,9 @@ def _fused_decoder_layer_forward(
     **kwargs,
 ):
     """GemmaDecoderLayer.forward (modeling_gemma.py) with the edges of the W4A4 ops fused:
-    input_layernorm into the QKV activation quant, RoPE + attention as
-    ``extension.prefix_attention``, the attention residual add into the o_proj epilogue,
+    input_layernorm into the QKV activation quant, RoPE + attention + o_proj as
+    ``extension.prefix_attention_o_proj`` (the o-proj activation quant inside the attention
+    kernel, the attention residual add in the o_proj epilogue),
     post_attention_layernorm into the gate/up activation quant (GELU-tanh*up epilogue) and
     the MLP residual add into the down_proj epilogue.  Calls that do not fit the fused
     attention run the layer's original forward."""
@@ -358,12 +359,11 @@ def _fused_decoder_layer_forward(
                                       unit_offset=off1)
     cos, sin = position_embeddings
     hd = attn.head_dim
-    out, key_states = ext.prefix_attention(q, k, v, cos, sin, attention_mask, float(attn.scaling),
-                                           q.size(-1) // hd, k.size(-1) // hd)
+    x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
+                                                    q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x)
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)
-    x2 = ext.int4_gemm_residual(out, attn.o_proj.packed, x)
     h = ext.rms_norm_int4_gemm2_gelu(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, unit_offset=off2)
     return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2)
 

@@ -79,7 +79,7 @@ def load_int4_gemm():
         "pi05w4a4_attn_kv_prep": (ctypes.c_int, [vp, vp, i64, vp, vp, i64, i32, i32, i32, vp, vp, vp]),
         "pi05w4a4_prefix_attention": (
             ctypes.c_int,
-            [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp],
+            [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp, vp, vp],
         ),
     }
     for name, (res, args) in sig.items():
@@ -364,7 +364,10 @@ def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int):
 def _prefix_attention_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
-) -> tuple[torch.Tensor, torch.Tensor]:
+    quantize_out: bool = False,
+):
+    """(out, key states) or, with ``quantize_out`` (one KV head, 8 query heads), (out, key
+    states, q codes, scales) of the output rows' K = 2048 activation quant."""
     d = ATTN_HEAD_DIM
     for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if not t.is_cuda:
@@ -385,14 +388,39 @@ def _prefix_attention_impl(
     k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
     kv_mfma = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
     out = torch.empty((b, s, h * d), dtype=torch.float16, device=q.device)
+    codes = scales = None
+    if quantize_out:
+        codes = torch.empty((int(lib.pi05w4a4_q_words(b * s, h * d)),), dtype=torch.int32, device=q.device)
+        scales = torch.empty((b * s,), dtype=torch.float32, device=q.device)
     with torch.cuda.device(q.device):
         st = _stream(q.device)
         _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
                                          _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
         _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
                                              _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
-                                             _ptr(out), h * d, st), "pi05w4a4_prefix_attention")
+                                             _ptr(out), h * d, _ptr(codes), _ptr(scales), st),
+               "pi05w4a4_prefix_attention")
+    if quantize_out:
+        return out, k_rope, codes, scales
     return out, k_rope
+
+
+def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+    """RoPE + attention + o_proj + residual add: with one KV head and 8 query heads of 256
+    the attention kernel quantizes its own output rows for the o GEMM; otherwise the output
+    goes through the separate quantizer.  Returns (residual + o_proj(out), key states, out)."""
+    k_in = ATTN_HEAD_DIM * int(num_heads)
+    _check_packed(w_o, k_in, "o_proj weight")
+    w, n_true = _as_mfma(w_o, k_in, tiled=False)
+    lead = tuple(q.shape[:-1])
+    if int(num_kv_heads) == 1 and k_in == 2048:
+        out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
+                                                            num_kv_heads, quantize_out=True)
+        with torch.cuda.device(q.device):
+            y = _gemm_from_q(codes, scales, k_in, [(w, n_true)], lead, q.device, "int4_gemm", residual=residual)[0]
+        return y, k_rope, out
+    out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads)
+    return _run(out, [w_o], tiled=False, kind="int4_gemm", residual=residual)[0], k_rope, out
 
 
 # ----------------------------------------------------------------------------- custom ops
@@ -401,7 +429,7 @@ def _register_custom_op() -> None:
     if _op_registered:
         return
     try:
-        torch.ops.pi05_w4a4.prefix_attention
+        torch.ops.pi05_w4a4.prefix_attention_o_proj
         _op_registered = True
         return
     except (AttributeError, RuntimeError):
@@ -527,6 +555,21 @@ def _register_custom_op() -> None:
         out = q.new_empty((b, s, num_heads * ATTN_HEAD_DIM))
         return out, q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM))
 
+    @torch.library.custom_op("pi05_w4a4::prefix_attention_o_proj", mutates_args=())
+    def _prefix_attention_o_proj(
+        q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+        mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
+        w_o: torch.Tensor, residual: torch.Tensor,
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        return _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o,
+                                             residual)
+
+    @_prefix_attention_o_proj.register_fake
+    def _prefix_attention_o_proj_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+        b, s = q.shape[0], q.shape[1]
+        return (q.new_empty((b, s, w_o.shape[0])), q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM)),
+                q.new_empty((b, s, num_heads * ATTN_HEAD_DIM)))
+
     _op_registered = True
 
 
@@ -620,6 +663,15 @@ def prefix_attention(
     key states bit-identical to the eager ones."""
     return torch.ops.pi05_w4a4.prefix_attention(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
                                                 int(num_kv_heads))
+
+
+def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+    """residual + o_proj(attention(q, k, v)) of a prefix forward, plus the RoPE'd key
+    states and the attention output: ``prefix_attention`` followed by
+    ``int4_gemm_residual``, with the o-proj activation quant done inside the attention
+    kernel when the layer has one KV head and 8 query heads of 256 (PaliGemma)."""
+    return torch.ops.pi05_w4a4.prefix_attention_o_proj(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
+                                                       int(num_kv_heads), w_o, residual)
 
 
 def preload() -> None:

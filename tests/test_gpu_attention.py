@@ -14,6 +14,7 @@ from __future__ import annotations
 
 import ctypes
 
+import numpy as np
 import pytest
 import torch
 
@@ -258,3 +259,56 @@ def test_decoder_attention_uses_kernel_and_fills_cache(ext, cuda, monkeypatch):
     assert torch.equal(kf, ke) and torch.equal(vf, ve)
     o_fused, o_eager = seen["o_in"][0], seen["o_in"][1]
     assert _rel_l2(o_fused, o_eager) <= REL_L2
+
+
+@pytest.mark.parametrize("b,s,kind", [(1, 776, "zeros"), (2, 77, "padding"), (1, 5, None)])
+def test_attention_output_quant_matches_oracle(ext, cuda, b, s, kind):
+    """With one KV head and 8 query heads the attention kernel quantizes its own output
+    rows for the o projection: codes, scale bits and row corrections equal the oracle's
+    K = 2048 activation quant of the fp16 output it also returns."""
+    from oracle import w4a4_oracle as orc
+    from pi05_fast.w4a4.pack import codes_from_fragment_major, qcorr_from_fragment_major
+
+    h, kvh = 8, 1
+    q, k, v, cos, sin = _inputs(b, s, h, kvh, cuda, seed=77 + s)
+    mask = None if kind is None else (torch.zeros(b, 1, s, s, dtype=torch.float16, device=cuda) if kind == "zeros"
+                                      else _padding_causal_mask(b, s, [max(1, s - 9 * i) for i in range(b)], cuda))
+    with torch.no_grad():
+        out, _, codes, scales = ext._prefix_attention_impl(q, k, v, cos, sin, mask, D**-0.5, h, kvh,
+                                                           quantize_out=True)
+    torch.cuda.synchronize()
+    m = b * s
+    q_ref, s_ref = orc.quant_activation(out.reshape(m, 2048).cpu().numpy())
+    got = orc.unpack_nibbles(codes_from_fragment_major(codes.cpu(), m, 2048).numpy(), 2048)
+    assert int(np.count_nonzero(got != q_ref)) == 0
+    assert np.array_equal(scales.cpu().numpy().view(np.int32), s_ref.view(np.int32))
+    qc = qcorr_from_fragment_major(codes.cpu(), m, 2048).numpy()
+    assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
+
+
+@pytest.mark.parametrize("b,s,h,kvh", [(1, 776, 8, 1), (2, 100, 8, 1), (1, 64, 4, 2)])
+def test_prefix_attention_o_proj_matches_oracle(ext, cuda, b, s, h, kvh):
+    """residual + o_proj(attention): the fp16 result equals the oracle's W4A4 o projection of
+    the returned attention output plus the residual, bit for bit, through the fused quant
+    (one KV head, 8 heads) and through the separate quantizer (other head counts)."""
+    from oracle import w4a4_oracle as orc
+    from tests import w4a4_inputs as inp
+
+    q, k, v, cos, sin = _inputs(b, s, h, kvh, cuda, seed=300 + s)
+    mask = _padding_causal_mask(b, s, [max(1, s - 13 * i) for i in range(b)], cuda)
+    gen = inp.generator(h * D + s)
+    w_o = inp.packed_weight(gen, 2048, h * D)
+    res = (torch.randn(b, s, 2048, generator=gen) * 2.0).half().to(cuda)
+    w_mfma = ext.repack_weight(w_o.to(cuda), k=h * D)
+    with torch.no_grad():
+        x2, key_states, out = ext.prefix_attention_o_proj(q, k, v, cos, sin, mask, D**-0.5, h, kvh, w_mfma, res)
+        want_attn = _reference(q, k, v, cos, sin, mask, D**-0.5, h, kvh)
+    torch.cuda.synchronize()
+    assert _rel_l2(out, want_attn) <= REL_L2
+    _, k_want = _torch_rope(q, k, cos, sin, h, kvh)
+    assert torch.equal(key_states, k_want.contiguous())
+    ref = orc.int4_gemm_ref(out.reshape(b * s, h * D).cpu().numpy(), w_o.numpy())
+    want = (ref.astype(np.float32) + res.reshape(b * s, 2048).cpu().numpy().astype(np.float32)).astype(np.float16)
+    got = x2.reshape(b * s, 2048).cpu().numpy()
+    nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
+    assert nbad == 0, f"{nbad}/{got.size} outputs differ"

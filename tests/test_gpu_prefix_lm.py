@@ -52,7 +52,7 @@ class _Recorder:
     """Wraps the extension ops (and the name linear.py imported) to record every call."""
 
     NAMES = ("int4_gemm", "int4_gemm2", "int4_gemm3", "int4_gemm2_gelu", "rms_norm_int4_gemm3",
-             "rms_norm_int4_gemm2_gelu", "int4_gemm_residual")
+             "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj")
 
     def __init__(self, monkeypatch):
         from pi05_fast.w4a4 import extension, linear
@@ -91,6 +91,17 @@ def _oracle_h(x: np.ndarray, w: torch.Tensor, k: int) -> np.ndarray:
 def _check_call(cuda, i, call) -> None:
     """One recorded W4A4 op against the oracle, bit for bit."""
     name, args, kwargs, outs = call
+    if name == "prefix_attention_o_proj":
+        # the o projection of the attention output it returned (quantized inside the kernel)
+        w_o, res = args[9], args[10]
+        x2, out = outs[0], outs[2]
+        k = out.shape[-1]
+        want = _oracle_h(out.reshape(-1, k).cpu().numpy(), w_o, k)
+        want = (want.astype(np.float32) + res.reshape(want.shape).cpu().numpy().astype(np.float32)).astype(np.float16)
+        got = x2.reshape(want.shape).cpu().numpy()
+        nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
+        assert nbad == 0, f"call {i} ({name}): {nbad}/{got.size} fp16 outputs differ from the oracle"
+        return
     x = args[0]
     k = x.shape[-1]
     what = f"call {i} ({name}, K={k})"
@@ -137,7 +148,8 @@ def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, f
     if fuse_layer:
         assert kinds.count("rms_norm_int4_gemm3") == layers  # input norm + QKV
         assert kinds.count("rms_norm_int4_gemm2_gelu") == layers  # post norm + gate/up + GELU*up
-        assert kinds.count("int4_gemm_residual") == 2 * layers  # o and down + residual adds
+        assert kinds.count("prefix_attention_o_proj") == layers  # attention, o + residual add
+        assert kinds.count("int4_gemm_residual") == layers  # down + residual add
     else:
         assert kinds.count("int4_gemm3") == layers  # QKV
         assert kinds.count("int4_gemm2_gelu") == layers  # gate/up + GELU*up

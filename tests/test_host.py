@@ -281,9 +281,9 @@ def test_attention_abi_validation_without_gpu(lib):
     def prep(b=1, s=776, kvh=1, d=256, ld=256, k=p):
         return lib.pi05w4a4_attn_kv_prep(k, p, ld, p, p, b, s, kvh, d, p, p, vp(0))
 
-    def attn(b=1, s=776, h=8, kvh=1, d=256, mask=vp(0), mlen=0, mbs=0, mrs=0, ld_q=2048, out=p):
+    def attn(b=1, s=776, h=8, kvh=1, d=256, mask=vp(0), mlen=0, mbs=0, mrs=0, ld_q=2048, out=p, qc=vp(0)):
         return lib.pi05w4a4_prefix_attention(p, ld_q, p, p, p, mask, mbs, mrs, mlen, 0.0625,
-                                             b, s, h, kvh, d, out, 2048, vp(0))
+                                             b, s, h, kvh, d, out, 2048, qc, vp(0), vp(0))
 
     assert lib.pi05w4a4_attn_kv_mfma_elems(1, 776, 1, 256) == 2 * 256 * 832  # K, V^T; keys padded to 64
     assert lib.pi05w4a4_attn_kv_mfma_elems(2, 64, 2, 256) == 2 * 2 * 2 * 256 * 64
@@ -299,6 +299,9 @@ def test_attention_abi_validation_without_gpu(lib):
     assert attn(mask=p, mlen=775, mrs=776) == 1 and "mask rows" in _err(lib)
     assert attn(mask=p, mlen=776, mrs=776, mbs=2) == 1 and "mask strides" in _err(lib)
     assert attn(mask=vp(260), mlen=776, mrs=776) == 1 and "8-byte" in _err(lib)
+    # the fused output quant needs one KV head and 8 query heads of 256, and its scales
+    assert attn(h=16, kvh=2, qc=p) == 1 and "one KV head" in _err(lib)
+    assert attn(qc=p) == 1 and "q_scales" in _err(lib)
 
 
 # ----------------------------------------------------------------------------- op surface
