@@ -20,9 +20,9 @@ time gives the kernel duration, int8 TOPS and the fraction of the MI355X dense i
 peak (GEMMs) or of HBM bandwidth (quantizers).  The graph removes host launch gaps
 between the back-to-back kernels.  The non-W4A4 kernels of the forward (prefix attention,
 its K/V prep, RMSNorm) are timed the same way under `other_kernels`.
-The dominant kernel of the forward (gate/up GEMM) is the `roofline` object; its `traffic`
-(HBM bytes per launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed
-under profiles/ when present.
+The dominant kernel of the forward (the gate/up GEMM with its fused GELU-tanh*up
+epilogue, ~32% of the forward) is the `roofline` object; its `traffic` (HBM bytes per
+launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under profiles/.
 
 `cpu_baseline` times the CPU oracle (numpy) on one decoder layer's W4A4 work at the
 same M and scales it to the full depth.
@@ -51,7 +51,10 @@ METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
-TRAFFIC_FILE = ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md"
+TRAFFIC_FILES = {
+    "gate_up": ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md",
+    "gate_up_gelu": ROOT / "profiles" / "gate_up_gelu_gemm_776x2048x32768_traffic.md",
+}
 
 
 def parse_args():
@@ -269,14 +272,15 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
     return {name: fn() for name, fn in jobs.items()}
 
 
-def read_traffic() -> tuple[float | None, str | None]:
-    """HBM bytes per launch of the gate/up GEMM from the committed rocprofv3 summary."""
-    if not TRAFFIC_FILE.is_file():
+def read_traffic(kernel: str) -> tuple[float | None, str | None]:
+    """HBM bytes per launch of a gate/up kernel from the committed rocprofv3 summary."""
+    path = TRAFFIC_FILES[kernel]
+    if not path.is_file():
         return None, None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", TRAFFIC_FILE.read_text())
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
     if not m:
         return None, None
-    return float(m.group(1)), str(TRAFFIC_FILE.relative_to(ROOT))
+    return float(m.group(1)), str(path.relative_to(ROOT))
 
 
 # ----------------------------------------------------------------------------- CPU baseline
@@ -454,8 +458,11 @@ def main() -> int:
     for name, c in calls.items():
         kernels[name]["calls_per_layer"] = c
     w4a4_us_per_layer = sum(kernels[n]["avg_us"] * c for n, c in calls.items())
-    dk = kernels["gate_up"]
-    traffic, traffic_src = read_traffic()
+    # The dominant kernel of the forward: the gate/up GEMM as the forward launches it (with
+    # the fused GELU-tanh*up epilogue unless --unfused-gelu).
+    dk_name = "gate_up" if args.unfused_gelu else "gate_up_gelu"
+    dk = kernels[dk_name]
+    traffic, traffic_src = read_traffic(dk_name)
     roofline = {
         "bound": "mfma",
         "achieved": dk["tops"],
@@ -463,7 +470,8 @@ def main() -> int:
         "unit": "TFLOP/s",
         "frac": round(dk["tops"] / INT8_PEAK_TOPS, 4),
         "traffic": traffic,
-        "kernel": "gemm_w4a4_kernel (gate/up, int4_gemm2)",
+        "kernel": "gemm_w4a4_kernel (gate/up, int4_gemm2)" if args.unfused_gelu
+                  else "gemm_w4a4_kernel (gate/up + GELU-tanh*up epilogue, int4_gemm2_gelu)",
         "ops_per_launch": dk["ops"],
         "avg_launch_us": dk["avg_us"],
         "ops_unit": "int8 MAC x 2 per second (dense int8 MFMA)",
