@@ -74,6 +74,8 @@ def parse_args():
                     help="gate/up as two fp16 outputs + eager gelu*up instead of the fused epilogue")
     ap.add_argument("--only-kernel", default="",
                     help="skip the forward; launch only this kernel class (for rocprofv3 --pmc runs)")
+    ap.add_argument("--no-extra-points", action="store_true",
+                    help="skip the 640/768-token, batch-8 and eager-attention forward points")
     ap.add_argument("--forward-only", action="store_true",
                     help="time the graph-replayed forward only (no per-kernel table, no CPU baseline): "
                          "for a kernel trace of the real forward")
@@ -246,6 +248,33 @@ class KernelBench:
         nbytes = 4.0 * m * k + 2 * k
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes,
                 "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def forward_point(torch, model, prefix_inputs, dev, tokens: int, batch: int, steps: int) -> dict:
+    """ms per graph-replayed forward at another prefix length / batch (same model)."""
+    x = prefix_inputs(batch, tokens, dev)
+    mask = torch.zeros(batch, 1, tokens, tokens, dtype=torch.float16, device=dev)
+    model(x, mask)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        model(x, mask)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        model(x, mask)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del graph
+    return {"tokens": tokens, "batch": batch, "ms_per_forward": round(ms, 4),
+            "tokens_per_s": round(tokens * batch / ms * 1e3, 1)}
 
 
 def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
@@ -445,6 +474,25 @@ def main() -> int:
         others = kb.attention(args.batch, args.tokens)
         others["rmsnorm"] = kb.rmsnorm(m)
 
+        # The other prefix lengths and the batch-8 throughput point of the same workload,
+        # and the 776-token forward with transformers' fp16 eager attention instead of the
+        # prefix-attention kernels (everything else unchanged).
+        points = {}
+        if not args.no_extra_points:
+            for tok, bat in ((640, 1), (768, 1), (776, 8)):
+                points[f"{tok}x{bat}"] = forward_point(torch, model, prefix_inputs, dev, tok, bat, 10)
+            old = os.environ.get("PI05_W4A4_FUSE_ATTN")
+            os.environ["PI05_W4A4_FUSE_ATTN"] = "0"
+            try:
+                p = forward_point(torch, model, prefix_inputs, dev, args.tokens, args.batch, 10)
+            finally:
+                if old is None:
+                    del os.environ["PI05_W4A4_FUSE_ATTN"]
+                else:
+                    os.environ["PI05_W4A4_FUSE_ATTN"] = old
+            p["attention"] = "transformers fp16 eager (PI05_W4A4_FUSE_ATTN=0)"
+            points[f"{args.tokens}x{args.batch}_eager_attention"] = p
+
     ops = prefix_ops(args.tokens, args.batch, args.layers)
     total_ops = sum(ops.values())
     # The W4A4 kernels one decoder layer launches (fused layer: RMSNorm in the QKV and
@@ -500,6 +548,8 @@ def main() -> int:
             "layers": args.layers,
             "timed": "hip-graph replay" if not args.no_graph else "eager",
             "fused_gelu_up": not args.unfused_gelu,
+            "attention": "prefix-attention kernels (fp16, eager-attention semantics); "
+                         "forward_points has the eager-attention forward",
             "graph_replay_bit_exact_vs_eager": graph_exact,
         },
         "eager_ms_per_forward": round(eager_ms, 3),
@@ -507,6 +557,7 @@ def main() -> int:
         "w4a4_kernel_ms_per_forward": round(w4a4_us_per_layer * args.layers / 1e3, 3),
         "gemms": kernels,
         "other_kernels": others,
+        "forward_points": points,
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
