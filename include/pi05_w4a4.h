@@ -190,6 +190,15 @@ int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* 
                        size_t workspace_bytes, void* stream);
 
 /*
+ * Elementwise y = fp16(gelu_tanh(gate) * up) on fp16 [n] arrays (y may alias either input),
+ * with the arithmetic of pi05w4a4_gemm_gelu_up's epilogue.  Replaces the eager
+ * `gelu(gate, approximate="tanh") * up` of the unfused MLP (apply.py:135-138); the result
+ * equals those two eager fp16 ops bit for bit.
+ */
+int pi05w4a4_gelu_tanh_mul(const void* gate_fp16, const void* up_fp16, int64_t n, void* y_fp16,
+                           void* stream);
+
+/*
  * RMSNorm of fp16 rows, the input norm of every attention and MLP block ahead of the QKV
  * and gate/up activation quant.  No counterpart in the reference's W4A4 code: it replaces
  * transformers' GemmaRMSNorm module (modeling_gemma.py:64-78), which the reference runs

@@ -378,6 +378,18 @@ int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t 
 }
 
 
+int pi05w4a4_gelu_tanh_mul(const void* gate_fp16, const void* up_fp16, int64_t n, void* y_fp16,
+                            void* stream) {
+  if (n < 0) return fail(PI05W4A4_EINVAL, "n must be >= 0, got %lld", (long long)n);
+  if (n == 0) return ok();
+  if (gate_fp16 == nullptr || up_fp16 == nullptr || y_fp16 == nullptr)
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!aligned(gate_fp16, 2) || !aligned(up_fp16, 2) || !aligned(y_fp16, 2))
+    return fail(PI05W4A4_EINVAL, "gate, up and y must be 2-byte aligned");
+  return hip_status(w4a4::launch_gelu_up(gate_fp16, up_fp16, n, y_fp16, static_cast<hipStream_t>(stream)),
+                    "gelu_tanh_mul launch");
+}
+
 size_t pi05w4a4_attn_kv_mfma_elems(int64_t b, int32_t s, int32_t kvh, int32_t d) {
   if (b < 1 || s < 1 || kvh < 1 || d < 1) return 0;
   return static_cast<size_t>(b) * kvh * 2 * d * static_cast<size_t>(w4a4::attn_s_pad(s));

@@ -54,6 +54,7 @@
 // accumulators, and paired gate/up tiles finished exactly as the eager
 // `gelu(gate, approximate="tanh") * up` on the fp16 gate and up (apply.py:135-138).
 
+#include "gelu_tanh.h"
 #include "w4a4_internal.h"
 
 namespace w4a4 {
@@ -75,21 +76,36 @@ __device__ __forceinline__ v4i unpack_w(uint32_t x, uint32_t y) {
              static_cast<int>(y & kHiNib), static_cast<int>(y & kLoNib)};
 }
 
-// torch.nn.functional.gelu(x, approximate="tanh") of an fp16 value, evaluated the way
-// PyTorch's elementwise GELU is (fp32: x^3 = (x*x)*x, inner = kBeta * fma(kKappa, x^3, x),
-// (0.5*x) * (1 + tanhf(inner))) and rounded to fp16.  Contraction is off so that only the
-// one FMA is formed, and the empty asm keeps the fp32 result in a register: otherwise the
-// backend folds the last multiply and the fp16 conversion into one v_fma_mix, which rounds
-// once and differs from the fp32-then-fp16 rounding on about a fifth of all fp16 inputs.
-// Compared with torch's eager GELU on the same GPU for every finite fp16 input: identical.
-__device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh) {
-#pragma clang fp contract(off)
-  const float x = static_cast<float>(xh);
-  const float x3 = (x * x) * x;
-  const float inner = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
-  float y = (0.5f * x) * (1.0f + tanhf(inner));
-  asm volatile("" : "+v"(y));
-  return static_cast<_Float16>(y);
+// GELU-tanh correction table (gelu_tanh.h), built at compile time from the generated
+// list of {index, exact - fast} pairs.
+struct GeluFixEntry {
+  uint16_t idx;
+  int8_t d;
+};
+constexpr GeluFixEntry kGeluFixList[] = {
+#include "gelu_tanh_fix.inc"
+};
+struct alignas(16) GeluFixTable {
+  int8_t v[kGeluFixEntries];
+};
+constexpr GeluFixTable make_gelu_fix() {
+  GeluFixTable t{};
+  for (const GeluFixEntry& e : kGeluFixList) t.v[e.idx] = e.d;
+  return t;
+}
+__device__ const GeluFixTable kGeluFix = make_gelu_fix();
+
+// torch.nn.functional.gelu(x, approximate="tanh") of an fp16 value, bit for bit: the fast
+// evaluation plus the table's correction (`fix` is the table in global memory or LDS).
+// Over every fp16 input, inf and NaN included, the result is identical to torch's eager
+// GELU on the same GPU: the input domain is exactly the 2^16 fp16 values, so that
+// exhaustive comparison covers all cases.
+__device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh, const int8_t* fix) {
+  const uint32_t xb = __builtin_bit_cast(uint16_t, xh);
+  bool in;
+  const int d = fix[gelu_fix_index(xb, in)];
+  const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(xh));
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + (in ? d : 0)));
 }
 
 // fp16 * fp16 as torch's eager mul: one fp32 product rounded to fp16.
@@ -132,6 +148,21 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   const int mt = tile % p.mtiles;
   const int nt = tile / p.mtiles;
   const int ks = blockIdx.y;
+
+  // GELU: the correction table goes to LDS for the epilogue's per-lane lookups, copied by
+  // direct global-to-LDS loads (no registers; lane L of a wave writes bytes 16L..16L+15 of
+  // the wave's 1 KB piece).  They complete under the main loop; a vmcnt(0) wait and the
+  // barrier ahead of the epilogue order them before the reads.
+  __shared__ __align__(16) int8_t fix_lds[GELU ? kGeluFixEntries : 16];
+  if constexpr (GELU) {
+    constexpr int kPieces = kGeluFixEntries / 1024;
+    static_assert(kGeluFixEntries % 1024 == 0, "the table is copied in 1 KB pieces");
+    for (int piece = wave; piece < kPieces; piece += NWAVES) {
+      __builtin_amdgcn_global_load_lds(
+          (const __attribute__((address_space(1))) void*)(kGeluFix.v + piece * 1024 + lane * 16),
+          (__attribute__((address_space(3))) void*)(fix_lds + piece * 1024), 16, 0, 0);
+    }
+  }
 
   // Group selection with scalar selects (no dynamic indexing of the argument struct).
   const int32_t* W = p.g[0].w;
@@ -316,8 +347,22 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       // Keep each prefetch at the top of its step: under register pressure the
       // scheduler would otherwise sink the loads next to their use.
       __builtin_amdgcn_sched_barrier(0);
+      // GELU, first step: vector loads complete in issue order, so once at most the
+      // MI + NI loads just issued are outstanding, the correction table's direct loads
+      // (issued first) have landed; the first block's operands, issued after them, are
+      // awaited here anyway.
+      if constexpr (GELU) {
+        if (i == 0 && j == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MI + NI) : "memory");
+      }
       if (j == 0 || i + j < nkb) compute(ra[j], rb[j], ra[(j + 1) % RING], rb[(j + 1) % RING]);
     }
+  }
+
+  // A wave without k blocks never waited for its correction-table loads (see the first
+  // step above): it waits now, before the barrier below (or the k fold's) publishes the
+  // table to the other waves.
+  if constexpr (GELU) {
+    if (nkb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
   __shared__ __align__(16) float epi_sa[TROWS];  // row scales / 16 of the tile
@@ -420,9 +465,22 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         if (GELU) {
           const v4i su = acc[mi][ni + NI / 2];
           const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
+          // The four table lookups are issued ahead of the GELU arithmetic, which hides
+          // their LDS latency.
+          _Float16 g16[4], u16[4];
+          int fix[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            o[r] = mul_f16(gelu_tanh_f16(dequant(s[r], sv[mi], swv[r])), dequant(su[r], sv[mi], swu[r]));
+            g16[r] = dequant(s[r], sv[mi], swv[r]);
+            u16[r] = dequant(su[r], sv[mi], swu[r]);
+            bool in;
+            const int d = fix_lds[gelu_fix_index(__builtin_bit_cast(uint16_t, g16[r]), in)];
+            fix[r] = in ? d : 0;
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(g16[r])) + fix[r];
+            o[r] = mul_f16(__builtin_bit_cast(_Float16, static_cast<uint16_t>(fb)), u16[r]);
           }
         } else {
 #pragma unroll
@@ -515,7 +573,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
     _Float16* y = static_cast<_Float16*>(p.g[0].y) + row * N + c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      y[e] = mul_f16(gelu_tanh_f16(dequant(gv[e], sav, swg[c + e])), dequant(uv[e], sav, swu[c + e]));
+      y[e] = mul_f16(gelu_tanh_f16(dequant(gv[e], sav, swg[c + e]), kGeluFix.v), dequant(uv[e], sav, swu[c + e]));
     }
     return;
   }
@@ -552,6 +610,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   }
 }
 
+// Elementwise y = fp16(gelu_tanh(g) * u) on fp16 inputs: the gate/up epilogue's arithmetic
+// on given values (grid-stride loop).
+__global__ __launch_bounds__(256) void gelu_up_kernel(const _Float16* g, const _Float16* u, int64_t n,
+                                                      _Float16* y) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    y[i] = mul_f16(gelu_tanh_f16(g[i], kGeluFix.v), u[i]);
+}
+
 template <int MI, int NI, int NWAVES, int KW, int RING = 2, int WPE = 2>
 hipError_t launch_cfg(const GemmParams& p, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles),
@@ -576,6 +643,14 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
     case kCfg1x2: return launch_cfg<1, 2, 4, 1>(p, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_gelu_up(const void* g, const void* u, int64_t n, void* y, hipStream_t stream) {
+  const int64_t blocks = (n + 255) / 256;
+  const dim3 grid(static_cast<unsigned>(blocks < 16384 ? blocks : 16384));
+  gelu_up_kernel<<<grid, 256, 0, stream>>>(static_cast<const _Float16*>(g), static_cast<const _Float16*>(u), n,
+                                           static_cast<_Float16*>(y));
+  return hipGetLastError();
 }
 
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t stream) {

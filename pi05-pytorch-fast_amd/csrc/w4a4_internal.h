@@ -140,6 +140,8 @@ hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t 
 // Chooses the tile configuration; returns the K split used (>= 1) through *ksplit_out.
 hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t stream);
+// y = fp16(gelu_tanh(g) * u) elementwise on n fp16 values (n >= 1).
+hipError_t launch_gelu_up(const void* g, const void* u, int64_t n, void* y, hipStream_t stream);
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int unit_offset, int64_t m,
                           int32_t k, void* y, hipStream_t stream);
 // RMSNorm fused into the K = 2048 activation quant (hipErrorInvalidValue for other K).

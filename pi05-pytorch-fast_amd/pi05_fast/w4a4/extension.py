@@ -73,6 +73,7 @@ def load_int4_gemm():
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
+        "pi05w4a4_gelu_tanh_mul": (ctypes.c_int, [vp, vp, i64, vp, vp]),
         "pi05w4a4_gemm_residual": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm_quantize": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
         "pi05w4a4_attn_kv_mfma_elems": (sz, [i64, i32, i32, i32]),
@@ -329,6 +330,25 @@ def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offse
     with torch.cuda.device(x.device):
         _check(lib.pi05w4a4_rmsnorm(_ptr(xc), _ptr(w), float(eps), 1 if unit_offset else 0, m, k,
                                     _ptr(y), _stream(x.device)), "pi05w4a4_rmsnorm")
+    return y
+
+
+def gelu_tanh_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """fp16(gelu(gate, approximate="tanh") * up) elementwise with the fused gate/up GEMM
+    epilogue's arithmetic; equal bit for bit to the two eager fp16 ops (apply.py:135-138)."""
+    if not gate.is_cuda or not up.is_cuda:
+        raise RuntimeError("gelu_tanh_mul expects CUDA/HIP tensors")
+    if gate.dtype != torch.float16 or up.dtype != torch.float16:
+        raise RuntimeError("gelu_tanh_mul expects float16 tensors")
+    if gate.shape != up.shape:
+        raise RuntimeError(f"gelu_tanh_mul shapes differ: {tuple(gate.shape)} vs {tuple(up.shape)}")
+    g = gate.contiguous()
+    u = up.contiguous()
+    y = torch.empty_like(g)
+    lib = load_int4_gemm()
+    with torch.cuda.device(gate.device):
+        _check(lib.pi05w4a4_gelu_tanh_mul(_ptr(g), _ptr(u), g.numel(), _ptr(y), _stream(gate.device)),
+               "pi05w4a4_gelu_tanh_mul")
     return y
 
 

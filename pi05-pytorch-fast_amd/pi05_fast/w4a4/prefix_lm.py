@@ -104,12 +104,23 @@ class PrefixLM(nn.Module):
         self.layers = layers
         self.norm = norm
         self.rotary_emb = rotary
+        self._pos_cache: dict = {}
+
+    def _positions(self, hidden: torch.Tensor, b: int, s: int):
+        """Position ids 0..s-1 and their rotary (cos, sin), which depend only on (b, s, dtype):
+        computed once per shape instead of every forward (six small kernels)."""
+        key = (b, s, hidden.dtype, hidden.device)
+        hit = self._pos_cache.get(key)
+        if hit is None:
+            position_ids = torch.arange(s, device=hidden.device)[None].expand(b, s)
+            hit = (position_ids, self.rotary_emb(hidden, position_ids))
+            self._pos_cache[key] = hit
+        return hit
 
     def forward(self, inputs_embeds: torch.Tensor, attention_mask: torch.Tensor | None = None) -> torch.Tensor:
         b, s, _ = inputs_embeds.shape
         hidden = inputs_embeds * torch.tensor(self.config.hidden_size**0.5, dtype=inputs_embeds.dtype)
-        position_ids = torch.arange(s, device=inputs_embeds.device)[None].expand(b, s)
-        pos = self.rotary_emb(hidden, position_ids)
+        position_ids, pos = self._positions(hidden, b, s)
         for layer in self.layers:
             hidden = layer(hidden, attention_mask=attention_mask, position_ids=position_ids,
                            position_embeddings=pos)
