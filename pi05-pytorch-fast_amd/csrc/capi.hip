@@ -66,9 +66,13 @@ struct Plan {
 
 // Tile configuration, tile counts and K split for one call.
 //  * M > 64: 112-row tiles (MI = 7: 776 = 7 x 112 - 8).  Wide GEMMs (gate/up) use 4 waves
-//    along N (112 x 256 workgroup tiles); when that leaves fewer than 1.5 workgroups per
-//    CU (QKV, o, down) the waves split K instead (112 x 64 tiles, 4x the workgroups):
-//    4 waves for moderate K, 8 waves (2 per SIMD, each with 1/8 of K) when K >= 8192.
+//    along N (112 x 256 workgroup tiles).  When that leaves fewer than 1.5 workgroups per
+//    CU (QKV, o, down):
+//    - K >= 8192 (down): 8 waves split K (2 per SIMD, each with 1/8 of K), 112 x 64 tiles;
+//    - otherwise 32 x 128 tiles that keep the whole K in each wave, when they fit in two
+//      workgroups per CU (at M = 776 with weights streamed from HBM: o 7.8 us and QKV
+//      9.3 us, against 10.1 and 12.0 with 4 waves splitting K of 112 x 64 tiles, and 9.0
+//      and 10.1 with 64 x 128 tiles), else 64 x 128 tiles, else the K split.
 //  * Small M: narrower tiles; the remaining parallelism comes from a global K split.
 Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
   Plan pl{};
@@ -92,7 +96,16 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
   pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
   pl.ntiles = count_tiles(pl.cfg);
   if (pl.cfg.id == w4a4::kCfg7x4 && 2 * pl.mtiles * pl.ntiles < 3 * kNumCUs) {
-    pl.cfg = (k >= 8192) ? kCfg7x4K8 : kCfg7x4K4;
+    if (k >= 8192) {
+      pl.cfg = kCfg7x4K8;
+    } else if (cdiv(m, 32) * count_tiles(kCfg2x2) <= 2 * kNumCUs) {
+      pl.cfg = kCfg2x2;
+    } else if (cdiv(m, 64) * count_tiles(kCfg4x2) <= 2 * kNumCUs) {
+      pl.cfg = kCfg4x2;
+    } else {
+      pl.cfg = kCfg7x4K4;
+    }
+    pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
     pl.ntiles = count_tiles(pl.cfg);
   }
   const int nkb = w4a4::kblocks128(k);
