@@ -86,6 +86,17 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const AttnParams p) {
   const int S = p.s;
   _Float16* kf = p.kv_mfma + (b * p.kvh + g) * 2 * static_cast<int64_t>(p.s_pad) * kD;
   _Float16* vf = kf + static_cast<int64_t>(p.s_pad) * kD;
+  // The V tile's loads are issued first, so that their latency overlaps the K part's
+  // (the compiler cannot move them above the K stores, which might alias).
+  half8 vx[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int it = tid + 256 * i;
+    const int tok = it >> 5;
+    const int c = (it & 31) * 8;
+    vx[i] = half8{};
+    if (t0 + tok < S) vx[i] = ld8(p.v + (b * S + t0 + tok) * p.ld_kv + g * kD + c);
+  }
   // K: 16 tokens x 16 chunk pairs (d in [c, c + 8) and d + 128), one per thread.  The
   // RoPE'd row goes to k_rope and, as the 16-key block u of the fragment-major copy, to
   // lane (token % 16) + 16 * ((d % 32) / 8) of fragment (u, d / 32).  Tokens past S are zero.
@@ -117,11 +128,7 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const AttnParams p) {
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int it = tid + 256 * i;
-    const int tok = it >> 5;
-    const int c = (it & 31) * 8;
-    half8 x = {};
-    if (t0 + tok < S) x = ld8(p.v + (b * S + t0 + tok) * p.ld_kv + g * kD + c);
-    st8(&tile[tok][c], x);
+    st8(&tile[it >> 5][(it & 31) * 8], vx[i]);
   }
   __syncthreads();
   const int nst = p.s_pad / 32;
@@ -181,6 +188,31 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     st8(qs + r * kQld + 128 + c, hi);
   }
   __syncthreads();
+
+  // The softmax phase's mask chunks, loaded now so that their latency hides under phase 1
+  // (after phase 0, whose query loads they would delay): thread t takes row t / 16 and the
+  // 8-key chunks 8 * (t % 16 + 16 * ch).
+  const bool has_mask = p.mask != nullptr;
+  half8 mk[SCH];
+  {
+    const int r = tid >> 4;
+    const int c = tid & 15;
+    const int rr = min(row0 + r, rows - 1);
+    const _Float16* mrow =
+        has_mask ? p.mask + b * p.mask_bs + static_cast<int64_t>(rr / n_rep) * p.mask_rs : nullptr;
+    const int mlast = p.mask_len - 4;
+#pragma unroll
+    for (int ch = 0; ch < SCH; ++ch) {
+      const int k0 = 8 * (c + 16 * ch);
+      mk[ch] = half8{};
+      if (has_mask && k0 < s_pad) {
+        const half4 mv0 = *reinterpret_cast<const half4*>(mrow + min(k0, mlast));
+        const half4 mv1 = *reinterpret_cast<const half4*>(mrow + min(k0 + 4, mlast));
+        mk[ch] = half8{mv0[0], mv0[1], mv0[2], mv0[3], mv1[0], mv1[1], mv1[2], mv1[3]};
+      }
+    }
+  }
+
   // MFMA operand B of S^T = K Q^T: lane L holds Q[row 16*qb + L%16][32*t + 8*(L/16) + 0..7].
   half8 qop[2][8];
 #pragma unroll
@@ -192,7 +224,8 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   // register ring (K loads two blocks ahead).  MFMA operand A is
   // K[key 16*j + L%16][32*t + 8*(L/16) + 0..7]; the result lane L holds
   // S^T[key 16*j + 4*(L/16) + i][row 16*qb + L%16], i = 0..3, stored to LDS as
-  // fp16(fp16(q.k) * scaling).  The mask is added in the softmax phase.
+  // fp16(fp16(q.k) * scaling), or -inf for the padding keys past S.  The mask is added in
+  // the softmax phase.
   const int nblk = s_pad / 16;
   const _Float16* kf = p.kv_mfma + (b * p.kvh + g) * 2 * static_cast<int64_t>(s_pad) * kD + 8 * lane;
   if (w < nblk) {
@@ -216,7 +249,8 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const _Float16 s16 = static_cast<_Float16>(acc[qb][i]);
-          sv[i] = static_cast<_Float16>(static_cast<float>(s16) * p.scaling);
+          sv[i] = (16 * j + 4 * lg + i < S) ? static_cast<_Float16>(static_cast<float>(s16) * p.scaling)
+                                            : static_cast<_Float16>(-__builtin_inff());
         }
         *reinterpret_cast<half4*>(&sc[(16 * qb + lr) * sld + 16 * j + 4 * lg]) = sv;
       }
@@ -239,49 +273,43 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   __syncthreads();
 
   // ---- phase 2: softmax of row r = tid / 16 by its 16 threads, keys 8*(c + 16*ch) + 0..7:
-  // s = fp16(score + mask) (keys past S: -inf), then the row max, exp, sum and
-  // p = fp16(exp(s - max) / sum), written back over the scores.
+  // s = fp16(score + mask) (padding keys are -inf), the row max (exact, in fp16), then
+  // e = exp(s - max) through the hardware exp2 as exp2(s * log2 e - max * log2 e) (one
+  // v_fma_mix with the fp16 s; relative error ~1e-6, far below the fp16 rounding of the
+  // probabilities), the fp32 sum l, and p = fp16(e * (1 / l)), written back over the
+  // scores.
   {
-#pragma clang fp contract(off)
     const int r = tid >> 4;
     const int c = tid & 15;
-    const int rr = min(row0 + r, rows - 1);
-    const bool has_mask = p.mask != nullptr;
-    const _Float16* mrow =
-        has_mask ? p.mask + b * p.mask_bs + static_cast<int64_t>(rr / n_rep) * p.mask_rs : nullptr;
-    const int mlast = p.mask_len - 4;
-    float e[SCH][8];
-    float m = -__builtin_inff();
+    half8 sv[SCH];
+    half8 mx;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) mx[i] = static_cast<_Float16>(-__builtin_inff());
 #pragma unroll
     for (int ch = 0; ch < SCH; ++ch) {
       const int k0 = 8 * (c + 16 * ch);
+      sv[ch] = mx;
       if (k0 < s_pad) {
-        half8 sv = ld8(&sc[r * sld + k0]);
-        if (has_mask) {
-          const half4 mv0 = *reinterpret_cast<const half4*>(mrow + min(k0, mlast));
-          const half4 mv1 = *reinterpret_cast<const half4*>(mrow + min(k0 + 4, mlast));
-          // fp16 additions round exactly like torch's fp32-opmath fp16 add.
-          sv += half8{mv0[0], mv0[1], mv0[2], mv0[3], mv1[0], mv1[1], mv1[2], mv1[3]};
-        }
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float v = (k0 + i < S) ? static_cast<float>(sv[i]) : -__builtin_inff();
-          e[ch][i] = v;
-          m = fmaxf(m, v);
-        }
+        // fp16 additions round exactly like torch's fp32-opmath fp16 add.
+        sv[ch] = ld8(&sc[r * sld + k0]) + mk[ch];
+        mx = __builtin_elementwise_max(mx, sv[ch]);
       }
     }
+    float m = static_cast<float>(mx[0]);
+#pragma unroll
+    for (int i = 1; i < 8; ++i) m = fmaxf(m, static_cast<float>(mx[i]));
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    // exp through the hardware exp2 (v_exp_f32): relative error ~1e-6 at the exponents
-    // that matter, far below the fp16 rounding of the probabilities.
+    constexpr float kLog2e = 1.4426950408889634f;
+    const float ml = m * kLog2e;
+    float e[SCH][8];
     float l = 0.0f;
 #pragma unroll
     for (int ch = 0; ch < SCH; ++ch) {
       if (8 * (c + 16 * ch) < s_pad) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          e[ch][i] = __expf(e[ch][i] - m);
+          e[ch][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(static_cast<float>(sv[ch][i]), kLog2e, -ml));
           l += e[ch][i];
         }
       }
