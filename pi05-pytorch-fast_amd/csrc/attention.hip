@@ -57,7 +57,6 @@ constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kQld = kD + 8;        // LDS row stride of the query tile (halves)
 constexpr int kOld = 2048 + 8;      // LDS row stride of the output rows quantized in phase 4
-constexpr int kQRow = 2048 + 4 * (2048 / 32);  // FWHT scratch floats per quantized row
 
 __device__ __forceinline__ half8 ld8(const _Float16* p) { return *reinterpret_cast<const half8*>(p); }
 __device__ __forceinline__ void st8(_Float16* p, half8 v) { *reinterpret_cast<half8*>(p) = v; }
@@ -393,11 +392,11 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   // ---- phase 4 (one KV head of 8 query heads): the workgroup's 32 rows are 4 whole
   // tokens of the o-proj input (8 heads x 256 = 2048), so it quantizes them itself, as the
   // K = 2048 activation quant would: the fp16 rows are staged in LDS over the
-  // probabilities and waves 0-3 each rotate and quantize one token (fwht_quant_row).
+  // probabilities and waves 0-3 each rotate and quantize one token in registers
+  // (fwht_quant_row_wave).
   if (p.qcodes != nullptr) {
     __syncthreads();  // every wave is done reading P
     _Float16* otile = sc;                                   // [4][kOld] fp16
-    float* scratch = reinterpret_cast<float*>(sc + 4 * kOld);  // [4][kQRow] fp32
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
       const int r = 16 * qb + lr;  // n_rep == 8: token r / 8, head r % 8
@@ -419,8 +418,7 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
       }
-      fwht_quant_row<11, 6>(v, scratch + w * kQRow, nullptr, nullptr, lane, b * S + tok, p.qcodes, p.qscales,
-                            p.qcorr, p.inv_sqrt_k);
+      fwht_quant_row_wave<11>(v, lane, b * S + tok, p.qcodes, p.qscales, p.qcorr, p.inv_sqrt_k);
     }
   }
 }
@@ -442,7 +440,7 @@ hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream) {
                   static_cast<unsigned>(p.b));
   size_t sc_bytes = static_cast<size_t>(kRows) * (p.s_pad + 8) * sizeof(_Float16);
   if (p.qcodes != nullptr) {
-    const size_t q_bytes = 4 * kOld * sizeof(_Float16) + 4 * kQRow * sizeof(float);
+    const size_t q_bytes = 4 * kOld * sizeof(_Float16);
     if (q_bytes > sc_bytes) sc_bytes = q_bytes;
   }
   const size_t lds = static_cast<size_t>(kRows) * kQld * sizeof(_Float16) + sc_bytes;

@@ -181,7 +181,8 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
   constexpr int R = 1 << (LOGK - LOGT);
   static_assert(T == 64 || ROWS == 1, "rows of more than one wave need a workgroup per row");
   constexpr int LROW = K + 4 * (K / R);  // LDS floats per row (4 pad floats per R)
-  __shared__ __align__(16) float lds[ROWS * LROW];
+  // One wave per row (T == 64) runs in registers only (fwht_quant_row_wave).
+  __shared__ __align__(16) float lds[T == 64 ? 1 : ROWS * LROW];
   __shared__ float red[ROWS * (T / 64 > 0 ? T / 64 : 1)];
   __shared__ int ired[T / 64];
 
@@ -225,7 +226,12 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     }
   }
 
-  fwht_quant_row<LOGK, LOGT>(v, L, red, ired, t, row, q, sa, qcorr, inv_sqrt_k);
+  if constexpr (T == 64) {
+    (void)L;
+    fwht_quant_row_wave<LOGK>(v, t, row, q, sa, qcorr, inv_sqrt_k);
+  } else {
+    fwht_quant_row<LOGK, LOGT>(v, L, red, ired, t, row, q, sa, qcorr, inv_sqrt_k);
+  }
 }
 
 // Unrotated quantization for every other K (K % 64 == 0): int4_gemm.cu:451-477.

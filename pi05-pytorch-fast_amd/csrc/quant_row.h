@@ -213,5 +213,170 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
   if (t == 0) qcorr[row] = -8 * s16;
 }
 
+
+// ---- One wave per row, registers only (T = 64).  Lane t holds R = K / 64 consecutive
+// elements t*R .. t*R + R - 1 in v[0..R-1] (r = log2 R register bits, then 6 lane bits).
+// The butterfly stages still run in increasing order of the stride, each writing
+// (a + b, a - b) exactly, so the result is bit-identical to the CPU transform:
+//   element bits 0 .. r-1     registers (pairs v[j], v[j ^ 2^b]);
+//   element bits r .. r+3     lane bits 0-3: the partner's value comes through DPP
+//                             (xor 1, 2: quad_perm; xor 4: quad_perm + row_half_mirror;
+//                             xor 8: row_ror:8) straight into the add, and the upper lane
+//                             adds its own value negated: partner + (-own) = a - b;
+//   element bits r+4, r+5     lane bits 4 and 5: v_permlane16_swap / v_permlane32_swap on
+//                             the register pairs of bit 0 / bit 1 (already transformed)
+//                             exchange that register bit with the lane bit, the stage runs
+//                             in registers, and the swaps are undone afterwards.
+// No LDS and no barrier; the wave max and sum use the same DPP / swap exchanges.
+constexpr int kDppXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRev4 = 0x1B;       // quad_perm [3,2,1,0]: lane i^3 within the quad
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i^7 within 8
+constexpr int kDppRor8 = 0x128;      // row_ror:8: lane i^8 within the 16-lane row
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+// x of lane (this lane ^ (1 << K)), K = 0..3.
+template <int K>
+__device__ __forceinline__ float lane_xor_f(float x) {
+  if constexpr (K == 0) return dpp_f<kDppXor1>(x);
+  else if constexpr (K == 1) return dpp_f<kDppXor2>(x);
+  else if constexpr (K == 2) return dpp_f<kDppHalfMirror>(dpp_f<kDppRev4>(x));
+  else return dpp_f<kDppRor8>(x);
+}
+template <int K>
+__device__ __forceinline__ int lane_xor_i(int x) {
+  if constexpr (K == 0) return dpp_i<kDppXor1>(x);
+  else if constexpr (K == 1) return dpp_i<kDppXor2>(x);
+  else if constexpr (K == 2) return dpp_i<kDppHalfMirror>(dpp_i<kDppRev4>(x));
+  else return dpp_i<kDppRor8>(x);
+}
+// Max / sum over the 64 lanes, the result in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, lane_xor_f<0>(v));
+  v = fmaxf(v, lane_xor_f<1>(v));
+  v = fmaxf(v, lane_xor_f<2>(v));
+  v = fmaxf(v, lane_xor_f<3>(v));
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += lane_xor_i<0>(v);
+  v += lane_xor_i<1>(v);
+  v += lane_xor_i<2>(v);
+  v += lane_xor_i<3>(v);
+  auto r16 = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  v = static_cast<int>(r16[0]) + static_cast<int>(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  return static_cast<int>(r32[0]) + static_cast<int>(r32[1]);
+}
+// Register pairs (v[j], v[j | 2^B]) exchange register bit B with lane bit 4 (SW = 16) or
+// lane bit 5 (SW = 32); applying it twice restores the layout.
+template <int SW, int B, int R>
+__device__ __forceinline__ void swap_lane_bit(float (&v)[R]) {
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (j & (1 << B)) continue;
+    auto r = (SW == 16) ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j | (1 << B)]), false, false)
+                        : __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j | (1 << B)]), false, false);
+    v[j] = __uint_as_float(r[0]);
+    v[j | (1 << B)] = __uint_as_float(r[1]);
+  }
+}
+template <int B, int R>
+__device__ __forceinline__ void reg_stage(float (&v)[R]) {
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    if (j & (1 << B)) continue;
+    const float a = v[j], c = v[j + (1 << B)];
+    v[j] = __fadd_rn(a, c);
+    v[j + (1 << B)] = __fsub_rn(a, c);
+  }
+}
+template <int K, int R>
+__device__ __forceinline__ void lane_stage(float (&v)[R], int lane) {
+  const uint32_t neg = static_cast<uint32_t>((lane >> K) & 1) << 31;  // upper lane: a - b
+#pragma unroll
+  for (int j = 0; j < R; ++j) {
+    const float partner = lane_xor_f<K>(v[j]);
+    v[j] = __fadd_rn(partner, __uint_as_float(__float_as_uint(v[j]) ^ neg));
+  }
+}
+
+template <int LOGK>
+__device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)], int t, int64_t row,
+                                                    int32_t* __restrict__ q, float* __restrict__ sa,
+                                                    int32_t* __restrict__ qcorr, float inv_sqrt_k) {
+  constexpr int K = 1 << LOGK;
+  constexpr int r = LOGK - 6;
+  constexpr int R = 1 << r;
+  static_assert(r >= 4, "runs of >= 16 consecutive elements per lane");
+#pragma unroll
+  for (int b = 0; b < r; ++b) {
+    if (b == 0) reg_stage<0>(v);
+    else if (b == 1) reg_stage<1>(v);
+    else if (b == 2) reg_stage<2>(v);
+    else if (b == 3) reg_stage<3>(v);
+    else if (b == 4) reg_stage<4>(v);
+    else if (b == 5) reg_stage<5>(v);
+    else if (b == 6) reg_stage<6>(v);
+    else if (b == 7) reg_stage<7>(v);
+  }
+  lane_stage<0>(v, t);
+  lane_stage<1>(v, t);
+  lane_stage<2>(v, t);
+  lane_stage<3>(v, t);
+  swap_lane_bit<16, 0>(v);
+  reg_stage<0>(v);  // element bit r + 4
+  swap_lane_bit<32, 1>(v);
+  reg_stage<1>(v);  // element bit r + 5
+  swap_lane_bit<32, 1>(v);
+  swap_lane_bit<16, 0>(v);
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = wave_max_dpp(amax);
+  const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
+  if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
+  // Codes of the lane's R consecutive elements: R / 8 words, word u = codes 8u .. 8u + 7.
+  uint32_t words[R / 8];
+  bool near_tie = false;
+  const float rcp = __builtin_amdgcn_rcpf(sdiv);
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) {
+    float c8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+    words[u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+  }
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+#pragma unroll
+    for (int u = 0; u < R / 8; ++u) {
+      float c8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+      words[u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < R / 8; u += 2) {
+    const uint2 wd = make_uint2(words[u] ^ kObFlipLo, words[u + 1] ^ kObFlipLo);
+    *reinterpret_cast<uint2*>(&q[frag_word_index(row, (t * R) / 8 + u, kblocks128(K))]) = wd;
+  }
+  int s16 = 0;
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) s16 += odd_code_sum16(words[u]);
+  s16 = wave_sum_dpp(s16);
+  if (t == 0) qcorr[row] = -8 * s16;
+}
 }  // namespace
 }  // namespace w4a4
