@@ -252,6 +252,23 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
                               int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream);
 
+/*
+ * pi05w4a4_prefix_attention plus cache warming: the CUs that the attention leaves idle
+ * (B * KVH * ceil(S * H / KVH / 32) < 256 workgroups) read warm_n <= 4 further device
+ * buffers (16-byte aligned, sizes multiples of 16 bytes) and discard the data, so that the
+ * kernels after it find them in the Infinity Cache.  No counterpart in the reference: the
+ * fused decoder layer passes its MLP weights (gate, up, down), which the gate/up and down
+ * GEMMs then read from the cache instead of HBM.  Results are those of
+ * pi05w4a4_prefix_attention.
+ */
+int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_mfma,
+                                   const void* cos_fp16, const void* sin_fp16, const void* mask,
+                                   int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
+                                   int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
+                                   int64_t ld_out, int32_t* q_codes, float* q_scales,
+                                   const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

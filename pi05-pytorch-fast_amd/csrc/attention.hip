@@ -148,7 +148,31 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const AttnParams p) {
   }
 }
 
-// ---- attention.  Grid (ceil(S * n_rep / 32), KVH, B), 512 threads (8 waves).
+// Cache warming by the workgroups past the query row blocks: `part` of `nparts` slices of
+// the buffers, 8 loads of 16 bytes in flight per thread; the data feed an empty asm.
+__device__ __forceinline__ void cache_warm_part(const CacheWarmParams& w, int64_t part, int64_t nparts, int tid) {
+  constexpr int kLoads = 8;
+  const int64_t stride = nparts * kThreads * kLoads;
+  uint32_t acc = 0;
+#pragma unroll 1
+  for (int bi = 0; bi < w.nbuf; ++bi) {
+    const uint4* src = static_cast<const uint4*>(w.ptr[bi]);
+    const int64_t n = w.n16[bi];
+    for (int64_t base = part * kThreads * kLoads + tid; base < n; base += stride) {
+      uint4 v[kLoads];
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) {
+        const int64_t idx = base + static_cast<int64_t>(i) * kThreads;
+        v[i] = idx < n ? src[idx] : make_uint4(0, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < kLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
+    }
+  }
+  asm volatile("" ::"v"(acc));
+}
+
+// ---- attention.  Grid (ceil(S * n_rep / 32) + warm, KVH, B), 512 threads (8 waves).
 // SCH = 8-key chunks per thread in the softmax phase (s_pad <= 128 * SCH).
 template <int SCH>
 __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnParams p) {
@@ -157,6 +181,12 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   _Float16* sc = lds + kRows * kQld;   // [kRows][sld]: scores, then probabilities
 
   const int tid = threadIdx.x;
+  if (static_cast<int>(blockIdx.x) >= p.row_blocks) {  // a cache-warming workgroup
+    const int64_t wx = gridDim.x - p.row_blocks;
+    cache_warm_part(p.warm, (static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y) * wx + (blockIdx.x - p.row_blocks),
+                    wx * gridDim.y * gridDim.z, tid);
+    return;
+  }
   const int lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15;
@@ -434,9 +464,16 @@ hipError_t launch_attn_kv_prep(const AttnParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream) {
+hipError_t launch_prefix_attention(const AttnParams& p_in, hipStream_t stream) {
+  AttnParams p = p_in;
   const int64_t rows = static_cast<int64_t>(p.s) * (p.h / p.kvh);
-  const dim3 grid(static_cast<unsigned>((rows + kRows - 1) / kRows), static_cast<unsigned>(p.kvh),
+  p.row_blocks = static_cast<int32_t>((rows + kRows - 1) / kRows);
+  // Cache warming uses the CUs that the attention leaves idle (one workgroup per CU fits
+  // by LDS): none when the attention alone fills the 256 CUs of an MI355X.
+  constexpr int64_t kCUs = 256;
+  const int64_t attn_wgs = static_cast<int64_t>(p.row_blocks) * p.kvh * p.b;
+  const int64_t warm_x = (p.warm.nbuf > 0 && attn_wgs < kCUs) ? (kCUs - attn_wgs) / (static_cast<int64_t>(p.kvh) * p.b) : 0;
+  const dim3 grid(static_cast<unsigned>(p.row_blocks + warm_x), static_cast<unsigned>(p.kvh),
                   static_cast<unsigned>(p.b));
   size_t sc_bytes = static_cast<size_t>(kRows) * (p.s_pad + 8) * sizeof(_Float16);
   if (p.qcodes != nullptr) {

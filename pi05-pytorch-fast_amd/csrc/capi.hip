@@ -436,11 +436,14 @@ int pi05w4a4_attn_kv_prep(const void* k, const void* v, int64_t ld_kv, const voi
   return hip_status(w4a4::launch_attn_kv_prep(p, static_cast<hipStream_t>(stream)), "attention K/V prep launch");
 }
 
-int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
-                              const void* cos_fp16, const void* sin_fp16, const void* mask,
-                              int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
-                              int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
-                              int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream) {
+}  // extern "C"
+
+namespace {
+int prefix_attention_call(const void* q, int64_t ld_q, const void* kv_mfma, const void* cos_fp16,
+                          const void* sin_fp16, const void* mask, int64_t mask_bs, int64_t mask_rs,
+                          int32_t mask_len, float scaling, int64_t b, int32_t s, int32_t h, int32_t kvh,
+                          int32_t d, void* out, int64_t ld_out, int32_t* q_codes, float* q_scales,
+                          const w4a4::CacheWarmParams& warm, void* stream) {
   int rc = validate_attention(b, s, h, kvh, d);
   if (rc) return rc;
   if (!q || !kv_mfma || !cos_fp16 || !sin_fp16 || (!out && !q_codes))
@@ -492,7 +495,44 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
     p.qcorr = q_codes + w4a4::q_payload_words((rows + 15) / 16, w4a4::kblocks128(2048));
     p.inv_sqrt_k = static_cast<float>(1.0 / std::sqrt(2048.0));
   }
+  p.warm = warm;
   return hip_status(w4a4::launch_prefix_attention(p, static_cast<hipStream_t>(stream)), "prefix attention launch");
+}
+}  // namespace
+
+extern "C" {
+
+int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
+                              const void* cos_fp16, const void* sin_fp16, const void* mask,
+                              int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
+                              int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
+                              int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream) {
+  return prefix_attention_call(q, ld_q, kv_mfma, cos_fp16, sin_fp16, mask, mask_bs, mask_rs, mask_len, scaling, b,
+                               s, h, kvh, d, out, ld_out, q_codes, q_scales, w4a4::CacheWarmParams{}, stream);
+}
+
+int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_mfma,
+                                   const void* cos_fp16, const void* sin_fp16, const void* mask,
+                                   int64_t mask_bs, int64_t mask_rs, int32_t mask_len, float scaling,
+                                   int64_t b, int32_t s, int32_t h, int32_t kvh, int32_t d, void* out,
+                                   int64_t ld_out, int32_t* q_codes, float* q_scales,
+                                   const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                                   void* stream) {
+  if (warm_n < 0 || warm_n > w4a4::kMaxWarmBuffers)
+    return fail(PI05W4A4_EINVAL, "cache warming takes 0..%d buffers, got %d", w4a4::kMaxWarmBuffers, warm_n);
+  if (warm_n > 0 && (warm_ptrs == nullptr || warm_bytes == nullptr))
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  w4a4::CacheWarmParams warm{};
+  for (int i = 0; i < warm_n; ++i) {
+    if (warm_ptrs[i] == nullptr || !aligned(warm_ptrs[i], 16) || warm_bytes[i] % 16 != 0)
+      return fail(PI05W4A4_EINVAL, "warm buffer %d must be non-null, 16-byte aligned and a multiple of 16 bytes", i);
+    if (warm_bytes[i] == 0) continue;
+    warm.ptr[warm.nbuf] = warm_ptrs[i];
+    warm.n16[warm.nbuf] = static_cast<int64_t>(warm_bytes[i] / 16);
+    ++warm.nbuf;
+  }
+  return prefix_attention_call(q, ld_q, kv_mfma, cos_fp16, sin_fp16, mask, mask_bs, mask_rs, mask_len, scaling, b,
+                               s, h, kvh, d, out, ld_out, q_codes, q_scales, warm, stream);
 }
 
 int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,

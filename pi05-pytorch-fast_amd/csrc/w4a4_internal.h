@@ -103,6 +103,16 @@ enum TileCfg : int {
   kCfg7x4K8 = 6,  // MI 7, NI 4, 8 waves along K (2 per SIMD): 112 x 64, for very long K
 };
 
+// Cache warming: up to kMaxWarmBuffers device buffers of n16[i] 16-byte words that a
+// kernel reads and discards with otherwise idle workgroups, so that the next kernel finds
+// them in the memory-side Infinity Cache.
+constexpr int kMaxWarmBuffers = 4;
+struct CacheWarmParams {
+  const void* ptr[kMaxWarmBuffers];
+  int64_t n16[kMaxWarmBuffers];
+  int32_t nbuf;
+};
+
 // Prefix attention (attention.hip): head_dim 256, grouped-query heads, fp16.
 constexpr int kAttnHeadDim = 256;
 constexpr int kAttnMaxKeys = 1024;
@@ -129,6 +139,8 @@ struct AttnParams {
   float* qscales;         //   codes, scales and row corrections as pi05w4a4_quantize writes
   int32_t* qcorr;         //   them for M = B * S rows
   float inv_sqrt_k;
+  int32_t row_blocks;     // set by the launcher: workgroups along x that own query rows
+  CacheWarmParams warm;   // read by the workgroups past row_blocks (nbuf 0: none)
 };
 int64_t attn_s_pad(int32_t s);
 

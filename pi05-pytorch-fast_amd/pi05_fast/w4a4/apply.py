@@ -359,8 +359,13 @@ def _fused_decoder_layer_forward(
                                       unit_offset=off1)
     cos, sin = position_embeddings
     hd = attn.head_dim
+    # The attention launch's idle CUs read the MLP weights into the Infinity Cache for the
+    # gate/up and down GEMMs (PI05_W4A4_CACHE_WARM=0: off).
+    warm = None if os.environ.get("PI05_W4A4_CACHE_WARM", "1") == "0" else [
+        mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed]
     x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
-                                                    q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x)
+                                                    q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
+                                                    warm=warm)
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)

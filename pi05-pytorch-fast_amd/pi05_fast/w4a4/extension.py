@@ -82,6 +82,11 @@ def load_int4_gemm():
             ctypes.c_int,
             [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp, vp, vp],
         ),
+        "pi05w4a4_prefix_attention_warm": (
+            ctypes.c_int,
+            [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp, vp,
+             ctypes.POINTER(vp), ctypes.POINTER(sz), i32, vp],
+        ),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -384,10 +389,12 @@ def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int):
 def _prefix_attention_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
-    quantize_out: bool = False,
+    quantize_out: bool = False, warm: list[torch.Tensor] | None = None,
 ):
     """(out, key states) or, with ``quantize_out`` (one KV head, 8 query heads), (out, key
-    states, q codes, scales) of the output rows' K = 2048 activation quant."""
+    states, q codes, scales) of the output rows' K = 2048 activation quant.  ``warm``: up to
+    four contiguous device tensors that the attention launch's idle workgroups read into
+    the Infinity Cache (``pi05w4a4_prefix_attention_warm``)."""
     d = ATTN_HEAD_DIM
     for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if not t.is_cuda:
@@ -416,16 +423,28 @@ def _prefix_attention_impl(
         st = _stream(q.device)
         _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
                                          _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
-        _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
-                                             _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
-                                             _ptr(out), h * d, _ptr(codes), _ptr(scales), st),
-               "pi05w4a4_prefix_attention")
+        ws = [t for t in (warm or []) if t is not None and t.numel() > 0]
+        if ws:
+            if len(ws) > 4 or any((not t.is_cuda) or (not t.is_contiguous()) for t in ws):
+                raise RuntimeError("prefix_attention: warm takes up to 4 contiguous CUDA/HIP tensors")
+            wp = (ctypes.c_void_p * len(ws))(*[t.data_ptr() for t in ws])
+            wb = (ctypes.c_size_t * len(ws))(*[(t.numel() * t.element_size()) // 16 * 16 for t in ws])
+            _check(lib.pi05w4a4_prefix_attention_warm(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
+                                                      _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
+                                                      _ptr(out), h * d, _ptr(codes), _ptr(scales), wp, wb, len(ws),
+                                                      st), "pi05w4a4_prefix_attention_warm")
+        else:
+            _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
+                                                 _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
+                                                 _ptr(out), h * d, _ptr(codes), _ptr(scales), st),
+                   "pi05w4a4_prefix_attention")
     if quantize_out:
         return out, k_rope, codes, scales
     return out, k_rope
 
 
-def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual,
+                                  warm=None):
     """RoPE + attention + o_proj + residual add: with one KV head and 8 query heads of 256
     the attention kernel quantizes its own output rows for the o GEMM; otherwise the output
     goes through the separate quantizer.  Returns (residual + o_proj(out), key states, out)."""
@@ -435,11 +454,11 @@ def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, n
     lead = tuple(q.shape[:-1])
     if int(num_kv_heads) == 1 and k_in == 2048:
         out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
-                                                            num_kv_heads, quantize_out=True)
+                                                            num_kv_heads, quantize_out=True, warm=warm)
         with torch.cuda.device(q.device):
             y = _gemm_from_q(codes, scales, k_in, [(w, n_true)], lead, q.device, "int4_gemm", residual=residual)[0]
         return y, k_rope, out
-    out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads)
+    out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, warm=warm)
     return _run(out, [w_o], tiled=False, kind="int4_gemm", residual=residual)[0], k_rope, out
 
 
@@ -579,13 +598,13 @@ def _register_custom_op() -> None:
     def _prefix_attention_o_proj(
         q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
         mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
-        w_o: torch.Tensor, residual: torch.Tensor,
+        w_o: torch.Tensor, residual: torch.Tensor, warm: list[torch.Tensor],
     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         return _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o,
-                                             residual)
+                                             residual, warm)
 
     @_prefix_attention_o_proj.register_fake
-    def _prefix_attention_o_proj_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+    def _prefix_attention_o_proj_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm):
         b, s = q.shape[0], q.shape[1]
         return (q.new_empty((b, s, w_o.shape[0])), q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM)),
                 q.new_empty((b, s, num_heads * ATTN_HEAD_DIM)))
@@ -685,13 +704,15 @@ def prefix_attention(
                                                 int(num_kv_heads))
 
 
-def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual):
+def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm=None):
     """residual + o_proj(attention(q, k, v)) of a prefix forward, plus the RoPE'd key
     states and the attention output: ``prefix_attention`` followed by
     ``int4_gemm_residual``, with the o-proj activation quant done inside the attention
-    kernel when the layer has one KV head and 8 query heads of 256 (PaliGemma)."""
+    kernel when the layer has one KV head and 8 query heads of 256 (PaliGemma).  ``warm``:
+    up to four weight tensors of the following ops that the attention launch's idle CUs
+    read into the Infinity Cache (results unchanged)."""
     return torch.ops.pi05_w4a4.prefix_attention_o_proj(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
-                                                       int(num_kv_heads), w_o, residual)
+                                                       int(num_kv_heads), w_o, residual, list(warm or []))
 
 
 def preload() -> None:

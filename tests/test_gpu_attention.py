@@ -312,3 +312,28 @@ def test_prefix_attention_o_proj_matches_oracle(ext, cuda, b, s, h, kvh):
     got = x2.reshape(b * s, 2048).cpu().numpy()
     nbad = int(np.count_nonzero(got.view(np.int16) != want.view(np.int16)))
     assert nbad == 0, f"{nbad}/{got.size} outputs differ"
+
+
+@pytest.mark.parametrize("b,s,h,kvh", [(1, 776, 8, 1), (2, 100, 8, 1), (8, 776, 8, 1)])
+def test_prefix_attention_cache_warm_changes_nothing(ext, cuda, b, s, h, kvh):
+    """The cache-warming variant (idle workgroups of the attention launch read further
+    buffers: here the weights of an MLP, 48 MB) returns the same bits as the plain call,
+    and leaves the buffers it read unchanged; at batch 8 the attention fills every CU and
+    no workgroup warms."""
+    from tests import w4a4_inputs as inp
+
+    q, k, v, cos, sin = _inputs(b, s, h, kvh, cuda, seed=900 + s + b)
+    mask = _padding_causal_mask(b, s, [max(1, s - 7 * i) for i in range(b)], cuda)
+    gen = inp.generator(77 + s)
+    w_o = ext.repack_weight(inp.packed_weight(gen, 2048, h * D).to(cuda), k=h * D)
+    res = (torch.randn(b, s, 2048, generator=gen) * 2.0).half().to(cuda)
+    big = [torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=cuda) for n in (4 << 20, 4 << 20, 4 << 20)]
+    keep = [t.clone() for t in big]
+    with torch.no_grad():
+        plain = ext.prefix_attention_o_proj(q, k, v, cos, sin, mask, D**-0.5, h, kvh, w_o, res)
+        warm = ext.prefix_attention_o_proj(q, k, v, cos, sin, mask, D**-0.5, h, kvh, w_o, res, warm=big)
+    torch.cuda.synchronize()
+    for a, c in zip(plain, warm):
+        assert torch.equal(a, c)
+    for t, t0 in zip(big, keep):
+        assert torch.equal(t, t0)

@@ -303,6 +303,19 @@ def test_attention_abi_validation_without_gpu(lib):
     assert attn(h=16, kvh=2, qc=p) == 1 and "one KV head" in _err(lib)
     assert attn(qc=p) == 1 and "q_scales" in _err(lib)
 
+    # the cache-warming variant: up to 4 buffers, 16-byte aligned, sizes multiples of 16;
+    # the attention arguments are validated the same way
+    def warm(ptrs, sizes, n=None, ld_q=2048):
+        arr = (vp * max(len(ptrs), 1))(*ptrs)
+        sz = (ctypes.c_size_t * max(len(sizes), 1))(*sizes)
+        return lib.pi05w4a4_prefix_attention_warm(p, ld_q, p, p, p, vp(0), 0, 0, 0, 0.0625, 1, 776, 8, 1, 256, p,
+                                                  2048, vp(0), vp(0), arr, sz, len(ptrs) if n is None else n, vp(0))
+
+    assert warm([p] * 5, [16] * 5) == 1 and "0..4 buffers" in _err(lib)
+    assert warm([vp(264)], [1024]) == 1 and "16-byte aligned" in _err(lib)
+    assert warm([p], [1000]) == 1 and "multiple of 16" in _err(lib)
+    assert warm([p], [1024], ld_q=1024) == 1 and "token stride" in _err(lib)
+
 
 # ----------------------------------------------------------------------------- op surface
 def test_custom_ops_registered_with_fakes():
