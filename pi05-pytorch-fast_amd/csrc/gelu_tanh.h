@@ -26,8 +26,8 @@ __device__ __forceinline__ float gelu_tanh_exact(float x) {
 // hardware exp2 and reciprocal, a third of the instructions of tanhf.  Every operation is
 // a single IEEE fp32 operation or one hardware instruction, so the result is the same in
 // every kernel that inlines this.  It differs from the exact expression's fp16 result on
-// 428 of the 65536 fp16 inputs, all with |x| in [2^-4, 8): 421 in x in [-5.2, -3], where
-// 1 + tanh cancels to a few ulps, and 7 single-ulp roundings elsewhere.
+// 428 of the 65536 fp16 inputs: 426 with x in [-8, -1) (mostly x in [-5.2, -3], where
+// 1 + tanh cancels to a few ulps) and 2 single-ulp roundings elsewhere.
 __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
 #pragma clang fp contract(off)
   const float x3 = (x * x) * x;
@@ -39,20 +39,21 @@ __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(y));
 }
 
-// Correction table: for the fp16 inputs with exponent field 11..17 (|x| in [2^-4, 8)),
-// the exact result's fp16 bit pattern minus the fast one's, as int8.  Entry index:
-// (bits & 0x7fff) - kGeluFixBase, plus kGeluFixSpan for negative x.  Outside that window
-// the fast result is exact.  The table is generated on the GPU from these two functions
-// (gelu_fix_gen.hip) and the exhaustive test compares every fp16 input with torch.
-constexpr uint32_t kGeluFixBase = 11u << 10;
-constexpr uint32_t kGeluFixSpan = 7u << 10;
-constexpr int kGeluFixEntries = 2 * kGeluFixSpan;
+// Corrections: the exact result's fp16 bit pattern minus the fast one's, for the inputs
+// where they differ (gelu_tanh_fix.inc, generated on the GPU from these two functions by
+// gelu_fix_gen.hip; the exhaustive test compares every fp16 input with torch).  Those in
+// the window of negative x with |x| in [1, 8) (bit patterns 0xbc00 .. 0xc7ff: 426 of
+// the 428) go to a 3 KB int8 table indexed by bits - kGeluFixBase; the others (2) are
+// compared one by one.
+constexpr uint32_t kGeluFixBase = 0xbc00u;
+constexpr uint32_t kGeluFixSpan = 3u << 10;
+constexpr int kGeluFixEntries = kGeluFixSpan;
 
 // Index of fp16 bit pattern xb in the table (0 outside the window, where *in is false).
 __device__ __forceinline__ uint32_t gelu_fix_index(uint32_t xb, bool& in) {
-  const uint32_t off = (xb & 0x7fffu) - kGeluFixBase;
+  const uint32_t off = xb - kGeluFixBase;
   in = off < kGeluFixSpan;
-  return (in ? off : 0u) + ((xb >> 15) ? kGeluFixSpan : 0u);
+  return in ? off : 0u;
 }
 
 }  // namespace w4a4

@@ -79,21 +79,48 @@ __device__ __forceinline__ v4i unpack_w(uint32_t x, uint32_t y) {
 // GELU-tanh correction table (gelu_tanh.h), built at compile time from the generated
 // list of {index, exact - fast} pairs.
 struct GeluFixEntry {
-  uint16_t idx;
+  uint16_t bits;
   int8_t d;
 };
 constexpr GeluFixEntry kGeluFixList[] = {
 #include "gelu_tanh_fix.inc"
 };
+constexpr bool gelu_fix_in_window(uint32_t bits) { return bits - kGeluFixBase < kGeluFixSpan; }
 struct alignas(16) GeluFixTable {
   int8_t v[kGeluFixEntries];
 };
 constexpr GeluFixTable make_gelu_fix() {
   GeluFixTable t{};
-  for (const GeluFixEntry& e : kGeluFixList) t.v[e.idx] = e.d;
+  for (const GeluFixEntry& e : kGeluFixList)
+    if (gelu_fix_in_window(e.bits)) t.v[e.bits - kGeluFixBase] = e.d;
   return t;
 }
 __device__ const GeluFixTable kGeluFix = make_gelu_fix();
+constexpr int count_gelu_strays() {
+  int n = 0;
+  for (const GeluFixEntry& e : kGeluFixList) n += gelu_fix_in_window(e.bits) ? 0 : 1;
+  return n;
+}
+constexpr int kGeluStrays = count_gelu_strays();
+static_assert(kGeluStrays <= 4, "corrections outside the table window are compared one by one");
+struct GeluStrays {
+  GeluFixEntry e[kGeluStrays > 0 ? kGeluStrays : 1];
+};
+constexpr GeluStrays make_gelu_strays() {
+  GeluStrays s{};
+  int n = 0;
+  for (const GeluFixEntry& e : kGeluFixList)
+    if (!gelu_fix_in_window(e.bits)) s.e[n++] = e;
+  return s;
+}
+constexpr GeluStrays kGeluStrayList = make_gelu_strays();
+
+// Correction of fp16 input bits xb outside the table window (0 for all but the strays).
+__device__ __forceinline__ int gelu_stray_fix(uint32_t xb, int d) {
+#pragma unroll
+  for (int i = 0; i < kGeluStrays; ++i) d = (xb == kGeluStrayList.e[i].bits) ? kGeluStrayList.e[i].d : d;
+  return d;
+}
 
 // torch.nn.functional.gelu(x, approximate="tanh") of an fp16 value, bit for bit: the fast
 // evaluation plus the table's correction (`fix` is the table in global memory or LDS).
@@ -105,7 +132,7 @@ __device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh, const int8_t* fix
   bool in;
   const int d = fix[gelu_fix_index(xb, in)];
   const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(xh));
-  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + (in ? d : 0)));
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + gelu_stray_fix(xb, in ? d : 0)));
 }
 
 // fp16 * fp16 as torch's eager mul: one fp32 product rounded to fp16.
@@ -474,8 +501,9 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
             g16[r] = dequant(s[r], sv[mi], swv[r]);
             u16[r] = dequant(su[r], sv[mi], swu[r]);
             bool in;
-            const int d = fix_lds[gelu_fix_index(__builtin_bit_cast(uint16_t, g16[r]), in)];
-            fix[r] = in ? d : 0;
+            const uint32_t xb = __builtin_bit_cast(uint16_t, g16[r]);
+            const int d = fix_lds[gelu_fix_index(xb, in)];
+            fix[r] = gelu_stray_fix(xb, in ? d : 0);
           }
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
