@@ -34,6 +34,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import os
 import re
@@ -95,10 +96,12 @@ class KernelBench:
     def _stream(self):
         return ctypes.c_void_p(self.torch.cuda.current_stream(self.dev).cuda_stream)
 
-    def _time(self, fn) -> float:
+    def _time(self, fn, iters: int | None = None) -> float:
         """Median microseconds per launch of `fn` over `reps` replays of a graph holding
-        `iters` launches, after an eager warm-up of about `warm_s` seconds."""
+        `iters` launches (default: the bench's), after an eager warm-up of about `warm_s`
+        seconds."""
         torch = self.torch
+        iters = iters or self.iters
         fn()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
@@ -108,7 +111,7 @@ class KernelBench:
             torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for _ in range(self.iters):
+            for _ in range(iters):
                 fn()
         graph.replay()
         torch.cuda.synchronize()
@@ -120,7 +123,7 @@ class KernelBench:
             graph.replay()
             e1.record()
             torch.cuda.synchronize()
-            per_launch.append(e0.elapsed_time(e1) * 1e3 / self.iters)
+            per_launch.append(e0.elapsed_time(e1) * 1e3 / iters)
         del graph
         return statistics.median(per_launch)
 
@@ -159,13 +162,18 @@ class KernelBench:
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
 
-    def gemm(self, m, k, ns, gelu=False, residual=False):
+    def gemm(self, m, k, ns, gelu=False, residual=False, copies=1):
+        """One W4A4 GEMM launch shape.  With `copies` > 1 (plain grouped GEMM only), that
+        many weight sets are packed and the timed graph cycles through them, one set per
+        launch, so that weights come from HBM rather than from the L2 / Infinity Cache."""
         torch, lib, P = self.torch, self.lib, self.ext._ptr
         gen = torch.Generator(device=self.dev).manual_seed(20260923 + k + sum(ns))
         x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
         q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
         sa = torch.empty(m, dtype=torch.float32, device=self.dev)
         self._check(lib.pi05w4a4_quantize(P(x), m, k, P(q), P(sa), self._stream()))
+        if copies > 1 and (gelu or residual):
+            raise ValueError("weight copies are for the plain grouped GEMM")
         ws = [self._packed(n, k, gen) for n in ns]
         g = len(ns)
         n_arr = (ctypes.c_int32 * g)(*ns)
@@ -184,12 +192,14 @@ class KernelBench:
             out_bytes = 4.0 * m * ns[0]
         else:
             outs = [torch.empty(m, n, dtype=torch.float16, device=self.dev) for n in ns]
-            w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for w in ws])
             y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in outs])
+            sets = [ws] + [[self._packed(n, k, gen) for n in ns] for _ in range(copies - 1)]
+            w_arrs = [(ctypes.c_void_p * g)(*[w.data_ptr() for w in s]) for s in sets]
+            turn = itertools.cycle(w_arrs)
             fn = lambda: self._check(lib.pi05w4a4_gemm_multi(  # noqa: E731
-                P(q), P(sa), m, k, g, w_arr, n_arr, y_arr, P(work), wsb, self._stream()))
+                P(q), P(sa), m, k, g, next(turn), n_arr, y_arr, P(work), wsb, self._stream()))
             out_bytes = 2.0 * m * sum(ns)
-        us = self._time(fn)
+        us = self._time(fn, iters=copies if copies > 1 else None)
         n = sum(ns)
         ops = 2.0 * m * n * k
         nbytes = m * k / 2 + 4 * m + n * k / 2 + 4 * n + out_bytes
@@ -296,9 +306,36 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         dst = kb.torch.empty_like(src)
         us = kb._time(lambda: dst.copy_(src))
         return {"copy": {"bytes_read": float(64 << 20), "bytes_written": float(64 << 20), "avg_us": round(us, 3)}}
+    if only == "qkv_m_sweep":
+        return {only: qkv_m_sweep(kb)}
     if only:
         return {only: jobs[only]()}
     return {name: fn() for name, fn in jobs.items()}
+
+
+def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
+    """The fused QKV projection (int4_gemm3: one activation quant, N = 2048 + 256 + 256,
+    K = 2048) and its RMSNorm + quant over a range of token counts, down to the
+    weight-streaming regime of M = 1 and 64.  `hot`: the same weights every launch (they
+    stay in the L2 / Infinity Cache); `cold`: each launch of the timed graph reads its own
+    copy of the 2.6 MB of packed weights (200 copies, 0.5 GB, beyond the 256 MB Infinity
+    Cache), as a forward that streams every layer's weights once does."""
+    out = {}
+    wbytes = 2560 * (2048 // 2 + 4)
+    for m in ms:
+        hot = kb.gemm(m, 2048, [2048, 256, 256])
+        cold = kb.gemm(m, 2048, [2048, 256, 256], copies=200)
+        nq = kb.rmsnorm_quant(m)
+        out[str(m)] = {
+            "gemm_hot_us": hot["avg_us"], "gemm_hot_tops": hot["tops"],
+            "gemm_cold_us": cold["avg_us"], "gemm_cold_tops": cold["tops"],
+            "frac_int8_peak_cold": cold["frac_int8_peak"],
+            "bytes": cold["bytes"], "weight_bytes": wbytes,
+            "gemm_cold_gbs": cold["gbs"], "frac_hbm_cold": round(cold["gbs"] / HBM_PEAK_GBS, 4),
+            "rmsnorm_quant_us": nq["avg_us"],
+            "block_cold_us": round(cold["avg_us"] + nq["avg_us"], 3),
+        }
+    return out
 
 
 def read_traffic(kernel: str) -> tuple[float | None, str | None]:
@@ -471,6 +508,7 @@ def main() -> int:
             return 0
 
         kernels = kernel_table(kb, m)
+        sweep = qkv_m_sweep(kb)
         others = kb.attention(args.batch, args.tokens)
         others["rmsnorm"] = kb.rmsnorm(m)
 
@@ -559,6 +597,7 @@ def main() -> int:
         "w4a4_gop_per_forward": round(total_ops / 1e9, 1),
         "w4a4_kernel_ms_per_forward": round(w4a4_us_per_layer * args.layers / 1e3, 3),
         "gemms": kernels,
+        "qkv_m_sweep": sweep,
         "other_kernels": others,
         "forward_points": points,
         "roofline": roofline,

@@ -6,6 +6,7 @@
 // reference, nothing here allocates device memory: the caller passes the outputs,
 // the quantized-activation buffers and the split-K workspace.
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -55,6 +56,9 @@ constexpr TileCfg kCfg7x4K8{w4a4::kCfg7x4K8, 7, 4, 8, 8};
 constexpr TileCfg kCfg4x2{w4a4::kCfg4x2, 4, 2, 4, 1};
 constexpr TileCfg kCfg2x2{w4a4::kCfg2x2, 2, 2, 4, 1};
 constexpr TileCfg kCfg1x2{w4a4::kCfg1x2, 1, 2, 4, 1};
+constexpr TileCfg kCfg1x2K4{w4a4::kCfg1x2K4, 1, 2, 4, 4};
+constexpr TileCfg kCfg2x2K4{w4a4::kCfg2x2K4, 2, 2, 4, 4};
+constexpr TileCfg kCfg4x2K4{w4a4::kCfg4x2K4, 4, 2, 4, 4};
 
 struct Plan {
   TileCfg cfg;
@@ -73,17 +77,26 @@ struct Plan {
 //      workgroups per CU (at M = 776 with weights streamed from HBM: o 7.8 us and QKV
 //      9.3 us, against 10.1 and 12.0 with 4 waves splitting K of 112 x 64 tiles, and 9.0
 //      and 10.1 with 64 x 128 tiles), else 64 x 128 tiles, else the K split.
-//  * Small M: narrower tiles; the remaining parallelism comes from a global K split.
+//  * M <= 64 (weight streaming): 16-, 32- or 64-row tiles of 32 columns whose four waves
+//    split K and fold their sums through LDS, so that one launch streams the weights
+//    (QKV at M = 1: 3.0 us, against 5.8 us for 16 x 128 tiles with a global K split and
+//    its reduce launch).  A global split stays for long K (down), with at least 4 k blocks
+//    per wave.  The paired gate/up GELU GEMM uses them up to M = 16 only, and 4-waves-
+//    along-N tiles with the global split above that.
 Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
   Plan pl{};
+  // The GELU pairing's 16-column K-split tiles make 1024 workgroups at gate/up size, each
+  // staging the GELU correction table: from M = 17 on the wider tiles are faster.
+  const bool stream_k = m <= 16 || (!gelu && m <= 64);
   if (m <= 16)
-    pl.cfg = kCfg1x2;
+    pl.cfg = stream_k ? kCfg1x2K4 : kCfg1x2;
   else if (m <= 32)
-    pl.cfg = kCfg2x2;
+    pl.cfg = stream_k ? kCfg2x2K4 : kCfg2x2;
   else if (m <= 64)
-    pl.cfg = kCfg4x2;
+    pl.cfg = stream_k ? kCfg4x2K4 : kCfg4x2;
   else
     pl.cfg = kCfg7x4;
+  const bool small = pl.cfg.kw > 1;
   auto count_tiles = [&](const TileCfg& c) {
     int64_t t = 0;
     if (gelu) {
@@ -116,6 +129,9 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
     const int64_t base = pl.mtiles * pl.ntiles;
     if (2 * base < kNumCUs) ks = static_cast<int>(cdiv(kNumCUs, base));
     if (ks > w4a4::kMaxKSplit) ks = w4a4::kMaxKSplit;
+    // Small M: the workgroup's waves already split K; a global split is left for long K
+    // only, keeping at least 4 k blocks per wave.
+    if (small) ks = std::min<int>(ks, std::max(1, nkb / (4 * pl.cfg.kw)));
   }
   if (ks > nkb) ks = nkb;
   if (ks < 1) ks = 1;

@@ -584,20 +584,30 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   const int64_t scale_off = static_cast<int64_t>(kblocks128(p.k)) * 16;
   const int64_t plane = M * p.n_total;
   const float sav = p.sa[row] * 0.0625f;  // the sums below are 16 * acc
+  // Partials are read four slices at a time (clamped slice indices, masked sums), so that
+  // four loads are in flight per thread instead of one dependent load per slice.
+  auto sum_slices = [&](int col) {
+    v4i s = v4i{0, 0, 0, 0};
+    const int32_t* base = p.partial + row * p.n_total + col;
+    for (int k0 = 0; k0 < p.ksplit; k0 += 4) {
+      v4i a[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        a[j] = *reinterpret_cast<const v4i*>(base + min(k0 + j, p.ksplit - 1) * plane);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (k0 + j < p.ksplit) s += a[j];
+    }
+    return s;
+  };
   if (GELU) {
     const int N = p.gelu_pair_n;
-    int4 g = make_int4(0, 0, 0, 0), u = make_int4(0, 0, 0, 0);
-    for (int ks = 0; ks < p.ksplit; ++ks) {
-      const int32_t* base = p.partial + ks * plane + row * p.n_total;
-      const int4 a = *reinterpret_cast<const int4*>(base + c);
-      const int4 b = *reinterpret_cast<const int4*>(base + N + c);
-      g.x += a.x; g.y += a.y; g.z += a.z; g.w += a.w;
-      u.x += b.x; u.y += b.y; u.z += b.z; u.w += b.w;
-    }
+    const v4i g = sum_slices(c);
+    const v4i u = sum_slices(N + c);
     const float* swg = reinterpret_cast<const float*>(p.g[0].w + N * scale_off);
     const float* swu = reinterpret_cast<const float*>(p.g[1].w + N * scale_off);
-    const int gv[4] = {g.x, g.y, g.z, g.w};
-    const int uv[4] = {u.x, u.y, u.z, u.w};
+    const int gv[4] = {g[0], g[1], g[2], g[3]};
+    const int uv[4] = {u[0], u[1], u[2], u[3]};
     _Float16* y = static_cast<_Float16*>(p.g[0].y) + row * N + c;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -605,11 +615,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
     }
     return;
   }
-  int4 s = make_int4(0, 0, 0, 0);
-  for (int ks = 0; ks < p.ksplit; ++ks) {
-    const int4 a = *reinterpret_cast<const int4*>(p.partial + ks * plane + row * p.n_total + c);
-    s.x += a.x; s.y += a.y; s.z += a.z; s.w += a.w;
-  }
+  const v4i s = sum_slices(c);
   // locate the group of column c (groups are consecutive in the partial columns)
   const int32_t* W = p.g[0].w;
   void* Y = p.g[0].y;
@@ -629,7 +635,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmParams p) 
   const int col = c - off;
   const float* sw = reinterpret_cast<const float*>(W + N * scale_off);
   _Float16* y = static_cast<_Float16*>(Y) + row * N + col;
-  const int sv[4] = {s.x, s.y, s.z, s.w};
+  const int sv[4] = {s[0], s[1], s[2], s[3]};
   const _Float16* res = p.res != nullptr ? p.res + row * N + col : nullptr;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -671,6 +677,12 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
     // latency (the QKV and o GEMMs of the forward: 11.0 -> 10.1 us each).
     case kCfg2x2: return launch_cfg<2, 2, 4, 1, 3, 2>(p, stream);
     case kCfg1x2: return launch_cfg<1, 2, 4, 1>(p, stream);
+    // Small M: four waves split K with a 4-deep ring (one workgroup streams 32 columns of
+    // weights; at M = 1 the QKV GEMM takes 3.0 us against 5.8 us for 16 x 128 tiles with
+    // a global K split and its reduce launch).
+    case kCfg1x2K4: return launch_cfg<1, 2, 4, 4, 4, 2>(p, stream);
+    case kCfg2x2K4: return launch_cfg<2, 2, 4, 4, 4, 2>(p, stream);
+    case kCfg4x2K4: return launch_cfg<4, 2, 4, 4, 4, 2>(p, stream);
     default: return hipErrorInvalidValue;
   }
 }

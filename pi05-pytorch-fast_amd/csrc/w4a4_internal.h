@@ -101,6 +101,10 @@ enum TileCfg : int {
   kCfg1x2 = 4,    // MI 1, NI 2: 16 x 128
   kCfg7x4K4 = 5,  // MI 7, NI 4, 4 waves along K: 112 x 64
   kCfg7x4K8 = 6,  // MI 7, NI 4, 8 waves along K (2 per SIMD): 112 x 64, for very long K
+  // Small M (weight streaming): 4 waves split K, 32-column tiles (GELU: 16 gate + 16 up).
+  kCfg1x2K4 = 7,  // MI 1: 16 x 32
+  kCfg2x2K4 = 8,  // MI 2: 32 x 32
+  kCfg4x2K4 = 9,  // MI 4: 64 x 32
 };
 
 // Cache warming: up to kMaxWarmBuffers device buffers of n16[i] 16-byte words that a

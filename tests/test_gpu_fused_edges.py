@@ -74,7 +74,7 @@ def test_rmsnorm_quantize_equals_norm_then_quantize_when_norm_matches(ext, cuda)
 
 
 @pytest.mark.parametrize("m,k,n", [(776, 2048, 2048), (776, 16384, 2048), (1, 16384, 2048), (64, 2048, 2048),
-                                   (5, 2048, 256)])
+                                   (5, 2048, 256), (30, 2048, 96), (64, 16384, 2048)])
 def test_gemm_residual_matches_oracle(ext, cuda, m, k, n):
     gen = inp.generator(m + k + n)
     x = inp.activations(gen, m, k) if k == 2048 else inp.geglu_activations(gen, m, k)

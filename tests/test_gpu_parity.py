@@ -152,6 +152,13 @@ GEMM_SHAPES = [
     (776, 2048, 2048),
     (3, 128, 16384),
     (776, 2048, 16384),
+    # small M (the K-split streaming tiles: 16, 32 and 64 rows of 32 columns), ragged N
+    (16, 48, 2048),
+    (17, 2560, 2048),
+    (32, 80, 1024),
+    (48, 2048, 4096),
+    (1, 2048, 16384),
+    (64, 2048, 16384),
 ]
 
 
@@ -226,7 +233,7 @@ def test_int4_gemm2_gate_up(ext, cuda, m):
     _assert_f16_equal(inp.to_np(u), orc.int4_gemm_ref(x.numpy(), wu.numpy()), "up")
 
 
-@pytest.mark.parametrize("m", [776, 64, 1])
+@pytest.mark.parametrize("m", [776, 64, 17, 16, 1])
 def test_int4_gemm2_gelu_matches_unfused(ext, cuda, m):
     gen = inp.generator(300 + m)
     x = inp.activations(gen, m, 2048).to(cuda)
