@@ -131,12 +131,18 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
           *reinterpret_cast<float4*>(&L[addr(t * R + 4 * c)]) =
               make_float4(v[4 * c], v[4 * c + 1], v[4 * c + 2], v[4 * c + 3]);
       } else {
+        // elem(p, t, j) is the OR of disjoint thread bits elem(p, t, 0) and register bits
+        // elem(p, 0, j), and the padded address is linear over such fields, so every
+        // access is one per-thread base plus a compile-time offset (the LDS
+        // instruction's immediate) instead of per-access index arithmetic.
+        float* const wb = L + addr(elem(p - 1, t, 0));
 #pragma unroll
-        for (int j = 0; j < R; ++j) L[addr(elem(p - 1, t, j))] = v[j];
+        for (int j = 0; j < R; ++j) wb[addr(elem(p - 1, 0, j))] = v[j];
       }
       sync();
+      const float* const rb = L + addr(elem(p, t, 0));
 #pragma unroll
-      for (int j = 0; j < R; ++j) v[j] = L[addr(elem(p, t, j))];
+      for (int j = 0; j < R; ++j) v[j] = rb[addr(elem(p, 0, j))];
       sync();
     }
     const int w = (LOGK - p * r) < r ? (LOGK - p * r) : r;

@@ -359,10 +359,12 @@ def _fused_decoder_layer_forward(
                                       unit_offset=off1)
     cos, sin = position_embeddings
     hd = attn.head_dim
-    # The attention launch's idle CUs read the MLP weights into the Infinity Cache for the
-    # gate/up and down GEMMs (PI05_W4A4_CACHE_WARM=0: off).
+    # The attention launch's idle CUs read the o-proj and MLP weights into the Infinity
+    # Cache for the o, gate/up and down GEMMs (PI05_W4A4_CACHE_WARM=0: off).  The next
+    # layer's QKV weights were tried as well: no gain, and the longer warming outlasts the
+    # attention.
     warm = None if os.environ.get("PI05_W4A4_CACHE_WARM", "1") == "0" else [
-        mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed]
+        attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed]
     x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
                                                     q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
                                                     warm=warm)
