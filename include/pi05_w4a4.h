@@ -257,8 +257,8 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
  * (B * KVH * ceil(S * H / KVH / 32) < 256 workgroups) read warm_n <= 4 further device
  * buffers (16-byte aligned, sizes multiples of 16 bytes) and discard the data, so that the
  * kernels after it find them in the Infinity Cache.  No counterpart in the reference: the
- * fused decoder layer passes its MLP weights (gate, up, down), which the gate/up and down
- * GEMMs then read from the cache instead of HBM.  Results are those of
+ * fused decoder layer passes its o-proj and MLP weights (o, gate, up, down), which the o,
+ * gate/up and down GEMMs then read from the cache instead of HBM.  Results are those of
  * pi05w4a4_prefix_attention.
  */
 int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_mfma,

@@ -367,7 +367,7 @@ def _fused_decoder_layer_forward(
         attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed]
     x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
                                                     q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
-                                                    warm=warm)
+                                                    warm=warm, return_out=False)
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)

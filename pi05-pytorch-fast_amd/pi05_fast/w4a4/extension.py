@@ -389,12 +389,13 @@ def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int):
 def _prefix_attention_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
-    quantize_out: bool = False, warm: list[torch.Tensor] | None = None,
+    quantize_out: bool = False, warm: list[torch.Tensor] | None = None, need_out: bool = True,
 ):
     """(out, key states) or, with ``quantize_out`` (one KV head, 8 query heads), (out, key
     states, q codes, scales) of the output rows' K = 2048 activation quant.  ``warm``: up to
     four contiguous device tensors that the attention launch's idle workgroups read into
-    the Infinity Cache (``pi05w4a4_prefix_attention_warm``)."""
+    the Infinity Cache (``pi05w4a4_prefix_attention_warm``).  ``need_out=False`` (with
+    ``quantize_out``): the fp16 output is not written and an empty tensor is returned."""
     d = ATTN_HEAD_DIM
     for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if not t.is_cuda:
@@ -414,7 +415,10 @@ def _prefix_attention_impl(
     lib = load_int4_gemm()
     k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
     kv_mfma = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
-    out = torch.empty((b, s, h * d), dtype=torch.float16, device=q.device)
+    if not (need_out or quantize_out):
+        raise RuntimeError("prefix_attention: the output can only be dropped when it is quantized")
+    out = torch.empty((b, s, h * d) if need_out else (0,), dtype=torch.float16, device=q.device)
+    out_ptr = _ptr(out) if need_out else None
     codes = scales = None
     if quantize_out:
         codes = torch.empty((int(lib.pi05w4a4_q_words(b * s, h * d)),), dtype=torch.int32, device=q.device)
@@ -431,12 +435,12 @@ def _prefix_attention_impl(
             wb = (ctypes.c_size_t * len(ws))(*[(t.numel() * t.element_size()) // 16 * 16 for t in ws])
             _check(lib.pi05w4a4_prefix_attention_warm(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
                                                       _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
-                                                      _ptr(out), h * d, _ptr(codes), _ptr(scales), wp, wb, len(ws),
+                                                      out_ptr, h * d, _ptr(codes), _ptr(scales), wp, wb, len(ws),
                                                       st), "pi05w4a4_prefix_attention_warm")
         else:
             _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
                                                  _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
-                                                 _ptr(out), h * d, _ptr(codes), _ptr(scales), st),
+                                                 out_ptr, h * d, _ptr(codes), _ptr(scales), st),
                    "pi05w4a4_prefix_attention")
     if quantize_out:
         return out, k_rope, codes, scales
@@ -444,17 +448,20 @@ def _prefix_attention_impl(
 
 
 def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual,
-                                  warm=None):
+                                  warm=None, return_out=True):
     """RoPE + attention + o_proj + residual add: with one KV head and 8 query heads of 256
     the attention kernel quantizes its own output rows for the o GEMM; otherwise the output
-    goes through the separate quantizer.  Returns (residual + o_proj(out), key states, out)."""
+    goes through the separate quantizer.  Returns (residual + o_proj(out), key states, out);
+    with ``return_out=False`` and the in-kernel quant, out is not written (an empty
+    tensor)."""
     k_in = ATTN_HEAD_DIM * int(num_heads)
     _check_packed(w_o, k_in, "o_proj weight")
     w, n_true = _as_mfma(w_o, k_in, tiled=False)
     lead = tuple(q.shape[:-1])
     if int(num_kv_heads) == 1 and k_in == 2048:
         out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
-                                                            num_kv_heads, quantize_out=True, warm=warm)
+                                                            num_kv_heads, quantize_out=True, warm=warm,
+                                                            need_out=return_out)
         with torch.cuda.device(q.device):
             y = _gemm_from_q(codes, scales, k_in, [(w, n_true)], lead, q.device, "int4_gemm", residual=residual)[0]
         return y, k_rope, out
@@ -598,16 +605,18 @@ def _register_custom_op() -> None:
     def _prefix_attention_o_proj(
         q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
         mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
-        w_o: torch.Tensor, residual: torch.Tensor, warm: list[torch.Tensor],
+        w_o: torch.Tensor, residual: torch.Tensor, warm: list[torch.Tensor], return_out: bool,
     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         return _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o,
-                                             residual, warm)
+                                             residual, warm, return_out)
 
     @_prefix_attention_o_proj.register_fake
-    def _prefix_attention_o_proj_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm):
+    def _prefix_attention_o_proj_fake(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm,
+                                      return_out):
         b, s = q.shape[0], q.shape[1]
+        dropped = not return_out and num_kv_heads == 1 and num_heads * ATTN_HEAD_DIM == 2048
         return (q.new_empty((b, s, w_o.shape[0])), q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM)),
-                q.new_empty((b, s, num_heads * ATTN_HEAD_DIM)))
+                q.new_empty((0,) if dropped else (b, s, num_heads * ATTN_HEAD_DIM)))
 
     _op_registered = True
 
@@ -704,15 +713,19 @@ def prefix_attention(
                                                 int(num_kv_heads))
 
 
-def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm=None):
+def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual, warm=None,
+                            return_out=True):
     """residual + o_proj(attention(q, k, v)) of a prefix forward, plus the RoPE'd key
     states and the attention output: ``prefix_attention`` followed by
     ``int4_gemm_residual``, with the o-proj activation quant done inside the attention
     kernel when the layer has one KV head and 8 query heads of 256 (PaliGemma).  ``warm``:
     up to four weight tensors of the following ops that the attention launch's idle CUs
-    read into the Infinity Cache (results unchanged)."""
+    read into the Infinity Cache (results unchanged).  ``return_out=False``: a caller that
+    does not use the attention output gets an empty tensor in its place, and the kernel
+    skips writing it when it quantizes the output itself."""
     return torch.ops.pi05_w4a4.prefix_attention_o_proj(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
-                                                       int(num_kv_heads), w_o, residual, list(warm or []))
+                                                       int(num_kv_heads), w_o, residual, list(warm or []),
+                                                       bool(return_out))
 
 
 def preload() -> None:

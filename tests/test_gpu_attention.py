@@ -337,3 +337,10 @@ def test_prefix_attention_cache_warm_changes_nothing(ext, cuda, b, s, h, kvh):
         assert torch.equal(a, c)
     for t, t0 in zip(big, keep):
         assert torch.equal(t, t0)
+    # a caller that does not use the attention output: the kernel skips writing it
+    with torch.no_grad():
+        lean = ext.prefix_attention_o_proj(q, k, v, cos, sin, mask, D**-0.5, h, kvh, w_o, res, warm=big,
+                                           return_out=False)
+    torch.cuda.synchronize()
+    assert torch.equal(lean[0], plain[0]) and torch.equal(lean[1], plain[1])
+    assert lean[2].numel() == (0 if kvh == 1 and h == 8 else plain[2].numel())

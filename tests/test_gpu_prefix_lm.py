@@ -95,6 +95,10 @@ def _check_call(cuda, i, call) -> None:
         # the o projection of the attention output it returned (quantized inside the kernel)
         w_o, res = args[9], args[10]
         x2, out = outs[0], outs[2]
+        if out.numel() == 0:  # the fused layer drops the attention output: recompute it
+            from pi05_fast.w4a4 import extension as ext
+
+            out = ext.prefix_attention(*args[:9])[0]
         k = out.shape[-1]
         want = _oracle_h(out.reshape(-1, k).cpu().numpy(), w_o, k)
         want = (want.astype(np.float32) + res.reshape(want.shape).cpu().numpy().astype(np.float32)).astype(np.float16)
