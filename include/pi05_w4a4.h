@@ -77,6 +77,18 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
                       void* stream);
 
 /*
+ * pi05w4a4_quantize plus cache warming: at K = 16384 (one 68 KB workgroup per row, two per
+ * CU) the workgroup slots that the last round of rows leaves idle read warm_n <= 4 further
+ * device buffers (16-byte aligned, sizes multiples of 16 bytes) and discard the data, so
+ * that the kernels after it find them in the Infinity Cache; other K ignore the buffers.
+ * No counterpart in the reference: the fused decoder layer passes the down-proj weights
+ * with the quantization of the down-proj input.  Results are those of pi05w4a4_quantize.
+ */
+int pi05w4a4_quantize_warm(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                           const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                           void* stream);
+
+/*
  * Words of a quantized-activation buffer q for M rows of K codes:
  * ceil(M/16)*16 * ceil(K/128)*16 code words + ceil(M/16)*16 qcorr words.
  * (The reference keeps row-major [M, K/8] codes inside its QuantizedX, int4_gemm.cu:479-485.)

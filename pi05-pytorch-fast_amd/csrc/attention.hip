@@ -42,6 +42,7 @@
 // memory path, about 64 B per clock, ~13k clocks at 776 keys; the softmax is VALU work
 // (a wave64 VALU instruction occupies its SIMD for 4 clocks).
 
+#include "cache_warm.h"
 #include "quant_row.h"
 
 namespace w4a4 {
@@ -148,30 +149,6 @@ __global__ __launch_bounds__(256) void kv_prep_kernel(const AttnParams p) {
   }
 }
 
-// Cache warming by the workgroups past the query row blocks: `part` of `nparts` slices of
-// the buffers, 8 loads of 16 bytes in flight per thread; the data feed an empty asm.
-__device__ __forceinline__ void cache_warm_part(const CacheWarmParams& w, int64_t part, int64_t nparts, int tid) {
-  constexpr int kLoads = 8;
-  const int64_t stride = nparts * kThreads * kLoads;
-  uint32_t acc = 0;
-#pragma unroll 1
-  for (int bi = 0; bi < w.nbuf; ++bi) {
-    const uint4* src = static_cast<const uint4*>(w.ptr[bi]);
-    const int64_t n = w.n16[bi];
-    for (int64_t base = part * kThreads * kLoads + tid; base < n; base += stride) {
-      uint4 v[kLoads];
-#pragma unroll
-      for (int i = 0; i < kLoads; ++i) {
-        const int64_t idx = base + static_cast<int64_t>(i) * kThreads;
-        v[i] = idx < n ? src[idx] : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < kLoads; ++i) acc ^= v[i].x ^ v[i].y ^ v[i].z ^ v[i].w;
-    }
-  }
-  asm volatile("" ::"v"(acc));
-}
-
 // ---- attention.  Grid (ceil(S * n_rep / 32) + warm, KVH, B), 512 threads (8 waves).
 // SCH = 8-key chunks per thread in the softmax phase (s_pad <= 128 * SCH).
 template <int SCH>
@@ -183,7 +160,7 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   const int tid = threadIdx.x;
   if (static_cast<int>(blockIdx.x) >= p.row_blocks) {  // a cache-warming workgroup
     const int64_t wx = gridDim.x - p.row_blocks;
-    cache_warm_part(p.warm, (static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y) * wx + (blockIdx.x - p.row_blocks),
+    cache_warm_part<kThreads>(p.warm, (static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y) * wx + (blockIdx.x - p.row_blocks),
                     wx * gridDim.y * gridDim.z, tid);
     return;
   }

@@ -236,8 +236,30 @@ int pi05w4a4_version(void) { return 100; }
 
 const char* pi05w4a4_last_error(void) { return g_last_error.c_str(); }
 
-int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
-                      void* stream) {
+namespace {
+
+// Validates the warm-buffer arguments of the cache-warming entry points and collects the
+// non-empty buffers.
+int collect_warm(const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                 w4a4::CacheWarmParams* warm) {
+  *warm = w4a4::CacheWarmParams{};
+  if (warm_n < 0 || warm_n > w4a4::kMaxWarmBuffers)
+    return fail(PI05W4A4_EINVAL, "cache warming takes 0..%d buffers, got %d", w4a4::kMaxWarmBuffers, warm_n);
+  if (warm_n > 0 && (warm_ptrs == nullptr || warm_bytes == nullptr))
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  for (int i = 0; i < warm_n; ++i) {
+    if (warm_ptrs[i] == nullptr || !aligned(warm_ptrs[i], 16) || warm_bytes[i] % 16 != 0)
+      return fail(PI05W4A4_EINVAL, "warm buffer %d must be non-null, 16-byte aligned and a multiple of 16 bytes", i);
+    if (warm_bytes[i] == 0) continue;
+    warm->ptr[warm->nbuf] = warm_ptrs[i];
+    warm->n16[warm->nbuf] = static_cast<int64_t>(warm_bytes[i] / 16);
+    ++warm->nbuf;
+  }
+  return ok();
+}
+
+int quantize_call(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                  const w4a4::CacheWarmParams* warm, void* stream) {
   if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
   if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
   if (m == 0) return ok();
@@ -248,8 +270,24 @@ int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, floa
   if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
   const float inv_sqrt_k = static_cast<float>(1.0 / std::sqrt(static_cast<double>(k)));
   return hip_status(w4a4::launch_quantize(x_fp16, m, k, q, sa, inv_sqrt_k,
-                                          static_cast<hipStream_t>(stream)),
+                                          static_cast<hipStream_t>(stream), warm),
                     "quantize launch");
+}
+
+}  // namespace
+
+int pi05w4a4_quantize(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                      void* stream) {
+  return quantize_call(x_fp16, m, k, q, sa, nullptr, stream);
+}
+
+int pi05w4a4_quantize_warm(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+                           const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                           void* stream) {
+  w4a4::CacheWarmParams warm;
+  const int rc = collect_warm(warm_ptrs, warm_bytes, warm_n, &warm);
+  if (rc) return rc;
+  return quantize_call(x_fp16, m, k, q, sa, &warm, stream);
 }
 
 size_t pi05w4a4_q_words(int64_t m, int32_t k) {
@@ -534,19 +572,9 @@ int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_m
                                    int64_t ld_out, int32_t* q_codes, float* q_scales,
                                    const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
                                    void* stream) {
-  if (warm_n < 0 || warm_n > w4a4::kMaxWarmBuffers)
-    return fail(PI05W4A4_EINVAL, "cache warming takes 0..%d buffers, got %d", w4a4::kMaxWarmBuffers, warm_n);
-  if (warm_n > 0 && (warm_ptrs == nullptr || warm_bytes == nullptr))
-    return fail(PI05W4A4_EINVAL, "null pointer argument");
-  w4a4::CacheWarmParams warm{};
-  for (int i = 0; i < warm_n; ++i) {
-    if (warm_ptrs[i] == nullptr || !aligned(warm_ptrs[i], 16) || warm_bytes[i] % 16 != 0)
-      return fail(PI05W4A4_EINVAL, "warm buffer %d must be non-null, 16-byte aligned and a multiple of 16 bytes", i);
-    if (warm_bytes[i] == 0) continue;
-    warm.ptr[warm.nbuf] = warm_ptrs[i];
-    warm.n16[warm.nbuf] = static_cast<int64_t>(warm_bytes[i] / 16);
-    ++warm.nbuf;
-  }
+  w4a4::CacheWarmParams warm;
+  const int rc = collect_warm(warm_ptrs, warm_bytes, warm_n, &warm);
+  if (rc) return rc;
   return prefix_attention_call(q, ld_q, kv_mfma, cos_fp16, sin_fp16, mask, mask_bs, mask_rs, mask_len, scaling, b,
                                s, h, kvh, d, out, ld_out, q_codes, q_scales, warm, stream);
 }

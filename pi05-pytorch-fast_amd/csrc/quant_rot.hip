@@ -23,6 +23,7 @@
 // Each stage writes (a + b, a - b) for the pair (i, i + h) exactly as the fp32 CPU
 // transform does, so the rotated values are bit-identical to it.
 
+#include "cache_warm.h"
 #include "quant_row.h"
 
 namespace w4a4 {
@@ -175,11 +176,19 @@ template <int LOGK, int LOGT, int ROWS, bool NORM = false>
 __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     const _Float16* __restrict__ x, int64_t m, int32_t* __restrict__ q, float* __restrict__ sa,
     int32_t* __restrict__ qcorr, float inv_sqrt_k, const _Float16* __restrict__ nw = nullptr,
-    float eps = 0.0f, int unit_offset = 0) {
+    float eps = 0.0f, int unit_offset = 0, const CacheWarmParams warm = CacheWarmParams{}) {
   constexpr int K = 1 << LOGK;
   constexpr int T = 1 << LOGT;
   constexpr int R = 1 << (LOGK - LOGT);
   static_assert(T == 64 || ROWS == 1, "rows of more than one wave need a workgroup per row");
+  // Workgroups past the rows (launched only with warm buffers) warm the cache and leave.
+  {
+    const int64_t row_blocks = (m + ROWS - 1) / ROWS;
+    if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
+      cache_warm_part<(ROWS << LOGT)>(warm, blockIdx.x - row_blocks, gridDim.x - row_blocks, threadIdx.x);
+      return;
+    }
+  }
   constexpr int LROW = K + 4 * (K / R);  // LDS floats per row (4 pad floats per R)
   // One wave per row (T == 64) runs in registers only (fwht_quant_row_wave).
   __shared__ __align__(16) float lds[T == 64 ? 1 : ROWS * LROW];
@@ -273,15 +282,22 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
 }  // namespace
 
 hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, float* sa,
-                           float inv_sqrt_k, hipStream_t stream) {
+                           float inv_sqrt_k, hipStream_t stream, const CacheWarmParams* warm) {
   if (m <= 0) return hipSuccess;
   const _Float16* xh = static_cast<const _Float16*>(x);
   int32_t* qcorr = q + q_payload_words((m + 15) / 16, kblocks128(k));
   const dim3 grid(static_cast<unsigned>(m));
   switch (k) {
-    case 16384:
-      fwht_quant_kernel<14, 8, 1><<<grid, 256, 0, stream>>>(xh, m, q, sa, qcorr, inv_sqrt_k);
+    case 16384: {
+      // Cache warming fills the slots that the last round of rows leaves idle (68 KB of LDS
+      // per row: two workgroups per CU, 512 slots on the 256 CUs).
+      constexpr int64_t kSlots = 2 * 256;
+      const int64_t tail = m % kSlots;
+      const int64_t extra = (warm != nullptr && warm->nbuf > 0 && tail != 0) ? kSlots - tail : 0;
+      fwht_quant_kernel<14, 8, 1><<<dim3(static_cast<unsigned>(m + extra)), 256, 0, stream>>>(
+          xh, m, q, sa, qcorr, inv_sqrt_k, nullptr, 0.0f, 0, extra > 0 ? *warm : CacheWarmParams{});
       break;
+    }
     case 2048:
       fwht_quant_kernel<11, 6, 4><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
           xh, m, q, sa, qcorr, inv_sqrt_k);

@@ -150,7 +150,7 @@ int64_t attn_s_pad(int32_t s);
 
 // Launchers (return hipError_t of the launch).
 hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, float* sa,
-                           float inv_sqrt_k, hipStream_t stream);
+                           float inv_sqrt_k, hipStream_t stream, const CacheWarmParams* warm = nullptr);
 hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t k,
                          int64_t src_stride, int32_t* dst, hipStream_t stream);
 // Chooses the tile configuration; returns the K split used (>= 1) through *ksplit_out.

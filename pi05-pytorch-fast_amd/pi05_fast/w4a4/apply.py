@@ -359,12 +359,12 @@ def _fused_decoder_layer_forward(
                                       unit_offset=off1)
     cos, sin = position_embeddings
     hd = attn.head_dim
-    # The attention launch's idle CUs read the o-proj and MLP weights into the Infinity
-    # Cache for the o, gate/up and down GEMMs (PI05_W4A4_CACHE_WARM=0: off).  The next
-    # layer's QKV weights were tried as well: no gain, and the longer warming outlasts the
-    # attention.
-    warm = None if os.environ.get("PI05_W4A4_CACHE_WARM", "1") == "0" else [
-        attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed]
+    # Cache warming (PI05_W4A4_CACHE_WARM=0: off): the attention launch's idle CUs read the
+    # o-proj, gate and up weights into the Infinity Cache, and the down-proj input quant's
+    # idle workgroup slots the down-proj weights.  The next layer's QKV weights were tried
+    # as well: no gain, and the longer warming outlasts the attention.
+    warming = os.environ.get("PI05_W4A4_CACHE_WARM", "1") != "0"
+    warm = [attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed] if warming else None
     x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
                                                     q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
                                                     warm=warm, return_out=False)
@@ -372,7 +372,7 @@ def _fused_decoder_layer_forward(
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)
     h = ext.rms_norm_int4_gemm2_gelu(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, unit_offset=off2)
-    return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2)
+    return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2, warm=[mlp.down_proj.packed] if warming else None)
 
 
 def fuse_decoder_layers(model: nn.Module) -> int:

@@ -63,6 +63,8 @@ def load_int4_gemm():
         "pi05w4a4_version": (ctypes.c_int, []),
         "pi05w4a4_last_error": (ctypes.c_char_p, []),
         "pi05w4a4_quantize": (ctypes.c_int, [vp, i64, i32, vp, vp, vp]),
+        "pi05w4a4_quantize_warm": (ctypes.c_int, [vp, i64, i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(sz),
+                                                  i32, vp]),
         "pi05w4a4_q_words": (sz, [i64, i32]),
         "pi05w4a4_mfma_words": (sz, [i32, i32]),
         "pi05w4a4_repack_weight": (ctypes.c_int, [vp, i32, i32, i32, i64, vp, vp]),
@@ -163,7 +165,19 @@ def is_mfma_layout(w: torch.Tensor, k: int) -> bool:
 
 
 # ----------------------------------------------------------------------------- pieces
-def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+def _warm_args(warm, who: str):
+    """(pointer array, byte-size array, count) of the non-empty warm tensors, or None."""
+    ws = [t for t in (warm or []) if t is not None and t.numel() > 0]
+    if not ws:
+        return None
+    if len(ws) > 4 or any((not t.is_cuda) or (not t.is_contiguous()) for t in ws):
+        raise RuntimeError(f"{who}: warm takes up to 4 contiguous CUDA/HIP tensors")
+    wp = (ctypes.c_void_p * len(ws))(*[t.data_ptr() for t in ws])
+    wb = (ctypes.c_size_t * len(ws))(*[(t.numel() * t.element_size()) // 16 * 16 for t in ws])
+    return wp, wb, len(ws)
+
+
+def quantize(x: torch.Tensor, warm: list[torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Fused FWHT + per-token INT4 quant + nibble pack (the reference's quantize_x,
     int4_gemm.cu:496-531): x fp16 [..., K] -> (q, sa fp32 [M]).
 
@@ -182,8 +196,12 @@ def quantize(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
     lib = load_int4_gemm()
     with torch.cuda.device(x2.device):
-        rc = lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device))
-        _check(rc, "pi05w4a4_quantize")
+        wa = _warm_args(warm, "quantize")
+        if wa is None:
+            _check(lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device)), "pi05w4a4_quantize")
+        else:
+            _check(lib.pi05w4a4_quantize_warm(_ptr(x2), m, k, _ptr(q), _ptr(sa), *wa, _stream(x2.device)),
+                   "pi05w4a4_quantize_warm")
     return q, sa
 
 
@@ -304,10 +322,10 @@ def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
 
 
 def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False,
-         norm=None, residual=None):
+         norm=None, residual=None, warm=None):
     k = _check_x(x)
     # the reference quantizes before checking the weights
-    q, sa = quantize(x) if norm is None else rms_norm_quantize(x, *norm)
+    q, sa = quantize(x, warm) if norm is None else rms_norm_quantize(x, *norm)
     conv = []
     for w in ws:
         _check_packed(w, k)
@@ -580,11 +598,12 @@ def _register_custom_op() -> None:
         return _fake_out(x, w_gate)
 
     @torch.library.custom_op("pi05_w4a4::int4_gemm_residual", mutates_args=())
-    def _int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
-        return _run(x, [packed_w], tiled=False, kind="int4_gemm", residual=residual)[0]
+    def _int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor,
+                            warm: list[torch.Tensor]) -> torch.Tensor:
+        return _run(x, [packed_w], tiled=False, kind="int4_gemm", residual=residual, warm=warm)[0]
 
     @_int4_gemm_residual.register_fake
-    def _int4_gemm_residual_fake(x, packed_w, residual):
+    def _int4_gemm_residual_fake(x, packed_w, residual, warm):
         return _fake_out(x, packed_w)
 
     # Not in the reference: RoPE + attention between int4_gemm3 and o_proj in two kernels.
@@ -692,10 +711,14 @@ def rms_norm_int4_gemm2_gelu(x, norm_weight, eps, w_gate, w_up, unit_offset=True
                                                         w_gate, w_up)
 
 
-def int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor) -> torch.Tensor:
+def int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor,
+                       warm: list[torch.Tensor] | None = None) -> torch.Tensor:
     """residual + int4_gemm(x, packed_w), the add done in the GEMM epilogue with the
-    rounding of the eager fp16 add (MFMA-layout or row-major weights, N % 16 == 0)."""
-    return torch.ops.pi05_w4a4.int4_gemm_residual(x, packed_w, residual)
+    rounding of the eager fp16 add (MFMA-layout or row-major weights, N % 16 == 0).
+    ``warm``: up to four device tensors that the K = 16384 activation quant's idle
+    workgroup slots read into the Infinity Cache (``pi05w4a4_quantize_warm``; results
+    unchanged)."""
+    return torch.ops.pi05_w4a4.int4_gemm_residual(x, packed_w, residual, list(warm or []))
 
 
 def prefix_attention(

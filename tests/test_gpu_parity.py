@@ -89,6 +89,26 @@ def test_quantize_matches_oracle(ext, cuda, m, k, kind):
     assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32)), "scale bits differ"
 
 
+@pytest.mark.parametrize("m", [776, 100, 512, 1])
+def test_quantize_cache_warm_changes_nothing(ext, cuda, m):
+    """The K = 16384 quantizer with cache warming (the slots the last round of rows leaves
+    idle read further buffers: here 48 MB) writes the same codes and scales as the plain
+    call and leaves the buffers it read unchanged; at M = 512 no slot is idle."""
+    gen = inp.generator(40 + m)
+    x = inp.geglu_activations(gen, m, 16384).to(cuda)
+    big = [torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=cuda) for n in (4 << 20,) * 3]
+    keep = [t.clone() for t in big]
+    q0, s0 = ext.quantize(x)
+    q1, s1 = ext.quantize(x, warm=big)
+    torch.cuda.synchronize()
+    # rows past M (the 16-row padding of the buffer) are never written: compare M rows
+    c0, c1 = _codes(q0, m, 16384), _codes(q1, m, 16384)
+    assert np.array_equal(c0, c1) and torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+    _assert_qcorr(q1, c1, "warm")
+    for t, t0 in zip(big, keep):
+        assert torch.equal(t, t0)
+
+
 @pytest.mark.parametrize("k", [2048, 16384])
 def test_quantize_exact_ties(ext, cuda, k):
     """Rows whose rotated values hit exact half-integer multiples of the scale: the GPU's

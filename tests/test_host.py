@@ -316,6 +316,18 @@ def test_attention_abi_validation_without_gpu(lib):
     assert warm([p], [1000]) == 1 and "multiple of 16" in _err(lib)
     assert warm([p], [1024], ld_q=1024) == 1 and "token stride" in _err(lib)
 
+    # the quantizer's cache-warming variant: the same buffer rules, then the quantize ones
+    def qwarm(ptrs, sizes, k=16384, x=p):
+        arr = (vp * max(len(ptrs), 1))(*ptrs)
+        sz = (ctypes.c_size_t * max(len(sizes), 1))(*sizes)
+        return lib.pi05w4a4_quantize_warm(x, 776, k, p, p, arr, sz, len(ptrs), vp(0))
+
+    assert qwarm([p] * 5, [16] * 5) == 1 and "0..4 buffers" in _err(lib)
+    assert qwarm([vp(264)], [1024]) == 1 and "16-byte aligned" in _err(lib)
+    assert qwarm([p], [1000]) == 1 and "multiple of 16" in _err(lib)
+    assert qwarm([p], [1024], k=100) == 1 and "multiple of 64" in _err(lib)
+    assert qwarm([p], [1024], x=vp(0)) == 1 and "null" in _err(lib)
+
 
 # ----------------------------------------------------------------------------- op surface
 def test_custom_ops_registered_with_fakes():
