@@ -586,9 +586,10 @@ def main() -> int:
             "layers": args.layers,
             "timed": "hip-graph replay" if not args.no_graph else "eager",
             "fused_gelu_up": not args.unfused_gelu,
-            # the attention launch's idle CUs pre-read each layer's MLP weights from HBM into
-            # the Infinity Cache, inside the timed forward
-            "mlp_weight_cache_warm": os.environ.get("PI05_W4A4_CACHE_WARM", "1") != "0",
+            # idle CUs pre-read weights from HBM into the Infinity Cache inside the timed
+            # forward: the attention launch each layer's o/gate/up weights, the K=16384
+            # quant launch its down weights
+            "weight_cache_warm": os.environ.get("PI05_W4A4_CACHE_WARM", "1") != "0",
             "attention": "prefix-attention kernels (fp16, eager-attention semantics); "
                          "forward_points has the eager-attention forward",
             "graph_replay_bit_exact_vs_eager": graph_exact,
