@@ -198,12 +198,6 @@ def unshuffle_wmma_weight(tiled: np.ndarray, k: int) -> np.ndarray:
     return np.concatenate([payload, flat[n * words : n * words + n, None]], axis=1)
 
 
-def pad_rows(packed: np.ndarray, pad_words: int) -> np.ndarray:
-    """Layout L2: L1 with pad_words-1 zero words appended per row (apply.py:68-69)."""
-    packed = np.asarray(packed, dtype=np.int32)
-    return np.pad(packed, ((0, 0), (0, pad_words - 1)))
-
-
 def gelu_tanh(x: np.ndarray) -> np.ndarray:
     """GELU, tanh approximation, in float64 (transformers GELUTanh = F.gelu(approximate='tanh'))."""
     x = np.asarray(x, dtype=np.float64)
@@ -220,16 +214,21 @@ def gelu_tanh_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
 def rms_norm_lanes(x: np.ndarray, weight: np.ndarray, eps: float, unit_offset: bool = True,
                    lanes: int = 64) -> np.ndarray:
     """GemmaRMSNorm (transformers modeling_gemma.py:64-78: fp32 inside, (1 + w), fp16
-    out) in the fp32 summation order of the fused RMSNorm + quant kernel, so that the fp16
-    rows it returns are the ones that kernel rotates and quantizes, bit for bit:
-    lane l sums x^2 over elements l*K/lanes .. (l+1)*K/lanes - 1 in order, the lanes are
-    combined by the butterfly p[l] += p[l ^ o] for o = lanes/2, .., 1, and
-    h = fp16((x * r) * g) with r = 1 / sqrt(ss * (1/K) + eps) (each op one fp32 rounding)
-    and g = 1 + w (unit_offset) or w.  x fp16 [M, K], weight fp16 [K]."""
+    out) in the fp32 summation order of the RMSNorm kernels (the standalone one and the
+    one fused into the K = 2048 activation quant), so that the fp16 rows it returns are
+    the ones those kernels write or rotate and quantize, bit for bit:
+    lane l sums x^2 over its R = 8 * ceil(K / (8 * lanes)) consecutive elements
+    l*R .. min((l+1)*R, K) - 1 in order, the lanes are combined by the butterfly
+    p[l] += p[l ^ o] for o = lanes/2, .., 1, and h = fp16((x * r) * g) with
+    r = 1 / sqrt(ss * fp32(1/K) + eps) (each op one fp32 rounding) and g = 1 + w
+    (unit_offset) or w.  x fp16 [M, K], weight fp16 [K], K a multiple of 8."""
     v = np.asarray(x, dtype=np.float16).astype(np.float32)
     m, k = v.shape
-    r_len = k // lanes
-    sq = v * v
+    if k % 8:
+        raise ValueError(f"K must be a multiple of 8, got {k}")
+    r_len = 8 * (-(-(k // 8) // lanes))
+    sq = np.zeros((m, lanes * r_len), dtype=np.float32)
+    sq[:, :k] = v * v  # elements past K add +0.0, which leaves every fp32 partial sum unchanged
     part = np.zeros((m, lanes), dtype=np.float32)
     per_lane = sq.reshape(m, lanes, r_len)
     for j in range(r_len):

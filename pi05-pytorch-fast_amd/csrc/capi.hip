@@ -7,6 +7,7 @@
 // the quantized-activation buffers and the split-K workspace.
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -14,6 +15,25 @@
 
 #include "../../include/pi05_w4a4.h"
 #include "w4a4_internal.h"
+
+namespace w4a4 {
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) dev = 0;
+  const int slot = dev < kMaxDevices ? dev : kMaxDevices - 1;
+  int n = cached[slot].load(std::memory_order_relaxed);
+  if (n > 0 && dev < kMaxDevices) return n;
+  n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;  // no device to ask (host-only callers): a whole MI355X
+  if (dev < kMaxDevices) cached[slot].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+}  // namespace w4a4
 
 namespace {
 
@@ -43,8 +63,6 @@ int hip_status(hipError_t e, const char* what) {
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
-constexpr int kNumCUs = 256;  // MI355X: 8 XCDs x 32 CUs
 
 struct TileCfg {
   int id, mi, ni, nwaves, kw;  // kw of the nwaves waves of a workgroup split K
@@ -85,6 +103,7 @@ struct Plan {
 //    along-N tiles with the global split above that.
 Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
   Plan pl{};
+  const int64_t kNumCUs = w4a4::device_cu_count();
   // The GELU pairing's 16-column K-split tiles make 1024 workgroups at gate/up size, each
   // staging the GELU correction table: from M = 17 on the wider tiles are faster.
   const bool stream_k = m <= 16 || (!gelu && m <= 64);

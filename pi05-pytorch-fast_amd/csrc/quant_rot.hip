@@ -290,8 +290,8 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
   switch (k) {
     case 16384: {
       // Cache warming fills the slots that the last round of rows leaves idle (68 KB of LDS
-      // per row: two workgroups per CU, 512 slots on the 256 CUs).
-      constexpr int64_t kSlots = 2 * 256;
+      // per row: two workgroups per CU).
+      const int64_t kSlots = 2 * static_cast<int64_t>(device_cu_count());
       const int64_t tail = m % kSlots;
       const int64_t extra = (warm != nullptr && warm->nbuf > 0 && tail != 0) ? kSlots - tail : 0;
       fwht_quant_kernel<14, 8, 1><<<dim3(static_cast<unsigned>(m + extra)), 256, 0, stream>>>(

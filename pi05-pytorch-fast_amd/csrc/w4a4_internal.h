@@ -148,6 +148,11 @@ struct AttnParams {
 };
 int64_t attn_s_pad(int32_t s);
 
+// Compute units of the current device (hipDeviceAttributeMultiprocessorCount, queried
+// once per device and cached; 256 on a whole MI355X, fewer on a partitioned one).  The
+// tile planner, the cache-warming launches and the attention grid size their work by it.
+int device_cu_count();
+
 // Launchers (return hipError_t of the launch).
 hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, float* sa,
                            float inv_sqrt_k, hipStream_t stream, const CacheWarmParams* warm = nullptr);

@@ -252,7 +252,8 @@ def _fused_attn_forward(
         self.v_proj.packed,
     )
     cos, sin = position_embeddings
-    if _prefix_attention_fits(self, q, k, attention_mask, past_key_values):
+    if (cos.dtype == torch.float16 and sin.dtype == torch.float16
+            and _prefix_attention_fits(self, q, k, attention_mask, past_key_values)):
         from pi05_fast.w4a4.extension import prefix_attention
 
         out, key_states = prefix_attention(
@@ -292,12 +293,13 @@ def _fused_attn_forward(
 
 
 def _norm_parts(norm) -> tuple[torch.Tensor, float, bool] | None:
-    """(fp16 weight, eps, unit_offset) of a Gemma RMSNorm module (transformers'
-    GemmaRMSNorm or norm.FusedRMSNorm), or None."""
+    """(weight, eps, unit_offset) of a Gemma RMSNorm module (transformers' GemmaRMSNorm
+    or norm.FusedRMSNorm) with a 1-D weight, or None.  The weight's dtype and device are
+    checked per call (``_norms_fit``)."""
     from pi05_fast.w4a4.norm import FusedRMSNorm
 
     w = getattr(norm, "weight", None)
-    if not isinstance(w, torch.Tensor) or w.dtype != torch.float16 or not w.is_cuda or w.dim() != 1:
+    if not isinstance(w, torch.Tensor) or w.dim() != 1:
         return None
     if isinstance(norm, FusedRMSNorm):
         return w, norm.eps, norm.unit_offset
@@ -306,10 +308,17 @@ def _norm_parts(norm) -> tuple[torch.Tensor, float, bool] | None:
     return None
 
 
+def _norms_fit(parts, x: torch.Tensor) -> bool:
+    """Whether the fused norm + quant kernels can take these norms for input x: fp16
+    weights on x's device."""
+    return all(p is not None and p[0].dtype == torch.float16 and p[0].device == x.device for p in parts)
+
+
 def _decoder_layer_fits(layer) -> bool:
     """A Gemma decoder layer whose seven projections are bias-free MFMA-layout W4A4 layers,
     whose MLP uses the fused GELU-tanh*up epilogue and whose norms are Gemma RMSNorms over
-    2048 features."""
+    2048 features.  Structure only: dtypes are checked per call, so a model that is cast to
+    fp16 after the pack is applied (rocm_pi05_optim.py:231-237) runs the fused layer."""
     attn, mlp = getattr(layer, "self_attn", None), getattr(layer, "mlp", None)
     if attn is None or mlp is None or not getattr(mlp, "_w4a4_fuse_gelu", False):
         return False
@@ -342,19 +351,21 @@ def _fused_decoder_layer_forward(
 
     attn, mlp = self.self_attn, self.mlp
     x = hidden_states
+    norms = (_norm_parts(self.input_layernorm), _norm_parts(self.post_attention_layernorm))
     if not (
         x.dtype == torch.float16
         and x.dim() == 3
         and x.is_contiguous()
         and position_embeddings is not None
+        and all(t.dtype == torch.float16 for t in position_embeddings)
+        and _norms_fit(norms, x)
         and _attention_call_fits(attn, (x.size(0), x.size(1), attn.q_proj.out_features),
                                  attn.k_proj.out_features, x.dtype, x.is_cuda, attention_mask, past_key_values)
     ):
         return self._w4a4_layer_forward(hidden_states, attention_mask=attention_mask, position_ids=position_ids,
                                         past_key_values=past_key_values, use_cache=use_cache,
                                         position_embeddings=position_embeddings, **kwargs)
-    w1, eps1, off1 = _norm_parts(self.input_layernorm)
-    w2, eps2, off2 = _norm_parts(self.post_attention_layernorm)
+    (w1, eps1, off1), (w2, eps2, off2) = norms
     q, k, v = ext.rms_norm_int4_gemm3(x, w1, eps1, attn.q_proj.packed, attn.k_proj.packed, attn.v_proj.packed,
                                       unit_offset=off1)
     cos, sin = position_embeddings
@@ -422,9 +433,13 @@ def fuse_shared_activation_quant(model: nn.Module) -> int:
             getattr(mod, "down_proj", None),
         )
         if all(isinstance(p, W4A4Linear) for p in gate_up) and hasattr(mod, "act_fn"):
+            # The fused epilogue reads row-major or MFMA-layout weights; WMMA-preshuffled
+            # gate/up weights (PI05_W4A4_MFMA=0 with the reference's gate preshuffle) take the
+            # reference's int4_gemm2_tiled + act_fn route instead.
             mod._w4a4_fuse_gelu = (
                 fuse_gelu
                 and gate_up[0].packed.shape == gate_up[1].packed.shape
+                and not (gate_up[0].preshuffled or gate_up[1].preshuffled)
                 and _is_torch_gelu_tanh(mod.act_fn)
             )
             mod.forward = types.MethodType(_fused_mlp_forward, mod)

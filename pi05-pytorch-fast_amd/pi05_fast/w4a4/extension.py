@@ -11,9 +11,10 @@ Validation and error messages follow the reference's TORCH_CHECKs
 (``pi05_fast/w4a4/csrc/int4_gemm.cu:487-501, 570-577``); they surface as RuntimeError.
 
 Weight layouts accepted (the reference's marker-stride convention):
-  * row-major ``[N, K/8+1]`` (L1) or row-padded ``[N, K/8+P]`` (L2) -- repacked into a
-    temporary MFMA-layout buffer on every call (slow path, kept for drop-in use);
-  * WMMA-tiled ``[N, K/8+9]`` (L3) -- ``*_tiled`` ops, repacked per call likewise;
+  * row-major ``[N, K/8+1]`` (L1) or row-padded ``[N, K/8+P]`` (L2) -- repacked into an
+    MFMA-layout copy on the first call with that tensor, which later calls reuse (kept
+    for drop-in use; the copy doubles the weight's device memory);
+  * WMMA-tiled ``[N, K/8+9]`` (L3) -- ``*_tiled`` ops, repacked once likewise;
   * MFMA-fragment-major ``[N, K/8+16]`` -- produced once by ``repack_weight`` (and by
     ``apply.replace_linears_from_packed`` at load), consumed directly (fast path).
 
@@ -24,6 +25,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 from pathlib import Path
 
 import torch
@@ -237,17 +239,59 @@ def repack_weight(w: torch.Tensor, k: int | None = None, tiled: bool | None = No
     return out
 
 
+# Repacked copies of weights that arrive in a reference layout (L1/L2/L3), one per source
+# tensor object: the repack runs on the first call only.  An entry is dropped when its
+# source tensor is freed, and it is rebuilt when the tensor is modified in place (its
+# version counter moves) or used with another K.
+_MFMA_CACHE: dict[int, tuple] = {}
+
+
 def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
-    """Weight in MFMA layout (converting per call when needed) and its true N."""
+    """Weight in MFMA layout (repacked once per source tensor when needed) and its true N."""
     n = int(w.size(0))
     if is_mfma_layout(w, k):
         return w, n
+    key = id(w)
+    hit = _MFMA_CACHE.get(key)
+    if hit is not None:
+        ref, version, hk, htiled, out = hit
+        if ref() is w and version == w._version and hk == k and htiled == tiled:
+            return out, n
     if tiled:
-        return repack_weight(w, k, tiled=True), n
-    if n % 16 != 0:
-        pad = 16 - n % 16
-        w = torch.nn.functional.pad(w.contiguous(), (0, 0, 0, pad))
-    return repack_weight(w, k, tiled=False), n
+        out = repack_weight(w, k, tiled=True)
+    else:
+        src = w
+        if n % 16 != 0:
+            src = torch.nn.functional.pad(w.contiguous(), (0, 0, 0, 16 - n % 16))
+        out = repack_weight(src, k, tiled=False)
+    _MFMA_CACHE[key] = (weakref.ref(w, lambda _r, key=key: _MFMA_CACHE.pop(key, None)), w._version, k, tiled, out)
+    return out, n
+
+
+def _check_gelu_weights(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> None:
+    """Gate and up weights of the fused GELU epilogue: one shape, row-major (L1/L2) or
+    MFMA layout.  WMMA-tiled weights (the K/8+9 marker stride of pack.py:45-50) would be
+    misread as row-major, so they are refused."""
+    if w_gate.shape != w_up.shape:
+        raise RuntimeError("gate and up weights must have the same shape")
+    k = int(x.size(-1)) if x.dim() else 0
+    if w_gate.dim() == 2 and w_gate.size(1) == k // 8 + WMMA_MARKER_WORDS:
+        raise RuntimeError("int4_gemm2_gelu takes row-major or MFMA-layout weights; WMMA-tiled "
+                           "(K/8+9) gate/up weights go through int4_gemm2_tiled")
+
+
+def _check_residual(residual: torch.Tensor, device: torch.device, shape: tuple) -> None:
+    """The residual of a fused residual-add GEMM: a float16 tensor of the output's shape on
+    the activations' device (the kernel reads it as fp16 through a device pointer)."""
+    if not isinstance(residual, torch.Tensor):
+        raise RuntimeError("residual must be a tensor")
+    if residual.device != device:
+        raise RuntimeError(f"residual must be on {device}, got {residual.device}")
+    if residual.dtype != torch.float16:
+        raise RuntimeError(f"residual must be float16, got {residual.dtype}")
+    if tuple(residual.shape) != tuple(shape):
+        raise RuntimeError(f"residual must be [{', '.join(map(str, shape))}] "
+                           f"with N a multiple of 16, got {tuple(residual.shape)}")
 
 
 def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, residual=None):
@@ -258,9 +302,10 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, 
     ns = [int(w.size(0)) for (w, _) in weights]
     if residual is not None:
         (w0, n_true), = weights
-        if n_true != ns[0] or tuple(residual.shape) != (*out_shape_prefix, n_true):
+        if n_true != ns[0]:
             raise RuntimeError(f"residual must be [{', '.join(map(str, out_shape_prefix))}, {n_true}] "
                                f"with N a multiple of 16, got {tuple(residual.shape)}")
+        _check_residual(residual, device, (*out_shape_prefix, n_true))
         res = residual if residual.is_contiguous() and residual.data_ptr() % 16 == 0 else residual.contiguous().clone()
         out = torch.empty((m, n_true), dtype=torch.float16, device=device)
         ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, 1, (ctypes.c_int32 * 1)(n_true), 0)
@@ -324,6 +369,8 @@ def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
 def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False,
          norm=None, residual=None, warm=None):
     k = _check_x(x)
+    if residual is not None:  # before any launch: the kernel reads it through a raw pointer
+        _check_residual(residual, x.device, (*x.shape[:-1], int(ws[0].size(0))))
     # the reference quantizes before checking the weights
     q, sa = quantize(x, warm) if norm is None else rms_norm_quantize(x, *norm)
     conv = []
@@ -379,12 +426,15 @@ ATTN_HEAD_DIM = 256
 ATTN_MAX_KEYS = 1024
 
 
-def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int):
+def _attention_mask_arg(mask: torch.Tensor | None, b: int, s: int, device: torch.device):
     """(tensor, batch stride, row stride, row length) of an additive fp16 mask [B|1, 1, S, >=S]
-    in the form the kernel reads (row length a multiple of 4 >= S, strides multiples of 4,
-    8-byte aligned); a padded copy is made only when the given tensor does not fit."""
+    on the queries' device, in the form the kernel reads (row length a multiple of 4 >= S,
+    strides multiples of 4, 8-byte aligned); a padded copy is made only when the given tensor
+    does not fit."""
     if mask is None:
         return None, 0, 0, 0
+    if mask.device != device:
+        raise RuntimeError(f"prefix_attention mask must be on {device}, got {mask.device}")
     if mask.dtype != torch.float16 or mask.dim() != 4 or mask.size(1) != 1:
         raise RuntimeError("prefix_attention mask must be an additive float16 [B, 1, S, Sk] tensor")
     if mask.size(0) not in (1, b) or mask.size(2) != s or mask.size(3) < s:
@@ -429,7 +479,7 @@ def _prefix_attention_impl(
                            f"{h} query and {kvh} KV heads of {d}")
     qc, kc, vc = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
     cs = [t.expand(b, s, d).contiguous() if t.dim() == 3 else t.reshape(b, s, d).contiguous() for t in (cos, sin)]
-    m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s)
+    m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s, q.device)
     lib = load_int4_gemm()
     k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
     kv_mfma = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
@@ -474,8 +524,9 @@ def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, n
     tensor)."""
     k_in = ATTN_HEAD_DIM * int(num_heads)
     _check_packed(w_o, k_in, "o_proj weight")
-    w, n_true = _as_mfma(w_o, k_in, tiled=False)
     lead = tuple(q.shape[:-1])
+    _check_residual(residual, q.device, (*lead, int(w_o.size(0))))  # before any launch
+    w, n_true = _as_mfma(w_o, k_in, tiled=False)
     if int(num_kv_heads) == 1 and k_in == 2048:
         out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
                                                             num_kv_heads, quantize_out=True, warm=warm,
@@ -554,8 +605,7 @@ def _register_custom_op() -> None:
     # Not in the reference: gate/up GEMMs with the GELU-tanh(gate) * up epilogue fused.
     @torch.library.custom_op("pi05_w4a4::int4_gemm2_gelu", mutates_args=())
     def _int4_gemm2_gelu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
-        if w_gate.shape != w_up.shape:
-            raise RuntimeError("gate and up weights must have the same shape")
+        _check_gelu_weights(x, w_gate, w_up)
         return _run(x, [w_gate, w_up], tiled=False, kind="gemm2_gelu", gelu=True)[0]
 
     @_int4_gemm2_gelu.register_fake
@@ -590,6 +640,7 @@ def _register_custom_op() -> None:
         x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
         w_gate: torch.Tensor, w_up: torch.Tensor,
     ) -> torch.Tensor:
+        _check_gelu_weights(x, w_gate, w_up)
         return _run(x, [w_gate, w_up], tiled=False, kind="int4_gemm2_gelu", gelu=True,
                     norm=(norm_weight, eps, unit_offset))[0]
 

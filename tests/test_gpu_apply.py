@@ -54,31 +54,24 @@ def _gemma(layers: int):
     return lm
 
 
-def test_pack_apply_forward(cuda, tmp_path, monkeypatch):
+def _pack(tmp_path, layers: int):
+    """A Gemma LM of PaliGemma-2B layer shapes, its checkpoint under the policy's module
+    path and the W4A4 pack written from it."""
     from safetensors.torch import save_file
 
-    from pi05_fast.w4a4 import W4A4Linear
-    from pi05_fast.w4a4.apply import apply_w4a4_from_dir
-    from pi05_fast.w4a4.norm import FusedRMSNorm
     from pi05_fast.w4a4.pack_w4a4_prefix import pack_checkpoint
-    from transformers.cache_utils import DynamicCache
 
-    layers = 2
     lm = _gemma(layers)
     ckpt = {f"model.{PREFIX}.{k}": v.contiguous() for k, v in lm.state_dict().items() if k.endswith("proj.weight")}
     save_file(ckpt, str(tmp_path / "model.safetensors"))
     meta = pack_checkpoint(tmp_path / "model.safetensors", tmp_path / "pack")
     assert len(meta["layers"]) == 7 * layers
+    return lm
 
-    policy = _Policy(lm.to(device=cuda, dtype=torch.float16)).eval()
-    assert apply_w4a4_from_dir(policy, tmp_path / "pack") == 7 * layers
-    for layer in lm.layers:
-        assert hasattr(layer, "_w4a4_layer_forward"), "fused decoder layer not installed"
-        assert isinstance(layer.input_layernorm, FusedRMSNorm)
-        assert all(isinstance(getattr(layer.mlp, p), W4A4Linear) for p in ("gate_proj", "up_proj", "down_proj"))
 
-    rec = _Recorder(monkeypatch)
-    s = 300
+def _run_lm(lm, cuda, s=300):
+    from transformers.cache_utils import DynamicCache
+
     gen = torch.Generator().manual_seed(5)
     x = (torch.randn(1, s, 2048, generator=gen) / 2048**0.5).half().to(cuda)
     cache = DynamicCache()
@@ -87,6 +80,20 @@ def test_pack_apply_forward(cuda, tmp_path, monkeypatch):
     torch.cuda.synchronize()
     hidden = out.last_hidden_state
     assert hidden.shape == (1, s, 2048) and torch.isfinite(hidden).all()
+    return hidden, cache
+
+
+def _cast_floating_tensors(module, dtype) -> None:
+    """The reference's prefix-LM cast after the pack is applied (rocm_pi05_optim.py:136-154):
+    floating parameters and buffers are cast in place, the INT4 packed weights are left."""
+    for t in list(module.parameters()) + list(module.buffers()):
+        if t.is_floating_point() and t.dtype != dtype:
+            t.data = t.data.to(dtype)
+
+
+def _check_fused_forward(lm, cuda, monkeypatch, layers, s=300):
+    rec = _Recorder(monkeypatch)
+    _, cache = _run_lm(lm, cuda, s)
     kinds = [c[0] for c in rec.calls]
     assert kinds.count("rms_norm_int4_gemm3") == layers
     assert kinds.count("prefix_attention_o_proj") == layers
@@ -98,3 +105,81 @@ def test_pack_apply_forward(cuda, tmp_path, monkeypatch):
     # the cached key states are the RoPE'd keys the attention op returned
     att = [c for c in rec.calls if c[0] == "prefix_attention_o_proj"]
     assert torch.equal(cache.layers[0].keys, att[0][3][1])
+
+
+def test_pack_apply_forward(cuda, tmp_path, monkeypatch):
+    from pi05_fast.w4a4 import W4A4Linear
+    from pi05_fast.w4a4.apply import apply_w4a4_from_dir
+    from pi05_fast.w4a4.norm import FusedRMSNorm
+
+    layers = 2
+    lm = _pack(tmp_path, layers)
+    policy = _Policy(lm.to(device=cuda, dtype=torch.float16)).eval()
+    assert apply_w4a4_from_dir(policy, tmp_path / "pack") == 7 * layers
+    for layer in lm.layers:
+        assert hasattr(layer, "_w4a4_layer_forward"), "fused decoder layer not installed"
+        assert isinstance(layer.input_layernorm, FusedRMSNorm)
+        assert all(isinstance(getattr(layer.mlp, p), W4A4Linear) for p in ("gate_proj", "up_proj", "down_proj"))
+    _check_fused_forward(lm, cuda, monkeypatch, layers)
+
+
+def test_pack_applied_to_bf16_model_then_cast_to_fp16(cuda, tmp_path, monkeypatch):
+    """The reference's order (rocm_pi05_optim.py:216-237): the policy is cast to bf16, the
+    pack is applied, and only then is the prefix LM cast to fp16.  The fused norms and
+    decoder layers are installed by structure, so after the cast the forward runs them."""
+    from pi05_fast.w4a4.apply import apply_w4a4_from_dir
+    from pi05_fast.w4a4.norm import FusedRMSNorm
+
+    layers = 2
+    lm = _pack(tmp_path, layers)
+    policy = _Policy(lm.to(device=cuda, dtype=torch.bfloat16)).eval()
+    assert apply_w4a4_from_dir(policy, tmp_path / "pack") == 7 * layers
+    for layer in lm.layers:
+        assert hasattr(layer, "_w4a4_layer_forward"), "fused decoder layer not installed on the bf16 model"
+        assert isinstance(layer.input_layernorm, FusedRMSNorm)
+        assert layer.input_layernorm.weight.dtype == torch.bfloat16
+    _cast_floating_tensors(lm, torch.float16)
+    assert lm.layers[0].input_layernorm.weight.dtype == torch.float16
+    _check_fused_forward(lm, cuda, monkeypatch, layers)
+
+
+def test_pack_apply_reference_layouts(cuda, tmp_path, monkeypatch):
+    """PI05_W4A4_MFMA=0: the reference's load-time layouts are kept (q/k/v/o/down row-padded
+    to K/8+8, gate/up WMMA-preshuffled to K/8+9, apply.py:45-88) and the reference's call
+    routes run: int4_gemm3 for QKV, int4_gemm2_tiled + act_fn for gate/up, int4_gemm for o
+    and down.  Every op matches the oracle, and each weight is repacked into the MFMA
+    layout on its first call only (a second forward repacks nothing)."""
+    from pi05_fast.w4a4 import extension as ext
+    from pi05_fast.w4a4.apply import apply_w4a4_from_dir
+
+    monkeypatch.setenv("PI05_W4A4_MFMA", "0")
+    layers = 2
+    lm = _pack(tmp_path, layers)
+    policy = _Policy(lm.to(device=cuda, dtype=torch.float16)).eval()
+    assert apply_w4a4_from_dir(policy, tmp_path / "pack") == 7 * layers
+    mlp = lm.layers[0].mlp
+    assert mlp.gate_proj.preshuffled and mlp.gate_proj.packed.shape[1] == 2048 // 8 + 9
+    assert lm.layers[0].self_attn.o_proj.packed.shape[1] == 2048 // 8 + 8
+    assert not mlp._w4a4_fuse_gelu
+    assert not hasattr(lm.layers[0], "_w4a4_layer_forward")
+
+    repacks = []
+    real = ext.repack_weight
+
+    def counting(*a, **kw):
+        repacks.append(tuple(a[0].shape))
+        return real(*a, **kw)
+
+    monkeypatch.setattr(ext, "repack_weight", counting)
+    rec = _Recorder(monkeypatch)
+    y1, _ = _run_lm(lm, cuda)
+    assert len(repacks) == 7 * layers
+    kinds = [c[0] for c in rec.calls]
+    assert kinds.count("int4_gemm3") == layers
+    assert kinds.count("int4_gemm2_tiled") == layers
+    assert kinds.count("int4_gemm") == 2 * layers
+    for i, call in enumerate(rec.calls):
+        _check_call(cuda, i, call)
+    y2, _ = _run_lm(lm, cuda)
+    assert len(repacks) == 7 * layers, "weights were repacked again on the second forward"
+    assert torch.equal(y1, y2)

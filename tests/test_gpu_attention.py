@@ -115,7 +115,7 @@ def _fragments_vt(vp: torch.Tensor) -> torch.Tensor:
     return vp.view(nst, 4, 8, 16, 16).permute(3, 0, 1, 4, 2).reshape(16, nst, 64, 8)
 
 
-@pytest.mark.parametrize("b,s,kvh", [(1, 776, 1), (2, 100, 1), (1, 1, 1), (1, 1024, 1), (1, 64, 2)])
+@pytest.mark.parametrize("b,s,kvh", [(1, 776, 1), (2, 100, 1), (1, 1, 1), (1, 1024, 1), (1, 64, 2), (8, 776, 1)])
 def test_key_rope_and_mfma_layouts(ext, cuda, b, s, kvh):
     h = 8
     q, k, v, cos, sin = _inputs(b, s, h, kvh, cuda, seed=s + b)
@@ -154,6 +154,8 @@ CASES = [
     (1, 1024, 8, 1, "padding"),
     (1, 128, 4, 2, "padding"),
     (2, 77, 8, 1, "padding"),
+    (8, 776, 8, 1, "zeros"),    # the batch-8 x 776 forward point
+    (8, 776, 8, 1, "padding"),
 ]
 
 
@@ -261,7 +263,7 @@ def test_decoder_attention_uses_kernel_and_fills_cache(ext, cuda, monkeypatch):
     assert _rel_l2(o_fused, o_eager) <= REL_L2
 
 
-@pytest.mark.parametrize("b,s,kind", [(1, 776, "zeros"), (2, 77, "padding"), (1, 5, None)])
+@pytest.mark.parametrize("b,s,kind", [(1, 776, "zeros"), (2, 77, "padding"), (1, 5, None), (8, 776, "zeros")])
 def test_attention_output_quant_matches_oracle(ext, cuda, b, s, kind):
     """With one KV head and 8 query heads the attention kernel quantizes its own output
     rows for the o projection: codes, scale bits and row corrections equal the oracle's
@@ -286,7 +288,7 @@ def test_attention_output_quant_matches_oracle(ext, cuda, b, s, kind):
     assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
 
 
-@pytest.mark.parametrize("b,s,h,kvh", [(1, 776, 8, 1), (2, 100, 8, 1), (1, 64, 4, 2)])
+@pytest.mark.parametrize("b,s,h,kvh", [(1, 776, 8, 1), (2, 100, 8, 1), (1, 64, 4, 2), (8, 776, 8, 1)])
 def test_prefix_attention_o_proj_matches_oracle(ext, cuda, b, s, h, kvh):
     """residual + o_proj(attention): the fp16 result equals the oracle's W4A4 o projection of
     the returned attention output plus the residual, bit for bit, through the fused quant

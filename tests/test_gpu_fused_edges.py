@@ -54,10 +54,11 @@ def test_rmsnorm_quantize_matches_oracle(ext, cuda, m, scale, offset):
     assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
 
 
-def test_rmsnorm_quantize_equals_norm_then_quantize_when_norm_matches(ext, cuda):
-    """When the standalone norm kernel's output equals the lane-order restatement (most
-    rows), the fused quant equals quantize(rms_norm(x)) exactly."""
-    m, k = 64, 2048
+def test_rmsnorm_quantize_equals_norm_then_quantize(ext, cuda):
+    """The fused norm + quant and the one-kernel norm followed by the quantizer give the
+    same codes, scales and row corrections, bit for bit: both norm kernels sum the squares
+    in one order and use a correctly rounded 1/sqrt."""
+    m, k = 776, 2048
     gen = inp.generator(5)
     x = inp.activations(gen, m, k).to(cuda)
     w = (torch.randn(k, generator=gen) * 0.1).half().to(cuda)
@@ -65,12 +66,53 @@ def test_rmsnorm_quantize_equals_norm_then_quantize_when_norm_matches(ext, cuda)
     q1, s1 = ext.quantize(h)
     q2, s2 = ext.rms_norm_quantize(x, w, 1e-6)
     torch.cuda.synchronize()
-    same_rows = (h.cpu().numpy().view(np.int16) ==
-                 orc.rms_norm_lanes(x.cpu().numpy(), w.cpu().numpy(), 1e-6).view(np.int16)).all(axis=1)
-    assert same_rows.mean() > 0.5
-    c1, c2 = _codes(q1, m, k), _codes(q2, m, k)
-    assert np.array_equal(c1[same_rows], c2[same_rows])
-    assert np.array_equal(inp.to_np(s1)[same_rows].view(np.int32), inp.to_np(s2)[same_rows].view(np.int32))
+    assert np.array_equal(inp.to_np(h).view(np.int16),
+                          orc.rms_norm_lanes(x.cpu().numpy(), w.cpu().numpy(), 1e-6).view(np.int16))
+    assert torch.equal(q1, q2)
+    assert np.array_equal(inp.to_np(s1).view(np.int32), inp.to_np(s2).view(np.int32))
+
+
+def _hidden_states(gen, m, k):
+    """Decoder-like residual-stream rows: N(0, 1) with 1% outlier channels x20 and a
+    per-row scale spread over two decades."""
+    x = inp.activations(gen, m, k).float()
+    return (x * torch.exp(torch.randn(m, 1, generator=gen) * 1.2)).half()
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_fused_norm_code_drift_against_eager_gemma_norm(ext, cuda, seed):
+    """The default fused RMSNorm + quant against the reference pipeline's order: transformers'
+    eager GemmaRMSNorm on the GPU, then the activation quant of int4_gemm3 (apply.py:145-165
+    with modeling_gemma's input_layernorm).  The two norms differ only in the fp32 summation
+    order and the rounding of the reciprocal square root, which moves a few fp16 norm outputs
+    by one ulp; the activation codes may then flip by +-1 where the rotated value sits at a
+    rounding tie.  Bar: at most 0.01% of codes differ, by at most 1 (the measured rate is in
+    the assertion message)."""
+    from transformers.models.gemma.modeling_gemma import GemmaRMSNorm
+
+    m, k = 776, 2048
+    gen = inp.generator(900 + seed)
+    x = _hidden_states(gen, m, k)
+    norm = GemmaRMSNorm(k, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(k, generator=gen) * 0.3)
+    norm = norm.to(device=cuda, dtype=torch.float16)
+    xd = x.to(cuda)
+    with torch.no_grad():
+        h_eager = norm(xd)
+    q_ref, s_ref = ext.quantize(h_eager)
+    q_fused, s_fused = ext.rms_norm_quantize(xd, norm.weight, 1e-6)
+    torch.cuda.synchronize()
+    h_diff = int((h_eager.view(torch.int16) != ext.rms_norm(xd, norm.weight, 1e-6).view(torch.int16)).sum())
+    c_ref, c_fused = _codes(q_ref, m, k), _codes(q_fused, m, k)
+    diff = np.abs(c_ref.astype(np.int32) - c_fused.astype(np.int32))
+    nflip = int(np.count_nonzero(diff))
+    frac = nflip / diff.size
+    msg = (f"seed {seed}: norm outputs differing {h_diff}/{m * k} ({100 * h_diff / (m * k):.4f}%), "
+           f"codes differing {nflip}/{diff.size} ({100 * frac:.5f}%), max |diff| {int(diff.max())}")
+    print(msg)
+    assert int(diff.max()) <= 1, msg
+    assert frac <= 1e-4, msg
 
 
 @pytest.mark.parametrize("m,k,n", [(776, 2048, 2048), (776, 16384, 2048), (1, 16384, 2048), (64, 2048, 2048),
@@ -95,3 +137,7 @@ def test_gemm_residual_rejects_bad_residual(ext, cuda):
     w = ext.repack_weight(inp.random_packed(inp.generator(1), 256, 2048).to(cuda), k=2048)
     with pytest.raises(RuntimeError, match="residual must be"):
         ext.int4_gemm_residual(x, w, torch.zeros(4, 128, dtype=torch.float16, device=cuda))
+    with pytest.raises(RuntimeError, match="residual must be float16"):
+        ext.int4_gemm_residual(x, w, torch.zeros(4, 256, dtype=torch.bfloat16, device=cuda))
+    with pytest.raises(RuntimeError, match="residual must be on cuda"):
+        ext.int4_gemm_residual(x, w, torch.zeros(4, 256, dtype=torch.float16))

@@ -338,3 +338,75 @@ def test_rms_norm_matches_gemma_module(ext, cuda, m, k):
     assert int(ulps.max()) <= 1, f"max difference {int(ulps.max())} fp16 ulps"
     frac = float((ulps > 0).float().mean())
     assert frac <= 5e-3, f"{100 * frac:.3f}% of outputs differ by one ulp"
+
+
+@pytest.mark.parametrize("m,k,offset", [(776, 2048, True), (5, 2048, False), (33, 16384, True), (7, 64, True),
+                                        (9, 192, True), (3, 4104, True)])
+def test_rms_norm_matches_oracle_lane_order(ext, cuda, m, k, offset):
+    """The one-kernel RMSNorm equals the oracle's rms_norm_lanes bit for bit: the kernel and
+    the RMSNorm fused into the K = 2048 activation quant share one summation order and a
+    correctly rounded 1/sqrt, which the oracle restates."""
+    gen = torch.Generator().manual_seed(m * 11 + k)
+    x = (torch.randn(m, k, generator=gen) * 3.0).to(torch.float16)
+    w = (torch.randn(k, generator=gen) * (0.05 if offset else 1.0)).to(torch.float16)
+    got = ext.rms_norm(x.to(cuda), w.to(cuda), 1e-6, unit_offset=offset)
+    torch.cuda.synchronize()
+    want = orc.rms_norm_lanes(x.numpy(), w.numpy(), 1e-6, unit_offset=offset)
+    _assert_f16_equal(inp.to_np(got), want, f"rms_norm M={m} K={k}")
+
+
+# ----------------------------------------------------------------------------- reference default gate/up route
+@pytest.mark.parametrize("m", [776, 272])
+def test_int4_gemm2_tiled_wmma_weights(ext, cuda, m):
+    """The reference's default gate/up route (apply.py:134-135): int4_gemm2_tiled over
+    WMMA-tiled (L3, [N, K/8+9]) gate and up weights, K = 2048, N = 16384, against the
+    oracle on the row-major weights, bit for bit; int4_gemm_tiled on the same weights too."""
+    from pi05_fast.w4a4.pack import preshuffle_wmma_weight
+
+    k, n = 2048, 16384
+    gen = inp.generator(400 + m)
+    x = inp.activations(gen, m, k)
+    wg = inp.random_packed(gen, n, k)
+    wu = inp.random_packed(gen, n, k)
+    tg, tu = (preshuffle_wmma_weight(w, k).to(cuda) for w in (wg, wu))
+    assert tg.shape == (n, k // 8 + 9)
+    g, u = ext.int4_gemm2_tiled(x.to(cuda), tg, tu)
+    g1 = ext.int4_gemm_tiled(x.to(cuda), tg)
+    torch.cuda.synchronize()
+    want_g = orc.int4_gemm_ref(x.numpy(), wg.numpy())
+    _assert_f16_equal(inp.to_np(g), want_g, f"gate M={m}")
+    _assert_f16_equal(inp.to_np(u), orc.int4_gemm_ref(x.numpy(), wu.numpy()), f"up M={m}")
+    _assert_f16_equal(inp.to_np(g1), want_g, f"int4_gemm_tiled M={m}")
+
+
+def test_reference_layout_repack_runs_once_per_weight(ext, cuda, monkeypatch):
+    """Weights kept in a reference layout (L1 row-major, L2 row-padded, L3 tiled) are
+    repacked into the MFMA layout on their first call only; an in-place update of the
+    weight invalidates the cached copy."""
+    from pi05_fast.w4a4.pack import preshuffle_wmma_weight
+
+    calls = []
+    real = ext.repack_weight
+
+    def counting(*a, **kw):
+        calls.append(a[0].shape)
+        return real(*a, **kw)
+
+    monkeypatch.setattr(ext, "repack_weight", counting)
+    gen = inp.generator(7)
+    x = inp.activations(gen, 40, 2048).to(cuda)
+    w1 = inp.random_packed(gen, 256, 2048).to(cuda)
+    w2 = torch.nn.functional.pad(inp.random_packed(gen, 256, 2048), (0, 7)).to(cuda)
+    w3 = preshuffle_wmma_weight(inp.random_packed(gen, 16384, 2048), 2048).to(cuda)
+    y1 = [ext.int4_gemm(x, w1) for _ in range(3)]
+    y2 = [ext.int4_gemm(x, w2) for _ in range(3)]
+    y3 = [ext.int4_gemm_tiled(x, w3) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert len(calls) == 3, calls
+    for ys in (y1, y2, y3):
+        assert all(torch.equal(ys[0], y) for y in ys[1:])
+    w1.view(torch.int32)[0, 0] ^= 0x11  # in place: the cached copy is stale now
+    y1b = ext.int4_gemm(x, w1)
+    torch.cuda.synchronize()
+    assert len(calls) == 4
+    _assert_f16_equal(inp.to_np(y1b), orc.int4_gemm_ref(x.cpu().numpy(), w1.cpu().numpy()), "after update")

@@ -51,8 +51,8 @@ def _build(cuda, layers: int, fuse_gelu: bool, fuse_layer: bool = True):
 class _Recorder:
     """Wraps the extension ops (and the name linear.py imported) to record every call."""
 
-    NAMES = ("int4_gemm", "int4_gemm2", "int4_gemm3", "int4_gemm2_gelu", "rms_norm_int4_gemm3",
-             "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj")
+    NAMES = ("int4_gemm", "int4_gemm_tiled", "int4_gemm2", "int4_gemm2_tiled", "int4_gemm3", "int4_gemm2_gelu",
+             "rms_norm_int4_gemm3", "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj")
 
     def __init__(self, monkeypatch):
         from pi05_fast.w4a4 import extension, linear
@@ -77,10 +77,15 @@ class _Recorder:
 
 
 def _row_major(w: torch.Tensor, k: int) -> np.ndarray:
+    """The L1 row-major [N, K/8+1] form of a weight in any layout the ops take: MFMA
+    (K/8+16), WMMA-tiled (K/8+9) or row-major / row-padded (scale at word K/8)."""
     from pi05_fast.w4a4 import pack
 
-    assert w.shape[1] == k // 8 + pack.MFMA_MARKER_WORDS, "forward weights are MFMA-layout"
-    return pack.unpack_mfma_weight(w.cpu(), k).numpy()
+    if w.shape[1] == k // 8 + pack.MFMA_MARKER_WORDS:
+        return pack.unpack_mfma_weight(w.cpu(), k).numpy()
+    if w.shape[1] == k // 8 + pack.WMMA_PRESHUFFLE_PAD_WORDS:
+        return orc.unshuffle_wmma_weight(w.cpu().numpy(), k)
+    return np.ascontiguousarray(w.cpu().numpy()[:, : k // 8 + 1])
 
 
 def _oracle_h(x: np.ndarray, w: torch.Tensor, k: int) -> np.ndarray:
@@ -132,15 +137,25 @@ def _check_call(cuda, i, call) -> None:
         assert nbad == 0, f"{what}: {nbad}/{got.size} fp16 outputs differ from the oracle"
 
 
-@pytest.mark.parametrize("fuse_layer", [True, False])
-@pytest.mark.parametrize("layers,tokens", [(2, 776), (18, 128)])
-def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, fuse_layer):
+# The benchmark's forward points: 776 tokens (the headline), 640 and 768 tokens, and the
+# batch-8 x 776 throughput point (M = 6208: 56 row tiles, a 7168-workgroup gate/up grid,
+# attention at batch 8), plus a deep short forward.
+FORWARDS = [
+    # layers, tokens, batch, fused decoder layer
+    (2, 776, 1, True), (2, 776, 1, False), (18, 128, 1, True), (18, 128, 1, False),
+    (2, 640, 1, True), (2, 768, 1, True), (1, 776, 8, True), (1, 776, 8, False),
+]
+
+
+@pytest.mark.parametrize("layers,tokens,batch,fuse_layer", FORWARDS)
+def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, batch, fuse_layer):
     from pi05_fast.w4a4.prefix_lm import prefix_inputs
 
+    print(f"prefix LM forward: {layers} layers x {tokens} tokens x batch {batch}, fused layer {fuse_layer}", flush=True)
     model, _ = _build(cuda, layers, fuse_gelu=True, fuse_layer=fuse_layer)
     rec = _Recorder(monkeypatch)
-    x = prefix_inputs(1, tokens, cuda)
-    mask = torch.zeros(1, 1, tokens, tokens, dtype=torch.float16, device=cuda)
+    x = prefix_inputs(batch, tokens, cuda)
+    mask = torch.zeros(batch, 1, tokens, tokens, dtype=torch.float16, device=cuda)
     with torch.no_grad():
         y = model(x, mask)
     torch.cuda.synchronize()

@@ -469,3 +469,88 @@ def test_prefix_lm_builds_and_fails_loudly_on_cpu():
         model(prefix_inputs(1, 8, "cpu"))
     ops = prefix_ops(776)
     assert abs(sum(ops.values()) / 1e9 - 3075.8) < 0.1
+
+
+def test_fused_forwards_trace_with_fullgraph(monkeypatch):
+    """The fused decoder layer, the fused MLP and a W4A4Linear trace with
+    ``torch.compile(fullgraph=True)`` (rocm_pi05_optim.py:254-262): Dynamo captures each as
+    one graph over the W4A4 custom ops, run here on meta tensors through the ops' fake
+    implementations (the GPU test compiles them with Inductor and runs them)."""
+    import types
+
+    import torch
+    from transformers.models.gemma.modeling_gemma import GemmaDecoderLayer
+
+    from pi05_fast.w4a4 import apply
+    from pi05_fast.w4a4.linear import W4A4Linear
+    from pi05_fast.w4a4.norm import FusedRMSNorm
+    from pi05_fast.w4a4.prefix_lm import gemma_config
+
+    cfg = gemma_config(1)
+    with torch.device("meta"):
+        layer = GemmaDecoderLayer(cfg, 0)
+    for parent in (layer.self_attn, layer.mlp):
+        for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+            lin = getattr(parent, name, None)
+            if lin is not None:
+                w = torch.empty(lin.out_features, lin.in_features // 8 + 16, dtype=torch.int32, device="meta")
+                setattr(parent, name, W4A4Linear(w, in_features=lin.in_features))
+    for name in ("input_layernorm", "post_attention_layernorm"):
+        weight = torch.nn.Parameter(torch.empty(2048, dtype=torch.float16, device="meta"), requires_grad=False)
+        setattr(layer, name, FusedRMSNorm(weight, 1e-6))
+    apply.fuse_shared_activation_quant(layer)
+    assert layer.mlp._w4a4_fuse_gelu
+    assert apply.fuse_decoder_layers(layer) == 1
+    # meta tensors are not on a GPU: let the call-time fit checks pass
+    monkeypatch.setattr(apply, "_attention_call_fits", lambda *a, **k: True)
+    monkeypatch.setattr(apply, "_norms_fit", lambda *a, **k: True)
+    x = torch.empty(1, 776, 2048, dtype=torch.float16, device="meta")
+    cos = torch.empty(1, 776, 256, dtype=torch.float16, device="meta")
+    mask = torch.empty(1, 1, 776, 776, dtype=torch.float16, device="meta")
+    torch._dynamo.reset()
+    y = torch.compile(layer, fullgraph=True, backend="eager")(x, attention_mask=mask, position_embeddings=(cos, cos))
+    assert (y[0] if isinstance(y, tuple) else y).shape == (1, 776, 2048)
+    torch._dynamo.reset()
+    assert torch.compile(layer.mlp, fullgraph=True, backend="eager")(x).shape == (1, 776, 2048)
+    torch._dynamo.reset()
+    assert torch.compile(layer.self_attn.o_proj, fullgraph=True, backend="eager")(x).shape == (1, 776, 2048)
+
+
+def test_residual_and_mask_checks_precede_any_launch():
+    """A residual or attention mask on the wrong device or of the wrong dtype is rejected by
+    the host checks (the kernels read them through raw device pointers)."""
+    import torch
+
+    from pi05_fast.w4a4 import extension as ext
+
+    dev = torch.device("cuda:0")
+    ok = torch.empty(4, 256, dtype=torch.float16, device="meta")
+    with pytest.raises(RuntimeError, match="residual must be on cuda:0"):
+        ext._check_residual(torch.zeros(4, 256, dtype=torch.float16), dev, (4, 256))
+    with pytest.raises(RuntimeError, match="residual must be on cuda:0"):
+        ext._check_residual(ok, dev, (4, 256))
+    meta = torch.device("meta")
+    with pytest.raises(RuntimeError, match="residual must be float16"):
+        ext._check_residual(torch.empty(4, 256, dtype=torch.bfloat16, device="meta"), meta, (4, 256))
+    with pytest.raises(RuntimeError, match="residual must be \\[4, 256\\]"):
+        ext._check_residual(torch.empty(4, 128, dtype=torch.float16, device="meta"), meta, (4, 256))
+    ext._check_residual(ok, meta, (4, 256))
+    with pytest.raises(RuntimeError, match="mask must be on cuda:0"):
+        ext._attention_mask_arg(torch.zeros(1, 1, 8, 8, dtype=torch.float16), 1, 8, dev)
+
+
+def test_gelu_op_rejects_wmma_tiled_weights():
+    """int4_gemm2_gelu reads row-major or MFMA-layout weights only: WMMA-tiled gate/up
+    weights (the K/8+9 marker stride) are refused instead of being misread."""
+    import torch
+
+    from pi05_fast.w4a4 import extension as ext
+
+    x = torch.empty(4, 2048, dtype=torch.float16, device="meta")
+    tiled = torch.empty(16384, 2048 // 8 + 9, dtype=torch.int32, device="meta")
+    with pytest.raises(RuntimeError, match="int4_gemm2_tiled"):
+        ext._check_gelu_weights(x, tiled, tiled)
+    with pytest.raises(RuntimeError, match="same shape"):
+        ext._check_gelu_weights(x, tiled, tiled[:16])
+    row = torch.empty(16384, 2048 // 8 + 1, dtype=torch.int32, device="meta")
+    ext._check_gelu_weights(x, row, row)
