@@ -214,11 +214,13 @@ int pi05w4a4_gelu_tanh_mul(const void* gate_fp16, const void* up_fp16, int64_t n
  * RMSNorm of fp16 rows, the input norm of every attention and MLP block ahead of the QKV
  * and gate/up activation quant.  No counterpart in the reference's W4A4 code: it replaces
  * transformers' GemmaRMSNorm module (modeling_gemma.py:64-78), which the reference runs
- * eagerly between its W4A4 ops, with one kernel of the same fp32 operation order:
- *   y = fp16((float(x) * rsqrt(mean(float(x)^2) + eps)) * (unit_offset + float(w))).
+ * eagerly between its W4A4 ops, with one kernel of the same fp32 operations:
+ *   y = fp16((float(x) * r) * (unit_offset + float(w))),
+ *   r = 1 / sqrt(sum(float(x)^2) * fp32(1/K) + eps)   (correctly rounded sqrt and division).
  * x, y fp16 [M, K] (may alias), w fp16 [K]; K % 8 == 0, K <= 16384; 16-byte aligned.
- * The sum of squares is reduced in another order than torch's, so a few outputs can
- * differ from the eager module's by one fp16 ulp.
+ * The sum of squares has the fixed lane order of pi05w4a4_rmsnorm_quantize's norm, so both
+ * entry points produce the same fp16 rows; torch sums in another order and rounds its
+ * rsqrt differently, so a few outputs can differ from the eager module's by one fp16 ulp.
  */
 int pi05w4a4_rmsnorm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
                      int64_t m, int32_t k, void* y_fp16, void* stream);
