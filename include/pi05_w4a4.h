@@ -202,6 +202,22 @@ int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* 
                        size_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free pi05w4a4_int4_gemm: quantize + GEMM of one MFMA-layout weight with the
+ * activation codes, row scales and split-K partials in a fixed device scratch array that
+ * the library holds on each GPU it runs on (PI05W4A4_NOALLOC_SCRATCH_BYTES, kept until the
+ * process ends) instead of caller buffers.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc); it calls no allocating routine.  Same
+ * arguments, checks and results as pi05w4a4_int4_gemm without qbuf / sabuf / workspace;
+ * a call whose buffers would exceed the scratch size fails with PI05W4A4_EINVAL before
+ * any launch.  Every call on one GPU shares that GPU's scratch: calls that overlap on one
+ * device (other streams, other host threads) race and must be serialised by the caller.
+ */
+#define PI05W4A4_NOALLOC_SCRATCH_BYTES (64u << 20)
+int pi05w4a4_int4_gemm_noalloc(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
+                               int32_t n, void* y_fp16, void* stream);
+
+/*
  * Elementwise y = fp16(gelu_tanh(gate) * up) on fp16 [n] arrays (y may alias either input),
  * with the arithmetic of pi05w4a4_gemm_gelu_up's epilogue.  Replaces the eager
  * `gelu(gate, approximate="tanh") * up` of the unfused MLP (apply.py:135-138); the result

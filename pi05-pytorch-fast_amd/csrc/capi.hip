@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/pi05_w4a4.h"
@@ -607,3 +608,76 @@ int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* 
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// Allocation-free int4_gemm (pi05w4a4_int4_gemm_noalloc).  The quantized activations, their
+// scales and the split-K partials of a call live in `scratch`, a fixed device array that
+// the code object holds on every GPU it is loaded on, instead of caller-allocated buffers.
+// In host code `scratch` names a host-side stand-in, never device memory: its device
+// address is looked up once per device with hipGetSymbolAddress and only that address is
+// passed to kernels.
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[PI05W4A4_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (hipGetSymbolAddress on its first use
+// there); sets the last error and returns null on failure.
+void* scratch_for_current_device() {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    fail(PI05W4A4_EHIP, "hipGetDevice: %s", hipGetErrorString(e));
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxScratchDevices) {
+    fail(PI05W4A4_EINVAL, "device %d is beyond the %d devices the scratch table holds", dev, kMaxScratchDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    const hipError_t se = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (se != hipSuccess || ptr == nullptr) {
+      fail(PI05W4A4_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(se));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+}  // namespace
+
+extern "C" int pi05w4a4_int4_gemm_noalloc(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,
+                                          int32_t n, void* y_fp16, void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  int rc = validate_weight(w_mfma, n, "weight");
+  if (rc) return rc;
+  if (m == 0) return ok();
+  if (x_fp16 == nullptr || y_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  // Scratch layout: codes + row corrections | row scales | split-K partials, 256-byte aligned.
+  const size_t q_bytes = align256(pi05w4a4_q_words(m, k) * sizeof(int32_t));
+  const size_t sa_bytes = align256(static_cast<size_t>(m) * sizeof(float));
+  const size_t ws_bytes = pi05w4a4_gemm_workspace_bytes(m, k, 1, &n, 0);
+  const size_t need = q_bytes + sa_bytes + ws_bytes;
+  if (need > PI05W4A4_NOALLOC_SCRATCH_BYTES)
+    return fail(PI05W4A4_EINVAL, "M=%lld K=%d N=%d needs %zu bytes of scratch, more than the %zu the library holds",
+                (long long)m, k, n, need, static_cast<size_t>(PI05W4A4_NOALLOC_SCRATCH_BYTES));
+  uint8_t* base = static_cast<uint8_t*>(scratch_for_current_device());
+  if (base == nullptr) return PI05W4A4_EHIP;
+  int32_t* q = reinterpret_cast<int32_t*>(base);
+  float* sa = reinterpret_cast<float*>(base + q_bytes);
+  void* ws = ws_bytes > 0 ? static_cast<void*>(base + q_bytes + sa_bytes) : nullptr;
+  // Nothing needs to start at zero: the quantizer writes every code, scale and correction
+  // that the GEMM keeps (pad rows and pad k codes meet discarded rows or zero weight
+  // words), and every split-K slice writes all of its partials before the reduce reads them.
+  return pi05w4a4_int4_gemm(x_fp16, m, k, w_mfma, n, y_fp16, q, sa, ws, ws_bytes, stream);
+}

@@ -76,6 +76,7 @@ def load_int4_gemm():
         "pi05w4a4_gemm_gelu_up": (ctypes.c_int, [vp, vp, i64, i32, vp, vp, i32, vp, vp, sz, vp]),
         "pi05w4a4_gemm_acc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_int4_gemm": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp, vp, vp, sz, vp]),
+        "pi05w4a4_int4_gemm_noalloc": (ctypes.c_int, [vp, i64, i32, vp, i32, vp, vp]),
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
         "pi05w4a4_gelu_tanh_mul": (ctypes.c_int, [vp, vp, i64, vp, vp]),
         "pi05w4a4_gemm_residual": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, sz, vp]),
