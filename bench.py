@@ -24,8 +24,9 @@ The dominant kernel of the forward (the gate/up GEMM with its fused GELU-tanh*up
 epilogue, ~32% of the forward) is the `roofline` object; its `traffic` (HBM bytes per
 launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under profiles/.
 
-`cpu_baseline` times the CPU oracle (numpy) on one decoder layer's W4A4 work at the
-same M and scales it to the full depth.
+`cpu_baseline` times the reference's W4A4 semantics in PyTorch on the host CPU (the
+oracle's torch restatement of pack.py:113-145, both integer matmul forms) on one decoder
+layer's projection calls at the same M and scales it to the full depth.
 
 Prints one JSON line.
 """
@@ -350,60 +351,91 @@ def read_traffic(kernel: str) -> tuple[float | None, str | None]:
 
 
 # ----------------------------------------------------------------------------- CPU baseline
-def cpu_baseline(tokens: int, batch: int, layers: int, budget_s: float) -> dict:
-    """CPU oracle (numpy) on one decoder layer's W4A4 work at M = tokens*batch, scaled to
-    `layers`.  Per GEMM: quantize the activation (fp32 FWHT + INT4), exact integer matmul
-    (fp32 BLAS), dequant to fp16."""
-    import numpy as np
-
-    from oracle import w4a4_oracle as orc
-
+def _cpu_model() -> str:
     try:
-        from threadpoolctl import threadpool_info
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = os.cpu_count() or 1
+
+def cpu_baseline(tokens: int, batch: int, layers: int, budget_s: float) -> dict:
+    """The reference's W4A4 semantics on the host CPU with PyTorch (oracle/w4a4_torch_cpu.py,
+    the restatement of pack.py:113-145): per projection call, fp32 FWHT + per-token INT4
+    quant, unpack of the packed weights, exact integer matmul, fp16 dequant -- one decoder
+    layer's calls at M = tokens * batch (QKV with one shared quant, o, gate/up with one shared
+    quant, down), each timed with both integer matmul forms (the reference's fp32
+    ``a @ b.T`` and ``torch._int_mm``): 2 warm-up calls, then the median of up to 5 calls.
+    The faster form of each call is summed and scaled to ``layers`` layers."""
+    import torch
+
+    from oracle import w4a4_torch_cpu as tcpu
+
+    torch.set_num_threads(os.cpu_count() or 1)
     m = tokens * batch
-    rng = np.random.default_rng(20260923)
+    gen = torch.Generator().manual_seed(20260923 + 4)
 
-    def act(k):
-        x = rng.standard_normal((m, k), dtype=np.float32)
-        x[:, rng.permutation(k)[: max(1, k // 100)]] *= 20.0
-        return x.astype(np.float16)
+    def act(k: int, geglu: bool = False) -> torch.Tensor:
+        if geglu:
+            g = torch.randn(m, k, generator=gen)
+            return (torch.nn.functional.gelu(g, approximate="tanh") * torch.randn(m, k, generator=gen)).half()
+        x = torch.randn(m, k, generator=gen)
+        x[:, torch.randperm(k, generator=gen)[: max(1, k // 100)]] *= 20.0
+        return x.half()
 
-    def wcodes(n, k):
-        return np.clip(np.rint(rng.standard_normal((n, k), dtype=np.float32) * 2), -7, 7).astype(np.int8)
+    def packed(n: int, k: int) -> torch.Tensor:
+        # codes ~ round(N(0, 2)) in [-7, 7] (a packed N(0, 0.02) weight's statistics), scale 0.01
+        codes = torch.randn(n, k, generator=gen).mul_(2.0).round_().clamp_(-7, 7).to(torch.int32) & 0xF
+        words = torch.zeros(n, k // 8, dtype=torch.int32)
+        c = codes.view(n, k // 8, 8)
+        for j in range(8):
+            words |= c[..., j] << (4 * j)
+        scale = torch.full((n, 1), 0.01, dtype=torch.float32).view(torch.int32)
+        return torch.cat([words, scale], dim=1)
 
-    shapes = [("qkv", 2048, 2560), ("o", 2048, 2048), ("gate_up", 2048, 32768), ("down", 16384, 2048)]
-    data = [(name, act(k), wcodes(n, k), np.full(n, 0.01, np.float32)) for name, k, n in shapes]
-
-    def one_layer():
-        for _, x, wc, sw in data:
-            q, sa = orc.quant_activation(x)
-            orc.dequant_fp16(orc.gemm_acc_int32(q, wc), sa, sw)
-
-    times = []
+    calls = [("qkv", act(2048), [packed(2048, 2048), packed(256, 2048), packed(256, 2048)]),
+             ("o", act(2048), [packed(2048, 2048)]),
+             ("gate_up", act(2048), [packed(16384, 2048), packed(16384, 2048)]),
+             ("down", act(16384, geglu=True), [packed(2048, 16384)])]
+    per_gemm = {}
     t_start = time.perf_counter()
-    one_layer()  # warm-up
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
-        t0 = time.perf_counter()
-        one_layer()
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > 4 * budget_s:
-            break
-    per_layer = statistics.median(times)
+    for name, x, ws in calls:
+        row = {}
+        for method in ("fp32", "int_mm"):
+            fn = lambda: tcpu.int4_gemm_ref(x, ws, method)  # noqa: E731
+            fn()
+            t0 = time.perf_counter()
+            fn()
+            one = time.perf_counter() - t0
+            reps = 5 if one * 5 < budget_s / 8 else 3
+            times = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                times.append(time.perf_counter() - t0)
+            row[method] = round(statistics.median(times) * 1e3, 2)
+        row["best"] = min(("fp32", "int_mm"), key=lambda k_: row[k_])
+        per_gemm[name] = row
+    per_layer_ms = sum(r[r["best"]] for r in per_gemm.values())
     return {
-        "value": round(per_layer * layers * 1e3, 1),
+        "value": round(per_layer_ms * layers, 1),
         "unit": "ms",
-        "cores": threads,
+        "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": (
-            f"one decoder layer of W4A4 work at M={m} (4 activation quants + QKV/o/gate-up/down "
-            f"integer GEMMs + fp16 dequant), median of {len(times)} runs x {layers} layers; "
-            f"numpy oracle, fp32-BLAS exact integer matmul, {threads} threads, "
-            f"os.cpu_count()={os.cpu_count()}; attention/norms not included"
+            f"one decoder layer's W4A4 projection calls at M={m} (QKV and gate/up with one shared "
+            f"activation quant each, o, down), each: fp32 FWHT + INT4 quant, weight unpack, exact "
+            f"integer matmul, fp16 dequant (pack.py:113-145 semantics in PyTorch CPU); the faster of "
+            f"the fp32 and torch._int_mm matmul per call, x {layers} layers; attention and norms not "
+            f"included; {round(time.perf_counter() - t_start, 1)} s of CPU timing"
         ),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "torch_threads": torch.get_num_threads(),
+        "per_gemm_ms": per_gemm,
+        "per_layer_ms": round(per_layer_ms, 2),
     }
 
 

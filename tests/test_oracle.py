@@ -290,3 +290,41 @@ def test_rms_norm_lanes_sum_order():
     h = orc.rms_norm_lanes(x, w, 0.0).astype(np.float64)
     r = 1.0 / np.sqrt((v * v).mean(axis=1))
     assert np.allclose(h, v * r[:, None], rtol=2**-10, atol=2**-14)
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 64, 16), (17, 2048, 48), (3, 16384, 16), (24, 192, 8), (40, 1024, 32)])
+def test_torch_cpu_baseline_matches_numpy_oracle(m, k, n):
+    """The PyTorch-CPU restatement that bench.py times (both integer matmul forms) gives the
+    numpy oracle's codes, scale bits and fp16 outputs bit for bit."""
+    import torch
+
+    from oracle import w4a4_torch_cpu as tcpu
+
+    rng = np.random.default_rng(m * 131 + k + n)
+    x = rng.standard_normal((m, k), dtype=np.float32)
+    x[:, rng.permutation(k)[: max(1, k // 100)]] *= 20.0
+    x = x.astype(np.float16)
+    packed = orc.pack_linear_weight(rng.standard_normal((n, k), dtype=np.float32) * 0.02)
+    q_ref, s_ref = orc.quant_activation(x)
+    q, s = tcpu.quant_activation(torch.from_numpy(x))
+    assert np.array_equal(q.numpy(), q_ref)
+    assert np.array_equal(s.numpy().view(np.int32), s_ref.view(np.int32))
+    want = orc.int4_gemm_ref(x, packed)
+    for method in ("fp32", "int_mm"):
+        if method == "int_mm" and m <= 16:
+            continue  # torch._int_mm takes more than 16 rows
+        (y,) = tcpu.int4_gemm_ref(torch.from_numpy(x), [torch.from_numpy(packed)], method)
+        assert np.array_equal(y.numpy().view(np.int16), want.view(np.int16)), method
+
+
+def test_torch_cpu_unpack_all_nibbles():
+    """Every nibble value (including -8) unpacks as the numpy oracle does."""
+    import torch
+
+    from oracle import w4a4_torch_cpu as tcpu
+
+    words = np.arange(-(2**31), 2**31, 2**20 + 12345, dtype=np.int64).astype(np.int32)[:256].reshape(16, 16)
+    packed = np.concatenate([words, np.full((16, 1), np.float32(0.5).view(np.int32), np.int32)], axis=1)
+    q, s = tcpu.unpack_weight(torch.from_numpy(packed))
+    q_ref, s_ref, _ = orc.unpack_linear_weight(packed)
+    assert np.array_equal(q.numpy(), q_ref) and np.array_equal(s.numpy(), s_ref)
