@@ -23,16 +23,20 @@ __device__ __forceinline__ float gelu_tanh_exact(float x) {
 }
 
 // fp16 bits of the fast evaluation: tanh(u) = 1 - 2 / (1 + 2^(2u log2 e)) from the
-// hardware exp2 and reciprocal, a third of the instructions of tanhf.  Every operation is
-// a single IEEE fp32 operation or one hardware instruction, so the result is the same in
-// every kernel that inlines this.  It differs from the exact expression's fp16 result on
-// 428 of the 65536 fp16 inputs: 426 with x in [-8, -1) (mostly x in [-5.2, -3], where
-// 1 + tanh cancels to a few ulps) and 2 single-ulp roundings elsewhere.
+// hardware exp2 and reciprocal, with 2u log2 e = x * (K0 + K1 x^2) (K0 = 2 log2(e)
+// sqrt(2/pi), K1 = K0 * 0.044715), and y = (0.5 x)(1 + tanh(u)) as in the exact
+// expression, so that the cancellation of 1 + tanh for negative x and the rounding of
+// 0.5 x for tiny x follow it.  Every operation is a single IEEE fp32 operation or one
+// hardware instruction, so the result is the same in every kernel that inlines this.  It
+// differs from the exact expression's fp16 result on a few hundred of the 65536 fp16
+// inputs, all with |x| in [2^-4, 5.3) (mostly negative x in [-5.2, -2], where 1 + tanh
+// cancels to a few ulps), by at most a few ulps: gelu_tanh_fix.inc lists them.
+constexpr float kGeluK0 = 2.3022081983184814f;   // 2 log2(e) sqrt(2/pi)
+constexpr float kGeluK1 = 0.10294324159622192f;  // K0 * 0.044715
 __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
 #pragma clang fp contract(off)
-  const float x3 = (x * x) * x;
-  const float inner = 0.7978845608028654f * __builtin_fmaf(0.044715f, x3, x);
-  const float e = __builtin_amdgcn_exp2f(inner * 2.8853900817779268f);  // exp(2 inner)
+  const float q = x * __builtin_fmaf(x * x, kGeluK1, kGeluK0);  // 2 log2(e) * inner
+  const float e = __builtin_amdgcn_exp2f(q);                     // exp(2 inner)
   const float t = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
   float y = (0.5f * x) * (1.0f + t);
   asm volatile("" : "+v"(y));
@@ -41,19 +45,22 @@ __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
 
 // Corrections: the exact result's fp16 bit pattern minus the fast one's, for the inputs
 // where they differ (gelu_tanh_fix.inc, generated on the GPU from these two functions by
-// gelu_fix_gen.hip; the exhaustive test compares every fp16 input with torch).  Those in
-// the window of negative x with |x| in [1, 8) (bit patterns 0xbc00 .. 0xc7ff: 426 of
-// the 428) go to a 3 KB int8 table indexed by bits - kGeluFixBase; the others (2) are
-// compared one by one.
-constexpr uint32_t kGeluFixBase = 0xbc00u;
-constexpr uint32_t kGeluFixSpan = 3u << 10;
-constexpr int kGeluFixEntries = kGeluFixSpan;
+// gelu_fix_gen.hip; the exhaustive test compares every fp16 input with torch).  They all
+// lie in the window |x| bits in [kGeluFixAbsBase, kGeluFixAbsBase + kGeluFixHalf - 1), and
+// the int8 table holds one half of kGeluFixHalf entries per sign, indexed by the |x| bits
+// minus the base; the last entry of each half is 0 and takes every input outside the
+// window (the index is clamped, and |x| bits below the base wrap to large values).
+constexpr uint32_t kGeluFixAbsBase = 0x2c00u;
+constexpr uint32_t kGeluFixHalf = 6656u;
+constexpr int kGeluFixEntries = 2 * kGeluFixHalf;  // 13 KB
 
-// Index of fp16 bit pattern xb in the table (0 outside the window, where *in is false).
-__device__ __forceinline__ uint32_t gelu_fix_index(uint32_t xb, bool& in) {
-  const uint32_t off = xb - kGeluFixBase;
-  in = off < kGeluFixSpan;
-  return in ? off : 0u;
+// Table slot of fp16 bit pattern xb (zero-extended): four ALU instructions.
+__host__ __device__ constexpr uint32_t gelu_fix_index(uint32_t xb) {
+  const uint32_t off = (xb & 0x7fffu) - kGeluFixAbsBase;
+  return (off < kGeluFixHalf - 1 ? off : kGeluFixHalf - 1) + (xb >> 15) * kGeluFixHalf;
+}
+__host__ __device__ constexpr bool gelu_fix_in_window(uint32_t xb) {
+  return ((xb & 0x7fffu) - kGeluFixAbsBase) < kGeluFixHalf - 1;
 }
 
 }  // namespace w4a4

@@ -77,7 +77,7 @@ __device__ __forceinline__ v4i unpack_w(uint32_t x, uint32_t y) {
 }
 
 // GELU-tanh correction table (gelu_tanh.h), built at compile time from the generated
-// list of {index, exact - fast} pairs.
+// list of {fp16 bits, exact - fast} pairs.
 struct GeluFixEntry {
   uint16_t bits;
   int8_t d;
@@ -85,42 +85,21 @@ struct GeluFixEntry {
 constexpr GeluFixEntry kGeluFixList[] = {
 #include "gelu_tanh_fix.inc"
 };
-constexpr bool gelu_fix_in_window(uint32_t bits) { return bits - kGeluFixBase < kGeluFixSpan; }
 struct alignas(16) GeluFixTable {
   int8_t v[kGeluFixEntries];
 };
 constexpr GeluFixTable make_gelu_fix() {
   GeluFixTable t{};
-  for (const GeluFixEntry& e : kGeluFixList)
-    if (gelu_fix_in_window(e.bits)) t.v[e.bits - kGeluFixBase] = e.d;
+  for (const GeluFixEntry& e : kGeluFixList) t.v[gelu_fix_index(e.bits)] = e.d;
   return t;
 }
 __device__ const GeluFixTable kGeluFix = make_gelu_fix();
-constexpr int count_gelu_strays() {
-  int n = 0;
-  for (const GeluFixEntry& e : kGeluFixList) n += gelu_fix_in_window(e.bits) ? 0 : 1;
-  return n;
-}
-constexpr int kGeluStrays = count_gelu_strays();
-static_assert(kGeluStrays <= 4, "corrections outside the table window are compared one by one");
-struct GeluStrays {
-  GeluFixEntry e[kGeluStrays > 0 ? kGeluStrays : 1];
-};
-constexpr GeluStrays make_gelu_strays() {
-  GeluStrays s{};
-  int n = 0;
+constexpr bool gelu_fixes_in_window() {
   for (const GeluFixEntry& e : kGeluFixList)
-    if (!gelu_fix_in_window(e.bits)) s.e[n++] = e;
-  return s;
+    if (!gelu_fix_in_window(e.bits)) return false;
+  return true;
 }
-constexpr GeluStrays kGeluStrayList = make_gelu_strays();
-
-// Correction of fp16 input bits xb outside the table window (0 for all but the strays).
-__device__ __forceinline__ int gelu_stray_fix(uint32_t xb, int d) {
-#pragma unroll
-  for (int i = 0; i < kGeluStrays; ++i) d = (xb == kGeluStrayList.e[i].bits) ? kGeluStrayList.e[i].d : d;
-  return d;
-}
+static_assert(gelu_fixes_in_window(), "every GELU correction lies in the table window");
 
 // torch.nn.functional.gelu(x, approximate="tanh") of an fp16 value, bit for bit: the fast
 // evaluation plus the table's correction (`fix` is the table in global memory or LDS).
@@ -129,10 +108,9 @@ __device__ __forceinline__ int gelu_stray_fix(uint32_t xb, int d) {
 // exhaustive comparison covers all cases.
 __device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh, const int8_t* fix) {
   const uint32_t xb = __builtin_bit_cast(uint16_t, xh);
-  bool in;
-  const int d = fix[gelu_fix_index(xb, in)];
+  const int d = fix[gelu_fix_index(xb)];
   const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(xh));
-  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + gelu_stray_fix(xb, in ? d : 0)));
+  return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + d));
 }
 
 // fp16 * fp16 as torch's eager mul: one fp32 product rounded to fp16.
@@ -493,23 +471,23 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
           const v4i su = acc[mi][ni + NI / 2];
           const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
           // The four table lookups are issued ahead of the GELU arithmetic, which hides
-          // their LDS latency.
-          _Float16 g16[4], u16[4];
+          // their LDS latency.  The product with up is a packed fp16 multiply: the product
+          // of two fp16 values is exact in fp32, so one fp16 rounding of it is the eager
+          // fp16 mul's result (fp32 product, rounded to fp16).
+          _Float16 g16[4];
+          half4 u16;
           int fix[4];
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             g16[r] = dequant(s[r], sv[mi], swv[r]);
             u16[r] = dequant(su[r], sv[mi], swu[r]);
-            bool in;
-            const uint32_t xb = __builtin_bit_cast(uint16_t, g16[r]);
-            const int d = fix_lds[gelu_fix_index(xb, in)];
-            fix[r] = gelu_stray_fix(xb, in ? d : 0);
+            fix[r] = fix_lds[gelu_fix_index(__builtin_bit_cast(uint16_t, g16[r]))];
           }
+          half4 gl;
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(g16[r])) + fix[r];
-            o[r] = mul_f16(__builtin_bit_cast(_Float16, static_cast<uint16_t>(fb)), u16[r]);
-          }
+          for (int r = 0; r < 4; ++r)
+            gl[r] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(gelu_tanh_fast_bits(static_cast<float>(g16[r])) + fix[r]));
+          o = gl * u16;
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = dequant(s[r], sv[mi], swv[r]);
