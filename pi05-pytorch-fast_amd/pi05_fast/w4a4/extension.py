@@ -23,6 +23,7 @@ There is no CPU fallback: without the library (or without a GPU) the ops raise.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import weakref
@@ -107,12 +108,72 @@ def _check(rc: int, what: str) -> None:
         raise RuntimeError(f"{what} failed ({rc}): {msg}")
 
 
-def _stream(device: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+# The current stream of a device as a raw pointer value (torch.cuda.current_stream(d)
+# .cuda_stream without building Stream objects), and tensor pointers as plain ints (the
+# ctypes argtypes convert them): the ops' host path runs once per projection in eager use.
+_raw_stream = torch._C._cuda_getCurrentRawStream
 
 
-def _ptr(t: torch.Tensor | None) -> ctypes.c_void_p:
-    return ctypes.c_void_p(0 if t is None else t.data_ptr())
+def _stream(device: torch.device) -> int:
+    idx = device.index
+    return _raw_stream(torch._C._cuda_getDevice() if idx is None else idx)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+_NO_SWITCH = contextlib.nullcontext()
+
+
+def _on_device(device: torch.device):
+    """torch.cuda.device(device), or nothing when it is already the current device (the
+    library launches on the current HIP device)."""
+    idx = device.index
+    if idx is None or idx == torch._C._cuda_getDevice():
+        return _NO_SWITCH
+    return torch.cuda.device(device)
+
+
+def _q_words(m: int, k: int) -> int:
+    """pi05w4a4_q_words: activation code words of M rows (16-row blocks x 128-deep k
+    blocks of 256 words) followed by one row correction per row of those blocks."""
+    if m <= 0 or k <= 0:
+        return 0
+    mb = (m + 15) // 16
+    return mb * 16 * ((k + 127) // 128) * 16 + mb * 16
+
+
+_WS_CACHE: dict[tuple, int] = {}
+_KV_ELEMS: dict[tuple, int] = {}
+_N_ARRAYS: dict[tuple, ctypes.Array] = {}
+
+
+def _n_array(ns: tuple) -> ctypes.Array:
+    arr = _N_ARRAYS.get(ns)
+    if arr is None:
+        arr = _N_ARRAYS[ns] = (ctypes.c_int32 * len(ns))(*ns)
+    return arr
+
+
+def _workspace_bytes(lib, device: torch.device, m: int, k: int, ns: tuple, gelu: bool) -> int:
+    """pi05w4a4_gemm_workspace_bytes, cached per shape and device (the split-K plan
+    depends on the device's CU count)."""
+    key = (device.index, m, k, ns, gelu)
+    nbytes = _WS_CACHE.get(key)
+    if nbytes is None:
+        with _on_device(device):
+            nbytes = _WS_CACHE[key] = int(lib.pi05w4a4_gemm_workspace_bytes(m, k, len(ns), _n_array(ns),
+                                                                             1 if gelu else 0))
+    return nbytes
+
+
+def _kv_mfma_elems(lib, b: int, s: int, kvh: int, d: int) -> int:
+    key = (b, s, kvh, d)
+    n = _KV_ELEMS.get(key)
+    if n is None:
+        n = _KV_ELEMS[key] = int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d))
+    return n
 
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
@@ -190,20 +251,21 @@ def quantize(x: torch.Tensor, warm: list[torch.Tensor] | None = None) -> tuple[t
     to 128 codes.
     """
     k = _check_x(x)
-    x2 = x.contiguous()
+    x2 = x if x.is_contiguous() else x.contiguous()
     if x2.data_ptr() % 16:
         x2 = x2.clone()
     m = x2.numel() // k
-    lib = load_int4_gemm()
-    q = torch.empty((int(lib.pi05w4a4_q_words(m, k)),), dtype=torch.int32, device=x2.device)
-    sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    lib = load_int4_gemm()
-    with torch.cuda.device(x2.device):
-        wa = _warm_args(warm, "quantize")
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = x2.device
+    q = torch.empty((_q_words(m, k),), dtype=torch.int32, device=dev)
+    sa = torch.empty((m,), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        wa = _warm_args(warm, "quantize") if warm else None
         if wa is None:
-            _check(lib.pi05w4a4_quantize(_ptr(x2), m, k, _ptr(q), _ptr(sa), _stream(x2.device)), "pi05w4a4_quantize")
+            _check(lib.pi05w4a4_quantize(x2.data_ptr(), m, k, q.data_ptr(), sa.data_ptr(), _stream(dev)),
+                   "pi05w4a4_quantize")
         else:
-            _check(lib.pi05w4a4_quantize_warm(_ptr(x2), m, k, _ptr(q), _ptr(sa), *wa, _stream(x2.device)),
+            _check(lib.pi05w4a4_quantize_warm(x2.data_ptr(), m, k, q.data_ptr(), sa.data_ptr(), *wa, _stream(dev)),
                    "pi05w4a4_quantize_warm")
     return q, sa
 
@@ -298,9 +360,9 @@ def _check_residual(residual: torch.Tensor, device: torch.device, shape: tuple) 
 def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, residual=None):
     """Shared-activation GEMMs of 1..3 MFMA-layout weights (one launch); with ``residual``
     (one weight) the epilogue adds it: fp16(fp16(y) + residual)."""
-    lib = load_int4_gemm()
+    lib = _lib if _lib is not None else load_int4_gemm()
     m = int(sa.size(0))
-    ns = [int(w.size(0)) for (w, _) in weights]
+    ns = tuple(int(w.size(0)) for (w, _) in weights)
     if residual is not None:
         (w0, n_true), = weights
         if n_true != ns[0]:
@@ -309,31 +371,26 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, 
         _check_residual(residual, device, (*out_shape_prefix, n_true))
         res = residual if residual.is_contiguous() and residual.data_ptr() % 16 == 0 else residual.contiguous().clone()
         out = torch.empty((m, n_true), dtype=torch.float16, device=device)
-        ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, 1, (ctypes.c_int32 * 1)(n_true), 0)
+        ws_bytes = _workspace_bytes(lib, device, m, k, ns, False)
         ws = _workspace(device, ws_bytes)
-        _check(lib.pi05w4a4_gemm_residual(_ptr(q), _ptr(sa), m, k, _ptr(w0), n_true, _ptr(res), _ptr(out),
-                                          _ptr(ws), ws_bytes, _stream(device)), "pi05w4a4_gemm_residual")
+        _check(lib.pi05w4a4_gemm_residual(q.data_ptr(), sa.data_ptr(), m, k, w0.data_ptr(), n_true, res.data_ptr(),
+                                          out.data_ptr(), _ptr(ws), ws_bytes, _stream(device)),
+               "pi05w4a4_gemm_residual")
         return [out.view(*out_shape_prefix, n_true)]
-    if gelu:
-        n = ns[0]
-        outs = [torch.empty((m, n), dtype=torch.float16, device=device)]
-        out_ptrs = [outs[0], outs[0]]
-    else:
-        outs = [torch.empty((m, nn), dtype=torch.float16, device=device) for nn in ns]
-        out_ptrs = outs
-    g = len(weights)
-    n_arr = (ctypes.c_int32 * g)(*ns)
-    ws_bytes = lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0)
+    ws_bytes = _workspace_bytes(lib, device, m, k, ns, gelu)
     ws = _workspace(device, ws_bytes)
     stream = _stream(device)
     if gelu:
-        rc = lib.pi05w4a4_gemm_gelu_up(_ptr(q), _ptr(sa), m, k, _ptr(weights[0][0]),
-                                       _ptr(weights[1][0]), ns[0], _ptr(outs[0]), _ptr(ws),
-                                       ws_bytes, stream)
+        outs = [torch.empty((m, ns[0]), dtype=torch.float16, device=device)]
+        rc = lib.pi05w4a4_gemm_gelu_up(q.data_ptr(), sa.data_ptr(), m, k, weights[0][0].data_ptr(),
+                                       weights[1][0].data_ptr(), ns[0], outs[0].data_ptr(), _ptr(ws), ws_bytes,
+                                       stream)
     else:
+        outs = [torch.empty((m, nn), dtype=torch.float16, device=device) for nn in ns]
+        g = len(ns)
         w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for (w, _) in weights])
-        y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in out_ptrs])
-        rc = lib.pi05w4a4_gemm_multi(_ptr(q), _ptr(sa), m, k, g, w_arr, n_arr, y_arr, _ptr(ws),
+        y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in outs])
+        rc = lib.pi05w4a4_gemm_multi(q.data_ptr(), sa.data_ptr(), m, k, g, w_arr, _n_array(ns), y_arr, _ptr(ws),
                                      ws_bytes, stream)
     _check(rc, "pi05w4a4_gemm")
     results = []
@@ -353,17 +410,18 @@ def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
         raise RuntimeError(f"the fused RMSNorm quantizer takes K = 2048, got {k}")
     if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 1 or weight.numel() != k:
         raise RuntimeError(f"RMSNorm weight must be a float16 CUDA/HIP tensor [{k}]")
-    x2 = x.contiguous()
+    x2 = x if x.is_contiguous() else x.contiguous()
     if x2.data_ptr() % 16:
         x2 = x2.clone()
-    w = weight.contiguous()
+    w = weight if weight.is_contiguous() else weight.contiguous()
     m = x2.numel() // k
-    lib = load_int4_gemm()
-    q = torch.empty((int(lib.pi05w4a4_q_words(m, k)),), dtype=torch.int32, device=x2.device)
-    sa = torch.empty((m,), dtype=torch.float32, device=x2.device)
-    with torch.cuda.device(x2.device):
-        _check(lib.pi05w4a4_rmsnorm_quantize(_ptr(x2), _ptr(w), float(eps), 1 if unit_offset else 0, m, k,
-                                             _ptr(q), _ptr(sa), _stream(x2.device)), "pi05w4a4_rmsnorm_quantize")
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = x2.device
+    q = torch.empty((_q_words(m, k),), dtype=torch.int32, device=dev)
+    sa = torch.empty((m,), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        _check(lib.pi05w4a4_rmsnorm_quantize(x2.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0, m, k,
+                                             q.data_ptr(), sa.data_ptr(), _stream(dev)), "pi05w4a4_rmsnorm_quantize")
     return q, sa
 
 
@@ -380,9 +438,9 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
         if tiled:
             _check_tiled(w, k)
         conv.append(_as_mfma(w, k, tiled))
-    with torch.cuda.device(x.device):
-        return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), x.device, kind, gelu=gelu,
-                            residual=residual)
+    dev = x.device
+    with _on_device(dev):
+        return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), dev, kind, gelu=gelu, residual=residual)
 
 
 def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool) -> torch.Tensor:
@@ -397,10 +455,11 @@ def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offse
     w = weight if weight.is_contiguous() else weight.contiguous()
     y = torch.empty_like(xc)
     m = xc.numel() // k if k else 0
-    lib = load_int4_gemm()
-    with torch.cuda.device(x.device):
-        _check(lib.pi05w4a4_rmsnorm(_ptr(xc), _ptr(w), float(eps), 1 if unit_offset else 0, m, k,
-                                    _ptr(y), _stream(x.device)), "pi05w4a4_rmsnorm")
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = x.device
+    with _on_device(dev):
+        _check(lib.pi05w4a4_rmsnorm(xc.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0, m, k,
+                                    y.data_ptr(), _stream(dev)), "pi05w4a4_rmsnorm")
     return y
 
 
@@ -413,12 +472,13 @@ def gelu_tanh_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
         raise RuntimeError("gelu_tanh_mul expects float16 tensors")
     if gate.shape != up.shape:
         raise RuntimeError(f"gelu_tanh_mul shapes differ: {tuple(gate.shape)} vs {tuple(up.shape)}")
-    g = gate.contiguous()
-    u = up.contiguous()
+    g = gate if gate.is_contiguous() else gate.contiguous()
+    u = up if up.is_contiguous() else up.contiguous()
     y = torch.empty_like(g)
-    lib = load_int4_gemm()
-    with torch.cuda.device(gate.device):
-        _check(lib.pi05w4a4_gelu_tanh_mul(_ptr(g), _ptr(u), g.numel(), _ptr(y), _stream(gate.device)),
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = gate.device
+    with _on_device(dev):
+        _check(lib.pi05w4a4_gelu_tanh_mul(g.data_ptr(), u.data_ptr(), g.numel(), y.data_ptr(), _stream(dev)),
                "pi05w4a4_gelu_tanh_mul")
     return y
 
@@ -481,30 +541,27 @@ def _prefix_attention_impl(
     qc, kc, vc = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
     cs = [t.expand(b, s, d).contiguous() if t.dim() == 3 else t.reshape(b, s, d).contiguous() for t in (cos, sin)]
     m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s, q.device)
-    lib = load_int4_gemm()
-    k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=q.device)
-    kv_mfma = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, kvh, d)), dtype=torch.float16, device=q.device)
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = q.device
+    k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=dev)
+    kv_mfma = torch.empty(_kv_mfma_elems(lib, b, s, kvh, d), dtype=torch.float16, device=dev)
     if not (need_out or quantize_out):
         raise RuntimeError("prefix_attention: the output can only be dropped when it is quantized")
-    out = torch.empty((b, s, h * d) if need_out else (0,), dtype=torch.float16, device=q.device)
+    out = torch.empty((b, s, h * d) if need_out else (0,), dtype=torch.float16, device=dev)
     out_ptr = _ptr(out) if need_out else None
     codes = scales = None
     if quantize_out:
-        codes = torch.empty((int(lib.pi05w4a4_q_words(b * s, h * d)),), dtype=torch.int32, device=q.device)
-        scales = torch.empty((b * s,), dtype=torch.float32, device=q.device)
-    with torch.cuda.device(q.device):
-        st = _stream(q.device)
+        codes = torch.empty((_q_words(b * s, h * d),), dtype=torch.int32, device=dev)
+        scales = torch.empty((b * s,), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        st = _stream(dev)
         _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
                                          _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
-        ws = [t for t in (warm or []) if t is not None and t.numel() > 0]
-        if ws:
-            if len(ws) > 4 or any((not t.is_cuda) or (not t.is_contiguous()) for t in ws):
-                raise RuntimeError("prefix_attention: warm takes up to 4 contiguous CUDA/HIP tensors")
-            wp = (ctypes.c_void_p * len(ws))(*[t.data_ptr() for t in ws])
-            wb = (ctypes.c_size_t * len(ws))(*[(t.numel() * t.element_size()) // 16 * 16 for t in ws])
+        wa = _warm_args(warm, "prefix_attention") if warm else None
+        if wa is not None:
             _check(lib.pi05w4a4_prefix_attention_warm(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
                                                       _ptr(m), mbs, mrs, mlen, float(scaling), b, s, h, kvh, d,
-                                                      out_ptr, h * d, _ptr(codes), _ptr(scales), wp, wb, len(ws),
+                                                      out_ptr, h * d, _ptr(codes), _ptr(scales), *wa,
                                                       st), "pi05w4a4_prefix_attention_warm")
         else:
             _check(lib.pi05w4a4_prefix_attention(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
@@ -532,7 +589,7 @@ def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, n
         out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
                                                             num_kv_heads, quantize_out=True, warm=warm,
                                                             need_out=return_out)
-        with torch.cuda.device(q.device):
+        with _on_device(q.device):
             y = _gemm_from_q(codes, scales, k_in, [(w, n_true)], lead, q.device, "int4_gemm", residual=residual)[0]
         return y, k_rope, out
     out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, warm=warm)
@@ -695,23 +752,51 @@ def _register_custom_op() -> None:
 _register_custom_op()
 
 
+# Eager calls skip the torch.ops dispatcher (tens of microseconds of host time per call,
+# several per decoder layer) when nothing needs it: plain tensors, no autograd graph to
+# record, no Dynamo trace, no dispatch or function mode.  The direct and the dispatched
+# route run the same implementation.
+_is_compiling = torch.compiler.is_compiling
+_dispatch_modes = torch._C._len_torch_dispatch_stack
+_function_modes = torch._C._is_torch_function_mode_enabled
+_PLAIN = (torch.Tensor, torch.nn.Parameter)
+
+
+def _direct(*ts) -> bool:
+    if _is_compiling() or _dispatch_modes() or _function_modes():
+        return False
+    grad = torch.is_grad_enabled()
+    for t in ts:
+        if t is not None and (type(t) not in _PLAIN or (grad and t.requires_grad)):
+            return False
+    return True
+
+
 def int4_gemm(x: torch.Tensor, packed_w: torch.Tensor) -> torch.Tensor:
     """Compiled-graph-friendly INT4 GEMM. x: fp16 [..., K], packed: int32 [N, K/8+1|+P|+16]."""
+    if _direct(x, packed_w):
+        return _run(x, [packed_w], tiled=False, kind="gemm")[0]
     return torch.ops.pi05_w4a4.int4_gemm(x, packed_w)
 
 
 def int4_gemm_tiled(x: torch.Tensor, packed_w: torch.Tensor) -> torch.Tensor:
     """INT4 GEMM with fragment-major weights (WMMA-tiled K/8+9 or MFMA K/8+16)."""
+    if _direct(x, packed_w):
+        return _run(x, [packed_w], tiled=True, kind="gemm")[0]
     return torch.ops.pi05_w4a4.int4_gemm_tiled(x, packed_w)
 
 
 def int4_gemm2(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Shared activation quant plus two INT4 GEMMs (one launch)."""
+    if _direct(x, w0, w1):
+        return tuple(_run(x, [w0, w1], tiled=False, kind="gemm2"))
     return torch.ops.pi05_w4a4.int4_gemm2(x, w0, w1)
 
 
 def int4_gemm2_tiled(x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     """Shared activation quant plus two fragment-major INT4 GEMMs."""
+    if _direct(x, w0, w1):
+        return tuple(_run(x, [w0, w1], tiled=True, kind="gemm2"))
     return torch.ops.pi05_w4a4.int4_gemm2_tiled(x, w0, w1)
 
 
@@ -719,11 +804,16 @@ def int4_gemm3(
     x: torch.Tensor, w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Shared activation quant plus three INT4 GEMMs (QKV, one launch)."""
+    if _direct(x, w0, w1, w2):
+        return tuple(_run(x, [w0, w1, w2], tiled=False, kind="gemm3"))
     return torch.ops.pi05_w4a4.int4_gemm3(x, w0, w1, w2)
 
 
 def int4_gemm2_gelu(x: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     """h = gelu_tanh(x @ W_gate^T) * (x @ W_up^T) with one shared activation quant."""
+    if _direct(x, w_gate, w_up):
+        _check_gelu_weights(x, w_gate, w_up)
+        return _run(x, [w_gate, w_up], tiled=False, kind="gemm2_gelu", gelu=True)[0]
     return torch.ops.pi05_w4a4.int4_gemm2_gelu(x, w_gate, w_up)
 
 
@@ -747,18 +837,27 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: boo
     """RMSNorm over the last dim in one kernel: fp16((x * rsqrt(mean(x^2) + eps)) *
     (unit_offset + weight)), fp32 inside (transformers GemmaRMSNorm semantics when
     ``unit_offset``)."""
+    if _direct(x, weight):
+        return _rms_norm_impl(x, weight, float(eps), bool(unit_offset))
     return torch.ops.pi05_w4a4.rms_norm(x, weight, float(eps), bool(unit_offset))
 
 
 def rms_norm_int4_gemm3(x, norm_weight, eps, w0, w1, w2, unit_offset=True):
     """int4_gemm3 of rms_norm(x): the decoder's input norm fused into the QKV activation
     quant (K = 2048)."""
+    if _direct(x, norm_weight, w0, w1, w2):
+        return tuple(_run(x, [w0, w1, w2], tiled=False, kind="int4_gemm3",
+                          norm=(norm_weight, float(eps), bool(unit_offset))))
     return torch.ops.pi05_w4a4.rms_norm_int4_gemm3(x, norm_weight, float(eps), bool(unit_offset), w0, w1, w2)
 
 
 def rms_norm_int4_gemm2_gelu(x, norm_weight, eps, w_gate, w_up, unit_offset=True):
     """int4_gemm2_gelu of rms_norm(x): the post-attention norm fused into the gate/up
     activation quant (K = 2048)."""
+    if _direct(x, norm_weight, w_gate, w_up):
+        _check_gelu_weights(x, w_gate, w_up)
+        return _run(x, [w_gate, w_up], tiled=False, kind="int4_gemm2_gelu", gelu=True,
+                    norm=(norm_weight, float(eps), bool(unit_offset)))[0]
     return torch.ops.pi05_w4a4.rms_norm_int4_gemm2_gelu(x, norm_weight, float(eps), bool(unit_offset),
                                                         w_gate, w_up)
 
@@ -770,6 +869,8 @@ def int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.
     ``warm``: up to four device tensors that the K = 16384 activation quant's idle
     workgroup slots read into the Infinity Cache (``pi05w4a4_quantize_warm``; results
     unchanged)."""
+    if _direct(x, packed_w, residual):
+        return _run(x, [packed_w], tiled=False, kind="int4_gemm", residual=residual, warm=warm)[0]
     return torch.ops.pi05_w4a4.int4_gemm_residual(x, packed_w, residual, list(warm or []))
 
 
@@ -784,6 +885,8 @@ def prefix_attention(
     [B|1, 1, S, >=S].  Returns (attention output [B, S, H*256], key states with RoPE
     [B, KVH, S, 256]): transformers' apply_rotary_pos_emb + eager_attention_forward, the
     key states bit-identical to the eager ones."""
+    if _direct(q, k, v, cos, sin, mask):
+        return _prefix_attention_impl(q, k, v, cos, sin, mask, float(scaling), int(num_heads), int(num_kv_heads))
     return torch.ops.pi05_w4a4.prefix_attention(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
                                                 int(num_kv_heads))
 
@@ -798,6 +901,9 @@ def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_
     read into the Infinity Cache (results unchanged).  ``return_out=False``: a caller that
     does not use the attention output gets an empty tensor in its place, and the kernel
     skips writing it when it quantizes the output itself."""
+    if _direct(q, k, v, cos, sin, mask, w_o, residual):
+        return _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
+                                             int(num_kv_heads), w_o, residual, warm, bool(return_out))
     return torch.ops.pi05_w4a4.prefix_attention_o_proj(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
                                                        int(num_kv_heads), w_o, residual, list(warm or []),
                                                        bool(return_out))

@@ -228,6 +228,42 @@ def test_library_version_and_sizes(lib):
     assert lib.pi05w4a4_mfma_words(0, 64) == 0
 
 
+def test_host_q_words_matches_library(lib):
+    from pi05_fast.w4a4 import extension as ext
+
+    for m in (0, 1, 15, 16, 17, 776, 1552, 6208):
+        for k in (0, 64, 128, 192, 2048, 16384):
+            assert ext._q_words(m, k) == lib.pi05w4a4_q_words(m, k), (m, k)
+
+
+def test_direct_route_only_for_plain_untraced_calls():
+    """The eager bypass of torch.ops is taken only when the dispatcher has nothing to do."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from torch.overrides import TorchFunctionMode
+
+    from pi05_fast.w4a4 import extension as ext
+
+    x = torch.zeros(4, 64, dtype=torch.float16)
+    w = torch.nn.Parameter(torch.zeros(16, 9, dtype=torch.int32), requires_grad=False)
+    assert ext._direct(x, w, None)
+    xg = torch.zeros(4, 64, requires_grad=True)
+    assert not ext._direct(xg, w)
+    with torch.no_grad():
+        assert ext._direct(xg, w)
+    with torch.inference_mode():
+        assert ext._direct(torch.zeros(4, 64), w)
+    with FakeTensorMode() as mode:
+        assert not ext._direct(torch.empty(4, 64))
+    assert not ext._direct(mode.from_tensor(x))
+
+    class _Mode(TorchFunctionMode):
+        def __torch_function__(self, func, types, args=(), kwargs=None):
+            return func(*args, **(kwargs or {}))
+
+    with _Mode():
+        assert not ext._direct(x)
+
+
 def test_workspace_sizing(lib):
     n1 = (ctypes.c_int32 * 1)(2048)
     ws_down = lib.pi05w4a4_gemm_workspace_bytes(776, 16384, 1, n1, 0)
