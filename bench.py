@@ -24,6 +24,11 @@ The dominant kernel of the forward (the gate/up GEMM with its fused GELU-tanh*up
 epilogue, ~32% of the forward) is the `roofline` object; its `traffic` (HBM bytes per
 launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under profiles/.
 
+`in_forward` times the same kernels inside the real (eager) forward: HIP events around
+each library call, with a bounded spin kernel queued ahead so that the host has enqueued
+the whole forward before the GPU runs it (no host gaps between kernels);
+`roofline.in_forward` is the dominant kernel's figure from it.
+
 `cpu_baseline` times the reference's W4A4 semantics in PyTorch on the host CPU (the
 oracle's torch restatement of pack.py:113-145, both integer matmul forms) on one decoder
 layer's projection calls at the same M and scales it to the full depth.
@@ -53,10 +58,10 @@ METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
-TRAFFIC_FILES = {
-    "gate_up": ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md",
-    "gate_up_gelu": ROOT / "profiles" / "gate_up_gelu_gemm_776x2048x32768_traffic.md",
-}
+# HBM-side traffic per launch of the W4A4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE summary);
+# the plain gate/up GEMM (--unfused-gelu) has its own.
+TRAFFIC_FILE = ROOT / "profiles" / "w4a4_kernels_776tok_traffic.md"
+TRAFFIC_FILE_GATE_UP = ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md"
 
 
 def parse_args():
@@ -288,6 +293,99 @@ def forward_point(torch, model, prefix_inputs, dev, tokens: int, batch: int, ste
             "tokens_per_s": round(tokens * batch / ms * 1e3, 1)}
 
 
+def _in_forward_label(fn_name: str, args: tuple, kwargs: dict) -> str:
+    """Kernel class of one library call made by the forward."""
+    if fn_name == "_gemm_from_q":
+        k, weights = args[2], args[3]
+        if kwargs.get("gelu"):
+            return "gate_up_gelu"
+        if kwargs.get("residual") is not None:
+            return "down_residual" if k == 16384 else "o_residual"
+        return {3: "qkv", 2: "gate_up"}.get(len(weights), "gemm")
+    if fn_name == "quantize":
+        return f"quant_k{int(args[0].size(-1))}"
+    if fn_name == "rms_norm_quantize":
+        return "rmsnorm_quant_k2048"
+    return "attention_with_kv_prep"
+
+
+def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
+    """Per-kernel GPU time inside the real forward: the eager forward runs with HIP events
+    recorded on the launching stream around each library call (GEMM launches, activation
+    quants, the two attention kernels).  A bounded spin kernel (torch.cuda._sleep) queued
+    ahead of each forward holds the GPU until the host has enqueued the whole forward, so
+    the kernels run back to back with no host gaps, in the cache state the forward leaves
+    them (preceding kernels, weight cache warming) and the event pairs time the kernels
+    alone.  `avg_us` is the mean pair interval less that of an empty pair (`event_pair_us`,
+    the markers' own cost); `raw_avg_us` keeps it."""
+    names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl")
+    orig = {n: getattr(ext, n) for n in names}
+    records = []
+
+    def wrap(name):
+        fn = orig[name]
+
+        def timed(*args, **kwargs):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            out = fn(*args, **kwargs)
+            e1.record()
+            records.append((_in_forward_label(name, args, kwargs), e0, e1))
+            return out
+
+        return timed
+
+    # spin length: calibrate cycles -> ms, aim at twice the host enqueue time
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    torch.cuda._sleep(1_000_000)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_per_mcycle = max(e0.elapsed_time(e1), 1e-3)
+    for n in names:
+        setattr(ext, n, wrap(n))
+    primed = True
+    try:
+        t0 = time.perf_counter()
+        model(x, mask)
+        torch.cuda.synchronize()
+        enqueue_ms = (time.perf_counter() - t0) * 1e3
+        spin_ms = min(4.0 * enqueue_ms + 5.0, 200.0)
+        records.clear()
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(spin_ms / ms_per_mcycle * 1e6))
+            t0 = time.perf_counter()
+            model(x, mask)
+            host_ms = (time.perf_counter() - t0) * 1e3
+            torch.cuda.synchronize()
+            primed = primed and host_ms < spin_ms
+    finally:
+        for n in names:
+            setattr(ext, n, orig[n])
+    # An event pair costs time of its own (two marker packets on the queue): the interval
+    # of a pair with nothing between it, measured the same way, is taken off each call.
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(10.0 / ms_per_mcycle * 1e6))
+    empty = []
+    for _ in range(200):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        b.record()
+        empty.append((a, b))
+    torch.cuda.synchronize()
+    pair_us = statistics.median(a.elapsed_time(b) * 1e3 for a, b in empty)
+    per = {}
+    for label, a, b in records:
+        per.setdefault(label, []).append(a.elapsed_time(b) * 1e3)
+    out = {lab: {"calls_per_forward": len(v) // reps, "avg_us": round(statistics.fmean(v) - pair_us, 3),
+                 "raw_avg_us": round(statistics.fmean(v), 3)} for lab, v in per.items()}
+    return {"kernels": out, "reps": reps, "queue_primed": primed, "spin_ms": round(spin_ms, 2),
+            "event_pair_us": round(pair_us, 3)}
+
+
 def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
     h, inter = 2048, 16384
     jobs = {
@@ -302,15 +400,16 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
         "rmsnorm_quant_k2048": lambda: kb.rmsnorm_quant(m),
     }
-    if only == "copy":  # calibration for the HBM traffic counters: a plain 64 MiB copy
+
+    def copy():  # calibration for the HBM traffic counters: a plain 64 MiB copy
         src = kb.torch.empty(64 << 20, dtype=kb.torch.uint8, device=kb.dev).fill_(1)
         dst = kb.torch.empty_like(src)
         us = kb._time(lambda: dst.copy_(src))
-        return {"copy": {"bytes_read": float(64 << 20), "bytes_written": float(64 << 20), "avg_us": round(us, 3)}}
-    if only == "qkv_m_sweep":
-        return {only: qkv_m_sweep(kb)}
-    if only:
-        return {only: jobs[only]()}
+        return {"bytes_read": float(64 << 20), "bytes_written": float(64 << 20), "avg_us": round(us, 3)}
+
+    if only:  # one class or a comma-separated list (also "copy", "qkv_m_sweep")
+        extra = {"copy": copy, "qkv_m_sweep": lambda: qkv_m_sweep(kb)}
+        return {name: {**jobs, **extra}[name]() for name in only.split(",")}
     return {name: fn() for name, fn in jobs.items()}
 
 
@@ -340,11 +439,14 @@ def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
 
 
 def read_traffic(kernel: str) -> tuple[float | None, str | None]:
-    """HBM bytes per launch of a gate/up kernel from the committed rocprofv3 summary."""
-    path = TRAFFIC_FILES[kernel]
+    """HBM bytes per launch of a kernel class from the committed rocprofv3 summary."""
+    path = TRAFFIC_FILE_GATE_UP if kernel == "gate_up" else TRAFFIC_FILE
     if not path.is_file():
         return None, None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", path.read_text())
+    text = path.read_text()
+    m = re.search(rf"traffic_bytes_per_launch\[{kernel}\]:\s*([0-9.eE+]+)", text)
+    if m is None and kernel == "gate_up":
+        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
     if not m:
         return None, None
     return float(m.group(1)), str(path.relative_to(ROOT))
@@ -518,6 +620,7 @@ def main() -> int:
             model(x, mask)
         torch.cuda.synchronize()
         eager_ms = (time.perf_counter() - t0) * 1e3 / n_eager
+        in_fwd = None if args.forward_only else in_forward_times(torch, ext, model, x, mask)
 
         def step():
             if graph is not None:
@@ -581,6 +684,13 @@ def main() -> int:
     dk_name = "gate_up" if args.unfused_gelu else "gate_up_gelu"
     dk = kernels[dk_name]
     traffic, traffic_src = read_traffic(dk_name)
+    fwd_dk = in_fwd["kernels"].get(dk_name)
+    in_forward_roof = None
+    if fwd_dk is not None:
+        tops_fwd = dk["ops"] / (fwd_dk["avg_us"] * 1e-6) / 1e12
+        in_forward_roof = {"avg_launch_us": fwd_dk["avg_us"], "achieved": round(tops_fwd, 1),
+                           "frac": round(tops_fwd / INT8_PEAK_TOPS, 4),
+                           "calls_per_forward": fwd_dk["calls_per_forward"]}
     roofline = {
         "bound": "mfma",
         "achieved": dk["tops"],
@@ -595,6 +705,8 @@ def main() -> int:
         "ops_unit": "int8 MAC x 2 per second (dense int8 MFMA)",
         "traffic_source": traffic_src,
         "algorithmic_bytes_per_launch": dk["bytes"],
+        # the same kernel timed inside the eager forward (in_forward below)
+        "in_forward": in_forward_roof,
     }
     out = {
         "metric": METRIC,
@@ -634,6 +746,7 @@ def main() -> int:
         "other_kernels": others,
         "forward_points": points,
         "roofline": roofline,
+        "in_forward": in_fwd,
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(args.tokens, args.batch, args.layers, args.cpu_seconds)

@@ -147,8 +147,11 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // ---- tile of this workgroup (XCD-aware order, see the header)
   int tile = blockIdx.x;
   {
+    // XCD x = b % 8 owns the contiguous tiles [x*q + min(x, r), ..) with q = total / 8,
+    // r = total % 8 (one more tile for the first r XCDs): a bijection for any total.
     const int total = p.ntiles * p.mtiles;
-    if ((total & 7) == 0) tile = (tile & 7) * (total >> 3) + (tile >> 3);
+    const int x = tile & 7, q = total >> 3, r = total & 7;
+    tile = x * q + min(x, r) + (tile >> 3);
   }
   const int mt = tile % p.mtiles;
   const int nt = tile / p.mtiles;
