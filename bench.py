@@ -215,6 +215,31 @@ class KernelBench:
                 "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb}
 
 
+    def qkv_rope(self, b, s, h=2048):
+        """The QKV GEMMs with RoPE and the attention's K/V layout in the epilogue
+        (pi05w4a4_gemm_qkv_rope, one KV head of 256) at B x S tokens."""
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        m = b * s
+        gen = torch.Generator(device=self.dev).manual_seed(20261202 + m)
+        x = torch.randn(m, h, device=self.dev, dtype=torch.float16, generator=gen)
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, h)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        self._check(lib.pi05w4a4_quantize(P(x), m, h, P(q), P(sa), self._stream()))
+        wq, wk, wv = (self._packed(n, h, gen) for n in (2048, 256, 256))
+        wk = self.ext.rope_pair_weight(wk)
+        cos = torch.rand(m, 256, device=self.dev, generator=gen).half()
+        sin = torch.rand(m, 256, device=self.dev, generator=gen).half()
+        yq = torch.empty(m, 2048, dtype=torch.float16, device=self.dev)
+        kr = torch.empty(m, 256, dtype=torch.float16, device=self.dev)
+        yv = torch.empty(m, 256, dtype=torch.float16, device=self.dev)
+        kv = torch.empty(int(lib.pi05w4a4_attn_kv_mfma_elems(b, s, 1, 256)), dtype=torch.float16, device=self.dev)
+        us = self._time(lambda: self._check(lib.pi05w4a4_gemm_qkv_rope(
+            P(q), P(sa), m, h, P(wq), 2048, P(wk), P(wv), P(cos), P(sin), b, s, P(yq), P(kr), P(yv), P(kv),
+            self._stream())))
+        ops = 2.0 * m * 2560 * h
+        return {"m": m, "k": h, "n": 2560, "avg_us": round(us, 3), "ops": ops,
+                "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+
     def attention(self, b, s, h=8, kvh=1):
         """The two prefix-attention kernels (K RoPE + V transpose, then attention) at one
         decoder layer's shapes, zero additive mask."""
@@ -306,7 +331,9 @@ def _in_forward_label(fn_name: str, args: tuple, kwargs: dict) -> str:
         return f"quant_k{int(args[0].size(-1))}"
     if fn_name == "rms_norm_quantize":
         return "rmsnorm_quant_k2048"
-    return "attention_with_kv_prep"
+    if fn_name == "_gemm_qkv_rope":
+        return "qkv_rope"
+    return "attention" if kwargs.get("kv_mfma") is not None else "attention_with_kv_prep"
 
 
 def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
@@ -318,7 +345,7 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
     them (preceding kernels, weight cache warming) and the event pairs time the kernels
     alone.  `avg_us` is the mean pair interval less that of an empty pair (`event_pair_us`,
     the markers' own cost); `raw_avg_us` keeps it."""
-    names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl")
+    names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl", "_gemm_qkv_rope")
     orig = {n: getattr(ext, n) for n in names}
     records = []
 
@@ -399,6 +426,7 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "o_residual": lambda: kb.gemm(m, h, [2048], residual=True),
         "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
         "rmsnorm_quant_k2048": lambda: kb.rmsnorm_quant(m),
+        "qkv_rope": lambda: kb.qkv_rope(1, m),
     }
 
     def copy():  # calibration for the HBM traffic counters: a plain 64 MiB copy
@@ -671,11 +699,13 @@ def main() -> int:
     # The W4A4 kernels one decoder layer launches (fused layer: RMSNorm in the QKV and
     # gate/up quants, the o-proj quant inside the attention kernel, residual adds in the o
     # and down epilogues).
-    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 0, "quant_k16384": 1, "qkv": 1, "o_residual": 1,
-             "down_residual": 1, "gate_up_gelu": 1, "gate_up": 0, "o": 0, "down": 0}
+    fused_kv = os.environ.get("PI05_W4A4_FUSE_KV", "1") != "0" and args.tokens % 8 == 0
+    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 0, "quant_k16384": 1, "qkv": 0 if fused_kv else 1,
+             "qkv_rope": 1 if fused_kv else 0, "o_residual": 1, "down_residual": 1, "gate_up_gelu": 1, "gate_up": 0,
+             "o": 0, "down": 0}
     if args.unfused_gelu:
-        calls.update({"rmsnorm_quant_k2048": 0, "quant_k2048": 3, "o_residual": 0, "down_residual": 0,
-                      "gate_up_gelu": 0, "gate_up": 1, "o": 1, "down": 1})
+        calls.update({"rmsnorm_quant_k2048": 0, "quant_k2048": 3, "qkv": 1, "qkv_rope": 0, "o_residual": 0,
+                      "down_residual": 0, "gate_up_gelu": 0, "gate_up": 1, "o": 1, "down": 1})
     for name, c in calls.items():
         kernels[name]["calls_per_layer"] = c
     w4a4_us_per_layer = sum(kernels[n]["avg_us"] * c for n, c in calls.items())

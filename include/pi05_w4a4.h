@@ -283,6 +283,34 @@ int pi05w4a4_prefix_attention(const void* q, int64_t ld_q, const void* kv_mfma,
                               int64_t ld_out, int32_t* q_codes, float* q_scales, void* stream);
 
 /*
+ * QKV GEMMs with the attention prep in the epilogue (one KV head of 256): pi05w4a4_gemm_multi
+ * of the three weights, where the K output goes through RoPE and both K and V are also
+ * written in the fragment-major layout pi05w4a4_attn_kv_prep produces, so that
+ * pi05w4a4_prefix_attention follows with no kv_prep launch.  No counterpart in the
+ * reference (its attention runs transformers' RoPE and eager attention after the
+ * int4_gemm3 of apply.py:145-191); the fused decoder layer of this package uses it.
+ *   w_k_rope: the K weight (MFMA layout, N = 256) with its 16-row blocks in RoPE-pair order
+ *     (block 2P + j holds output channels 16P + 128j .. + 15, P < 8; pi05w4a4_permute_rope_pairs);
+ *   cos_fp16 / sin_fp16: fp16 [B * S, 256] rotary tables of the rows;
+ *   y_q fp16 [M, n_q]; k_rope fp16 [M, 256] (the key states with RoPE, dimension order);
+ *   y_v fp16 [M, 256]; kv_mfma: pi05w4a4_attn_kv_mfma_elems(B, S, 1, 256) elements, pad keys
+ *   zeroed.  M = B * S with S a multiple of 8 and at most 1024.  The whole K runs in one
+ *   launch (no global K split, so no workspace), also where pi05w4a4_gemm_multi would split.
+ */
+int pi05w4a4_gemm_qkv_rope(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                           const int32_t* w_q_mfma, int32_t n_q, const int32_t* w_k_rope,
+                           const int32_t* w_v_mfma, const void* cos_fp16, const void* sin_fp16,
+                           int64_t b, int32_t s, void* y_q, void* k_rope, void* y_v, void* kv_mfma,
+                           void* stream);
+
+/*
+ * The K weight of pi05w4a4_gemm_qkv_rope from an MFMA-layout K weight (N = 256, any K):
+ * 16-row block 2P + j of dst is block P + 8j of src, with its scales and corrections.
+ * dst holds pi05w4a4_mfma_words(256, K) words (a [256, K/8 + 16] tensor); not in place.
+ */
+int pi05w4a4_permute_rope_pairs(const int32_t* src_mfma, int32_t k, int32_t* dst_mfma, void* stream);
+
+/*
  * pi05w4a4_prefix_attention plus cache warming: the CUs that the attention leaves idle
  * (B * KVH * ceil(S * H / KVH / 32) < 256 workgroups) read warm_n <= 4 further device
  * buffers (16-byte aligned, sizes multiples of 16 bytes) and discard the data, so that the

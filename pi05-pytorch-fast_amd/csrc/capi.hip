@@ -188,12 +188,21 @@ int validate_weight(const int32_t* w, int32_t n, const char* name) {
   return PI05W4A4_OK;
 }
 
+// Attention prep of pi05w4a4_gemm_qkv_rope (groups 1 and 2 are K and V).
+struct QkvRope {
+  const void* cos;
+  const void* sin;
+  void* kv;
+  int32_t seq;
+};
+
 int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroups,
              const int32_t* const* w, const int32_t* n, void* const* y, int mode,
              void* workspace, size_t workspace_bytes, hipStream_t stream,
-             const void* residual = nullptr) {
+             const void* residual = nullptr, const QkvRope* rope = nullptr) {
   const bool gelu = mode == w4a4::kEpiGeluUp;
-  const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc);
+  // The attention prep epilogue needs the whole K in one launch: no global split for it.
+  const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc && rope == nullptr);
   if (pl.mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
   w4a4::GemmParams p{};
   p.q = q;
@@ -219,6 +228,15 @@ int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroup
   p.n_total = static_cast<int32_t>(n_total);
   p.gelu_pair_n = gelu ? n[0] : 0;
   p.res = static_cast<const _Float16*>(residual);
+  if (rope != nullptr) {
+    p.rope_group = 2;
+    p.vt_group = 3;
+    p.cosb = static_cast<const _Float16*>(rope->cos);
+    p.sinb = static_cast<const _Float16*>(rope->sin);
+    p.kv = static_cast<_Float16*>(rope->kv);
+    p.seq = rope->seq;
+    p.s_pad = static_cast<int32_t>(w4a4::attn_s_pad(rope->seq));
+  }
   if (pl.ksplit > 1) {
     const size_t need = static_cast<size_t>(pl.ksplit) * static_cast<size_t>(m) *
                         static_cast<size_t>(n_total) * sizeof(int32_t);
@@ -395,6 +413,58 @@ int pi05w4a4_gemm_residual(const int32_t* q, const float* sa, int64_t m, int32_t
   void* ys[1] = {y_fp16};
   return run_gemm(q, sa, m, k, 1, ws, ns, ys, w4a4::kEpiFp16, workspace, workspace_bytes,
                   static_cast<hipStream_t>(stream), residual_fp16);
+}
+
+int pi05w4a4_gemm_qkv_rope(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                           const int32_t* w_q_mfma, int32_t n_q, const int32_t* w_k_rope,
+                           const int32_t* w_v_mfma, const void* cos_fp16, const void* sin_fp16,
+                           int64_t b, int32_t s, void* y_q, void* k_rope, void* y_v, void* kv_mfma,
+                           void* stream) {
+  int rc = validate_gemm_common(q, sa, m, k);
+  if (rc) return rc;
+  if (b < 1 || s < 1 || s % 8 != 0 || s > w4a4::kAttnMaxKeys || m != b * s)
+    return fail(PI05W4A4_EINVAL, "gemm_qkv_rope: M = B * S with S a multiple of 8 in [8, %d], got M=%lld B=%lld S=%d",
+                w4a4::kAttnMaxKeys, (long long)m, (long long)b, s);
+  rc = validate_weight(w_q_mfma, n_q, "q weight");
+  if (rc) return rc;
+  rc = validate_weight(w_k_rope, w4a4::kAttnHeadDim, "k weight");
+  if (rc) return rc;
+  rc = validate_weight(w_v_mfma, w4a4::kAttnHeadDim, "v weight");
+  if (rc) return rc;
+  const void* ptrs[] = {y_q, k_rope, y_v, kv_mfma, cos_fp16, sin_fp16};
+  for (const void* ptr : ptrs) {
+    if (ptr == nullptr) return fail(PI05W4A4_EINVAL, "gemm_qkv_rope: null output or rotary table");
+    if (!aligned(ptr, 16)) return fail(PI05W4A4_EINVAL, "gemm_qkv_rope: outputs and rotary tables must be 16-byte aligned");
+  }
+  const int32_t* ws[3] = {w_q_mfma, w_k_rope, w_v_mfma};
+  const int32_t ns[3] = {n_q, w4a4::kAttnHeadDim, w4a4::kAttnHeadDim};
+  void* ys[3] = {y_q, k_rope, y_v};
+  const QkvRope rope{cos_fp16, sin_fp16, kv_mfma, s};
+  return run_gemm(q, sa, m, k, 3, ws, ns, ys, w4a4::kEpiFp16, nullptr, 0, static_cast<hipStream_t>(stream),
+                  nullptr, &rope);
+}
+
+int pi05w4a4_permute_rope_pairs(const int32_t* src_mfma, int32_t k, int32_t* dst_mfma, void* stream) {
+  if (src_mfma == nullptr || dst_mfma == nullptr) return fail(PI05W4A4_EINVAL, "null weight");
+  if (k <= 0 || k % 64 != 0 || k > kMaxK) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
+  if (src_mfma == dst_mfma) return fail(PI05W4A4_EINVAL, "permute_rope_pairs is not in place");
+  const int64_t block = static_cast<int64_t>(w4a4::kblocks128(k)) * 256;  // words per 16-row block
+  const int64_t payload = 16 * block;                                     // 256 rows
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int nb = 0; nb < 16; ++nb) {
+    const int src_nb = (nb >> 1) + 8 * (nb & 1);
+    hipError_t e = hipMemcpyAsync(dst_mfma + nb * block, src_mfma + src_nb * block, block * 4,
+                                  hipMemcpyDeviceToDevice, st);
+    // scales (256 floats after the payload), then the column corrections
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(dst_mfma + payload + nb * 16, src_mfma + payload + src_nb * 16, 64,
+                         hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess)
+      e = hipMemcpyAsync(dst_mfma + payload + 256 + nb * 16, src_mfma + payload + 256 + src_nb * 16, 64,
+                         hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return hip_status(e, "permute_rope_pairs copy");
+  }
+  return ok();
 }
 
 int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,

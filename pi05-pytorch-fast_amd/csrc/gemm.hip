@@ -130,6 +130,29 @@ __device__ __forceinline__ _Float16 dequant(int32_t acc, float sa, float sw) {
   return static_cast<_Float16>(y);
 }
 
+// RoPE of four dimension pairs (d, d + 128), each product and sum rounded to fp16 as
+// torch's (x * cos) + (rotate_half(x) * sin) on fp16 tensors (attention.hip's rope_pair).
+__device__ __forceinline__ void rope4(half4& lo, half4& hi, half4 clo, half4 chi, half4 slo, half4 shi) {
+#pragma clang fp contract(off)
+  const half4 a = lo * clo;
+  const half4 b = hi * slo;
+  const half4 c = hi * chi;
+  const half4 e = lo * shi;
+  lo = a - b;
+  hi = c + e;
+}
+
+// Slot (16-byte, 8 halves) of key token t, dimensions dd .. dd + 7 (dd % 8 == 0) in the
+// fragment-major K of one batch (kv_prep_kernel's layout).
+__device__ __forceinline__ int kfrag_slot(int t, int dd) {
+  return ((t >> 4) * 8 + (dd >> 5)) * 64 + (t & 15) + 16 * ((dd & 31) >> 3);
+}
+// Slot of dimension d, keys t0 .. t0 + 7 (t0 % 8 == 0) in the fragment-major V^T of one
+// batch with nst 32-key steps.
+__device__ __forceinline__ int64_t vfrag_slot(int d, int t0, int nst) {
+  return (static_cast<int64_t>((d >> 4) * nst + (t0 >> 5))) * 64 + 16 * ((t0 & 31) >> 3) + (d & 15);
+}
+
 template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
@@ -178,6 +201,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   int N = p.g[0].n;
   int tile_begin = 0;
   int col_off = 0;
+  int gsel = 0;
   const int32_t* W2 = p.g[1].w;  // GELU: the up weight
   {
     int acc_off = p.g[0].n;
@@ -189,6 +213,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         N = p.g[i].n;
         tile_begin = p.g[i].tile_begin;
         col_off = acc_off;
+        gsel = i;
       }
       if (i < p.ngroups) acc_off += p.g[i].n;
     }
@@ -314,6 +339,31 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = first_part ? (wc[ni] + qc[mi]) : v4i{0, 0, 0, 0};
+  }
+
+  // QKV attention prep, small tiles (2 x 2 fragments per wave): the K group's rotary
+  // values are fetched now so that their latency hides under the main loop.  The loads
+  // are unconditional (other waves read a fixed in-bounds word of the codes) to keep the
+  // vmcnt bookkeeping exact.
+  constexpr bool kRopePre = !GELU && MI * (NI / 2) <= 2;
+  half4 rpre[kRopePre ? MI : 1][kRopePre ? NI / 2 : 1][4];
+  if constexpr (kRopePre) {
+    const bool rope_wave = p.rope_group == gsel + 1;
+    const _Float16* dummy = reinterpret_cast<const _Float16*>(p.q);
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int j = 0; j < NI / 2; ++j) {
+        const int64_t rl = min(m0 + mi * 16 + (lane & 15), M - 1);
+        const int64_t off = rl * kAttnHeadDim + ((wcol >> 5) + j) * 16 + (lane >> 4) * 4;
+        const _Float16* c = rope_wave ? p.cosb + off : dummy;
+        const _Float16* sn = rope_wave ? p.sinb + off : dummy;
+        const int hi = rope_wave ? 128 : 0;
+        rpre[mi][j][0] = *reinterpret_cast<const half4*>(c);
+        rpre[mi][j][1] = *reinterpret_cast<const half4*>(c + hi);
+        rpre[mi][j][2] = *reinterpret_cast<const half4*>(sn);
+        rpre[mi][j][3] = *reinterpret_cast<const half4*>(sn + hi);
+      }
   }
 
   // Epilogue scales of the whole workgroup tile, fetched now so that their latency hides
@@ -463,8 +513,12 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
     // Residual (one-group fp16 mode): y = fp16(y + res), the rounding of torch's fp16 add.
     static_assert(GELU || (LPR == RLPR && RPI == RRPI), "residual pieces follow the store layout");
+    // Attention prep (QKV): this wave's group is K in RoPE-pair order, or V.
+    const bool rope = !GELU && p.rope_group == gsel + 1;
+    const bool vtr = !GELU && p.vt_group == gsel + 1;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
+      half4 ob[GELU ? 1 : NI];
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
         const v4i s = acc[mi][ni];
@@ -495,7 +549,41 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = dequant(s[r], sv[mi], swv[r]);
         }
-        *reinterpret_cast<half4*>(stage + lrow * LSR + ni * 16 + lcol) = o;
+        if constexpr (GELU)
+          *reinterpret_cast<half4*>(stage + lrow * LSR + ni * 16 + lcol) = o;
+        else
+          ob[ni] = o;
+      }
+      if constexpr (!GELU) {
+        if (rope) {
+          // Fragment pair (2j, 2j + 1) holds key dimensions d .. d + 3 and d + 128 .. d + 131
+          // of the lane's row: RoPE, then the fragment-major K copy; the staged key states
+          // are stored in dimension order below.
+          const int64_t r = m0 + mi * 16 + lrow;
+          const int64_t rl = min(r, M - 1);
+          const int rb = static_cast<int>(rl / p.seq);
+          const int t = static_cast<int>(rl) - rb * p.seq;
+          _Float16* kf = p.kv + static_cast<int64_t>(rb) * 2 * p.s_pad * kAttnHeadDim;
+#pragma unroll
+          for (int j = 0; j < NI / 2; ++j) {
+            const int d = ((wcol >> 5) + j) * 16 + lcol;
+            if constexpr (kRopePre) {
+              rope4(ob[2 * j], ob[2 * j + 1], rpre[mi][j][0], rpre[mi][j][1], rpre[mi][j][2], rpre[mi][j][3]);
+            } else {
+              const _Float16* cr = p.cosb + rl * kAttnHeadDim + d;
+              const _Float16* sr = p.sinb + rl * kAttnHeadDim + d;
+              rope4(ob[2 * j], ob[2 * j + 1], *reinterpret_cast<const half4*>(cr),
+                    *reinterpret_cast<const half4*>(cr + 128), *reinterpret_cast<const half4*>(sr),
+                    *reinterpret_cast<const half4*>(sr + 128));
+            }
+            if (r < M) {
+              *reinterpret_cast<half4*>(kf + kfrag_slot(t, d & ~7) * 8 + (d & 7)) = ob[2 * j];
+              *reinterpret_cast<half4*>(kf + kfrag_slot(t, (d + 128) & ~7) * 8 + (d & 7)) = ob[2 * j + 1];
+            }
+          }
+        }
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) *reinterpret_cast<half4*>(stage + lrow * LSR + ni * 16 + lcol) = ob[ni];
       }
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -508,18 +596,77 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         // displace the weights streaming through L2 (measured 1-3% faster).
         if (rr < 16 && m0 + trow < M && wcol + tcol < N) {
           const uint32_t off = static_cast<uint32_t>(trow * N + tcol) * 2u;
+          char* dst = yw + off;
           if constexpr (!GELU) {
             if (has_res) {
               half8 o8 = __builtin_bit_cast(half8, v);
               o8 += __builtin_bit_cast(half8, resv[mi][j]);
               v = __builtin_bit_cast(uint4, o8);
             }
+            if (rope) {
+              // GEMM column gc = 32P + 16h + c is key dimension 16P + 128h + c
+              const int gc = wcol + tcol;
+              const int kd = ((gc >> 5) + 8 * ((gc >> 4) & 1)) * 16 + (gc & 15);
+              dst = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + (m0 + trow) * N + kd);
+            }
           }
           __builtin_nontemporal_store(v4i{static_cast<int>(v.x), static_cast<int>(v.y), static_cast<int>(v.z), static_cast<int>(v.w)},
-                                      reinterpret_cast<v4i*>(yw + off));
+                                      reinterpret_cast<v4i*>(dst));
+        }
+      }
+      if constexpr (!GELU) {
+        if (vtr) {
+          // V^T fragments: lane pairs (dimension, 8-key group) of the staged 16 rows.  A row
+          // group never straddles two batches (seq and the tile rows are multiples of 8).
+          const int nst = p.s_pad / 32;
+#pragma unroll
+          for (int it = 0; it < NI / 2; ++it) {
+            const int idx = lane + 64 * it;
+            const int dim = idx % OCW;
+            const int kg = idx / OCW;
+            const int64_t row0 = m0 + mi * 16 + kg * 8;
+            half8 x;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = stage[(kg * 8 + e) * LSR + dim];
+            if (row0 < M && wcol + dim < N) {
+              const int rb = static_cast<int>(row0 / p.seq);
+              const int t0 = static_cast<int>(row0) - rb * p.seq;
+              _Float16* vf = p.kv + (static_cast<int64_t>(rb) * 2 + 1) * p.s_pad * kAttnHeadDim;
+              *reinterpret_cast<half8*>(vf + vfrag_slot(wcol + dim, t0, nst) * 8) = x;
+            }
+          }
         }
       }
       __builtin_amdgcn_wave_barrier();
+    }
+    if constexpr (!GELU) {
+      if (rope || vtr) {
+        // Keys seq .. s_pad - 1 of every batch whose last token lies in this tile: zeros.
+        const int npad = p.s_pad - p.seq;
+        const int64_t mend = min(m0 + 16 * MI, M);
+        for (int64_t b = m0 / p.seq; b * p.seq < mend; ++b) {
+          const int64_t last = b * p.seq + p.seq - 1;
+          if (last < m0 || last >= mend) continue;
+          _Float16* kf = p.kv + b * 2 * p.s_pad * kAttnHeadDim;
+          if (rope) {
+            constexpr int NG = NI * 2;  // 8-dimension groups of the wave's key dimensions
+            for (int idx = lane; idx < npad * NG; idx += 64) {
+              const int t = p.seq + idx / NG;
+              const int g = idx % NG;
+              const int dd = ((wcol >> 5) + (g >> 2) + 8 * ((g >> 1) & 1)) * 16 + 8 * (g & 1);
+              *reinterpret_cast<half8*>(kf + kfrag_slot(t, dd) * 8) = half8{};
+            }
+          } else {
+            _Float16* vf = kf + static_cast<int64_t>(p.s_pad) * kAttnHeadDim;
+            const int nst = p.s_pad / 32;
+            for (int idx = lane; idx < (npad / 8) * OCW; idx += 64) {
+              const int d = wcol + idx % OCW;
+              const int t0 = p.seq + 8 * (idx / OCW);
+              if (d < N) *reinterpret_cast<half8*>(vf + vfrag_slot(d, t0, nst) * 8) = half8{};
+            }
+          }
+        }
+      }
     }
   } else {
     // kEpiPartial: partial sums of 16 * acc, int32 [ksplit, M, n_total] at column

@@ -42,6 +42,19 @@ struct GemmParams {
   int32_t n_total;
   int32_t gelu_pair_n;  // for kEpiGeluUp: columns of the gate (= up) weight
   const _Float16* res;  // kEpiFp16, one group: fp16 [M, N] added to the output (or null)
+  // Attention prep in the QKV epilogue (kEpiFp16, one KV head of 256): group rope_group - 1
+  // is K with its output channels in RoPE-pair order (16-column block 2P + j holds the key
+  // dimensions 16P + 128j .. + 15), finished with RoPE into its y (the key states, [M, 256]
+  // in dimension order) and into the fragment-major K of kv; group vt_group - 1 is V,
+  // written plain and as the fragment-major V^T of kv (the layout of kv_prep_kernel,
+  // attention.hip).  0: no such group.  Rows are tokens: row r = b * seq + t.
+  int32_t rope_group;
+  int32_t vt_group;
+  const _Float16* cosb;  // [M, 256] rotary tables of the rows
+  const _Float16* sinb;
+  _Float16* kv;          // per batch: K then V^T fragments, keys padded to s_pad (zeroed here)
+  int32_t seq;           // tokens per batch, a multiple of 8
+  int32_t s_pad;         // attn_s_pad(seq)
 };
 
 // MFMA-fragment-major layout of packed INT4 codes, shared by the weights (r = output

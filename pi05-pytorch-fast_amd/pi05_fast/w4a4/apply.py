@@ -366,8 +366,6 @@ def _fused_decoder_layer_forward(
                                         past_key_values=past_key_values, use_cache=use_cache,
                                         position_embeddings=position_embeddings, **kwargs)
     (w1, eps1, off1), (w2, eps2, off2) = norms
-    q, k, v = ext.rms_norm_int4_gemm3(x, w1, eps1, attn.q_proj.packed, attn.k_proj.packed, attn.v_proj.packed,
-                                      unit_offset=off1)
     cos, sin = position_embeddings
     hd = attn.head_dim
     # Cache warming (PI05_W4A4_CACHE_WARM=0: off): the attention launch's idle CUs read the
@@ -376,14 +374,55 @@ def _fused_decoder_layer_forward(
     # as well: no gain, and the longer warming outlasts the attention.
     warming = os.environ.get("PI05_W4A4_CACHE_WARM", "1") != "0"
     warm = [attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed] if warming else None
-    x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
-                                                    q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
-                                                    warm=warm, return_out=False)
+    wk_rope = _k_rope_weight(attn, x)
+    if wk_rope is not None:
+        # One KV head: RoPE and the attention's K/V layout in the QKV GEMM epilogue.
+        q, key_states, v, kv = ext.rms_norm_int4_gemm3_rope(x, w1, eps1, attn.q_proj.packed, wk_rope,
+                                                            attn.v_proj.packed, cos, sin, unit_offset=off1)
+        x2, _ = ext.prefix_attention_o_proj_kv(q, v, kv, cos, sin, attention_mask, float(attn.scaling),
+                                               q.size(-1) // hd, attn.o_proj.packed, x, warm=warm, return_out=False)
+    else:
+        q, k, v = ext.rms_norm_int4_gemm3(x, w1, eps1, attn.q_proj.packed, attn.k_proj.packed, attn.v_proj.packed,
+                                          unit_offset=off1)
+        x2, key_states, _ = ext.prefix_attention_o_proj(q, k, v, cos, sin, attention_mask, float(attn.scaling),
+                                                        q.size(-1) // hd, k.size(-1) // hd, attn.o_proj.packed, x,
+                                                        warm=warm, return_out=False)
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)
     h = ext.rms_norm_int4_gemm2_gelu(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, unit_offset=off2)
     return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2, warm=[mlp.down_proj.packed] if warming else None)
+
+
+def _k_rope_weight(attn: nn.Module, x: torch.Tensor):
+    """The RoPE-pair-ordered copy of the K weight (``extension.rope_pair_weight``) when the
+    QKV call can take the attention prep in its epilogue: one KV head of 256, MFMA-layout
+    q/k/v weights, a token count that is a multiple of 8; else None.  The copy is kept on
+    the module and rebuilt when the K weight tensor is replaced or modified in place (in
+    eager calls; a compiled graph uses the copy an eager call built, else the separate prep).
+    ``PI05_W4A4_FUSE_KV=0`` keeps the separate K/V prep launch."""
+    if os.environ.get("PI05_W4A4_FUSE_KV", "1") == "0" or int(x.size(1)) % 8:
+        return None
+    wk = attn.k_proj.packed
+    kin = int(x.size(-1))
+    if int(wk.size(0)) != 256 or attn.head_dim != 256 or int(attn.v_proj.packed.size(0)) != 256:
+        return None
+    if not all(w.dim() == 2 and w.size(1) == kin // 8 + MFMA_MARKER_WORDS
+               for w in (attn.q_proj.packed, wk, attn.v_proj.packed)):
+        return None
+    hit = getattr(attn, "_w4a4_k_rope", None)
+    if torch.compiler.is_compiling():
+        # a traced graph uses the copy an eager call built; it builds none itself
+        return hit[2] if hit is not None and hit[0] is wk else None
+    if hit is not None and hit[0] is wk and hit[1] == wk._version:
+        return hit[2]
+    if not wk.is_cuda:
+        return None
+    from pi05_fast.w4a4.extension import rope_pair_weight
+
+    out = rope_pair_weight(wk)
+    attn._w4a4_k_rope = (wk, wk._version, out)
+    return out
 
 
 def fuse_decoder_layers(model: nn.Module) -> int:

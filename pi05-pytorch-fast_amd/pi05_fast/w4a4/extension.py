@@ -93,6 +93,9 @@ def load_int4_gemm():
             [vp, i64, vp, vp, vp, vp, i64, i64, i32, ctypes.c_float, i64, i32, i32, i32, i32, vp, i64, vp, vp,
              ctypes.POINTER(vp), ctypes.POINTER(sz), i32, vp],
         ),
+        "pi05w4a4_gemm_qkv_rope": (
+            ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, vp, i64, i32, vp, vp, vp, vp, vp]),
+        "pi05w4a4_permute_rope_pairs": (ctypes.c_int, [vp, i32, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -519,12 +522,16 @@ def _prefix_attention_impl(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     mask: torch.Tensor | None, scaling: float, num_heads: int, num_kv_heads: int,
     quantize_out: bool = False, warm: list[torch.Tensor] | None = None, need_out: bool = True,
+    kv_mfma: torch.Tensor | None = None,
 ):
     """(out, key states) or, with ``quantize_out`` (one KV head, 8 query heads), (out, key
     states, q codes, scales) of the output rows' K = 2048 activation quant.  ``warm``: up to
     four contiguous device tensors that the attention launch's idle workgroups read into
     the Infinity Cache (``pi05w4a4_prefix_attention_warm``).  ``need_out=False`` (with
-    ``quantize_out``): the fp16 output is not written and an empty tensor is returned."""
+    ``quantize_out``): the fp16 output is not written and an empty tensor is returned.
+    ``kv_mfma``: K with RoPE and V^T already in the fragment-major layout (from
+    ``rms_norm_int4_gemm3_rope``); k and v are then only checked for shape, the K/V prep
+    launch is skipped and the key states are returned as None."""
     d = ATTN_HEAD_DIM
     for name, t in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         if not t.is_cuda:
@@ -539,12 +546,18 @@ def _prefix_attention_impl(
         raise RuntimeError(f"prefix_attention: q {tuple(q.shape)} / k {tuple(k.shape)} do not match "
                            f"{h} query and {kvh} KV heads of {d}")
     qc, kc, vc = (t if t.is_contiguous() else t.contiguous() for t in (q, k, v))
-    cs = [t.expand(b, s, d).contiguous() if t.dim() == 3 else t.reshape(b, s, d).contiguous() for t in (cos, sin)]
+    cs = _rope_tables(cos, sin, b, s)
     m, mbs, mrs, mlen = _attention_mask_arg(mask, b, s, q.device)
     lib = _lib if _lib is not None else load_int4_gemm()
     dev = q.device
-    k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=dev)
-    kv_mfma = torch.empty(_kv_mfma_elems(lib, b, s, kvh, d), dtype=torch.float16, device=dev)
+    prepped = kv_mfma is not None
+    if prepped:
+        if kv_mfma.device != dev or kv_mfma.dtype != torch.float16 or kv_mfma.numel() != _kv_mfma_elems(lib, b, s, kvh, d):
+            raise RuntimeError("prefix_attention: kv_mfma must be the fp16 fragment-major K/V^T of this call")
+        k_rope = None
+    else:
+        k_rope = torch.empty((b, kvh, s, d), dtype=torch.float16, device=dev)
+        kv_mfma = torch.empty(_kv_mfma_elems(lib, b, s, kvh, d), dtype=torch.float16, device=dev)
     if not (need_out or quantize_out):
         raise RuntimeError("prefix_attention: the output can only be dropped when it is quantized")
     out = torch.empty((b, s, h * d) if need_out else (0,), dtype=torch.float16, device=dev)
@@ -555,8 +568,9 @@ def _prefix_attention_impl(
         scales = torch.empty((b * s,), dtype=torch.float32, device=dev)
     with _on_device(dev):
         st = _stream(dev)
-        _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
-                                         _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
+        if not prepped:
+            _check(lib.pi05w4a4_attn_kv_prep(_ptr(kc), _ptr(vc), kvh * d, _ptr(cs[0]), _ptr(cs[1]), b, s, kvh, d,
+                                             _ptr(k_rope), _ptr(kv_mfma), st), "pi05w4a4_attn_kv_prep")
         wa = _warm_args(warm, "prefix_attention") if warm else None
         if wa is not None:
             _check(lib.pi05w4a4_prefix_attention_warm(_ptr(qc), h * d, _ptr(kv_mfma), _ptr(cs[0]), _ptr(cs[1]),
@@ -573,8 +587,70 @@ def _prefix_attention_impl(
     return out, k_rope
 
 
+def _rope_tables(cos: torch.Tensor, sin: torch.Tensor, b: int, s: int) -> list[torch.Tensor]:
+    return [t.expand(b, s, ATTN_HEAD_DIM).contiguous() if t.dim() == 3 else t.reshape(b, s, ATTN_HEAD_DIM).contiguous()
+            for t in (cos, sin)]
+
+
+def rope_pair_weight(w: torch.Tensor) -> torch.Tensor:
+    """The K weight of ``rms_norm_int4_gemm3_rope``: an MFMA-layout K projection (N = 256
+    output channels = one head of 256) with its 16-channel blocks in RoPE-pair order, so
+    that one wave of the QKV GEMM holds the dimensions d and d + 128 that RoPE mixes
+    (``pi05w4a4_permute_rope_pairs``)."""
+    if w.dim() != 2 or int(w.size(0)) != ATTN_HEAD_DIM or w.dtype != torch.int32 or not w.is_cuda:
+        raise RuntimeError("rope_pair_weight takes an int32 MFMA-layout K weight [256, K/8+16] on the GPU")
+    k = (int(w.size(1)) - MFMA_MARKER_WORDS) * 8
+    if not is_mfma_layout(w, k):
+        raise RuntimeError("rope_pair_weight takes an MFMA-layout weight ([N, K/8+16])")
+    src = w.contiguous()
+    out = torch.zeros_like(src)
+    lib = _lib if _lib is not None else load_int4_gemm()
+    with _on_device(w.device):
+        _check(lib.pi05w4a4_permute_rope_pairs(src.data_ptr(), k, out.data_ptr(), _stream(w.device)),
+               "pi05w4a4_permute_rope_pairs")
+    return out
+
+
+def _rms_norm_qkv_rope_impl(x, norm_weight, eps, unit_offset, w_q, w_k_rope, w_v, cos, sin):
+    """(q [B, S, Nq], key states with RoPE [B, 1, S, 256], v [B, S, 256], fragment-major K/V^T)
+    of ``rms_norm_int4_gemm3`` plus the attention prep, from one norm + quant and one GEMM
+    launch (``pi05w4a4_gemm_qkv_rope``)."""
+    if x.dim() != 3:
+        raise RuntimeError("rms_norm_int4_gemm3_rope expects x [B, S, 2048]")
+    k = _check_x(x)
+    for name, w in (("q", w_q), ("k", w_k_rope), ("v", w_v)):
+        _check_packed(w, k, f"{name} weight")
+        if not is_mfma_layout(w, k):
+            raise RuntimeError(f"rms_norm_int4_gemm3_rope takes MFMA-layout weights ({name})")
+    if int(w_k_rope.size(0)) != ATTN_HEAD_DIM or int(w_v.size(0)) != ATTN_HEAD_DIM:
+        raise RuntimeError("rms_norm_int4_gemm3_rope needs one KV head of 256")
+    b, s = int(x.size(0)), int(x.size(1))
+    for name, t in (("cos", cos), ("sin", sin)):
+        if not t.is_cuda or t.dtype != torch.float16 or t.device != x.device:
+            raise RuntimeError(f"rms_norm_int4_gemm3_rope: {name} must be float16 on {x.device}")
+    q, sa = rms_norm_quantize(x, norm_weight, eps, unit_offset)
+    return _gemm_qkv_rope(q, sa, k, w_q, w_k_rope, w_v, _rope_tables(cos, sin, b, s), b, s, x.device)
+
+
+def _gemm_qkv_rope(q, sa, k, w_q, w_k_rope, w_v, cs, b, s, dev):
+    """The GEMM launch of rms_norm_int4_gemm3_rope on quantized activations."""
+    lib = _lib if _lib is not None else load_int4_gemm()
+    m = b * s
+    nq = int(w_q.size(0))
+    yq = torch.empty((b, s, nq), dtype=torch.float16, device=dev)
+    k_rope = torch.empty((b, 1, s, ATTN_HEAD_DIM), dtype=torch.float16, device=dev)
+    yv = torch.empty((b, s, ATTN_HEAD_DIM), dtype=torch.float16, device=dev)
+    kv = torch.empty(_kv_mfma_elems(lib, b, s, 1, ATTN_HEAD_DIM), dtype=torch.float16, device=dev)
+    with _on_device(dev):
+        _check(lib.pi05w4a4_gemm_qkv_rope(q.data_ptr(), sa.data_ptr(), m, k, w_q.data_ptr(), nq, w_k_rope.data_ptr(),
+                                          w_v.data_ptr(), cs[0].data_ptr(), cs[1].data_ptr(), b, s, yq.data_ptr(),
+                                          k_rope.data_ptr(), yv.data_ptr(), kv.data_ptr(), _stream(dev)),
+               "pi05w4a4_gemm_qkv_rope")
+    return yq, k_rope, yv, kv
+
+
 def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, w_o, residual,
-                                  warm=None, return_out=True):
+                                  warm=None, return_out=True, kv_mfma=None):
     """RoPE + attention + o_proj + residual add: with one KV head and 8 query heads of 256
     the attention kernel quantizes its own output rows for the o GEMM; otherwise the output
     goes through the separate quantizer.  Returns (residual + o_proj(out), key states, out);
@@ -588,11 +664,12 @@ def _prefix_attention_o_proj_impl(q, k, v, cos, sin, mask, scaling, num_heads, n
     if int(num_kv_heads) == 1 and k_in == 2048:
         out, k_rope, codes, scales = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads,
                                                             num_kv_heads, quantize_out=True, warm=warm,
-                                                            need_out=return_out)
+                                                            need_out=return_out, kv_mfma=kv_mfma)
         with _on_device(q.device):
             y = _gemm_from_q(codes, scales, k_in, [(w, n_true)], lead, q.device, "int4_gemm", residual=residual)[0]
         return y, k_rope, out
-    out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, warm=warm)
+    out, k_rope = _prefix_attention_impl(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_heads, warm=warm,
+                                         kv_mfma=kv_mfma)
     return _run(out, [w_o], tiled=False, kind="int4_gemm", residual=residual)[0], k_rope, out
 
 
@@ -602,7 +679,7 @@ def _register_custom_op() -> None:
     if _op_registered:
         return
     try:
-        torch.ops.pi05_w4a4.prefix_attention_o_proj
+        torch.ops.pi05_w4a4.prefix_attention_o_proj_kv
         _op_registered = True
         return
     except (AttributeError, RuntimeError):
@@ -744,6 +821,40 @@ def _register_custom_op() -> None:
         b, s = q.shape[0], q.shape[1]
         dropped = not return_out and num_kv_heads == 1 and num_heads * ATTN_HEAD_DIM == 2048
         return (q.new_empty((b, s, w_o.shape[0])), q.new_empty((b, num_kv_heads, s, ATTN_HEAD_DIM)),
+                q.new_empty((0,) if dropped else (b, s, num_heads * ATTN_HEAD_DIM)))
+
+    # Not in the reference: the QKV GEMMs with RoPE and the attention's K/V layout in the
+    # epilogue, and the attention + o_proj that reads them (no K/V prep launch).
+    @torch.library.custom_op("pi05_w4a4::rms_norm_int4_gemm3_rope", mutates_args=())
+    def _rms_norm_int4_gemm3_rope(
+        x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
+        w_q: torch.Tensor, w_k_rope: torch.Tensor, w_v: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+    ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        return _rms_norm_qkv_rope_impl(x, norm_weight, eps, unit_offset, w_q, w_k_rope, w_v, cos, sin)
+
+    @_rms_norm_int4_gemm3_rope.register_fake
+    def _rms_norm_int4_gemm3_rope_fake(x, norm_weight, eps, unit_offset, w_q, w_k_rope, w_v, cos, sin):
+        b, s = x.shape[0], x.shape[1]
+        s_pad = (s + 63) // 64 * 64
+        return (x.new_empty((b, s, w_q.shape[0])), x.new_empty((b, 1, s, ATTN_HEAD_DIM)),
+                x.new_empty((b, s, ATTN_HEAD_DIM)), x.new_empty((b * 2 * s_pad * ATTN_HEAD_DIM,)))
+
+    @torch.library.custom_op("pi05_w4a4::prefix_attention_o_proj_kv", mutates_args=())
+    def _prefix_attention_o_proj_kv(
+        q: torch.Tensor, v: torch.Tensor, kv_mfma: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+        mask: torch.Tensor | None, scaling: float, num_heads: int, w_o: torch.Tensor, residual: torch.Tensor,
+        warm: list[torch.Tensor], return_out: bool,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        y, _, out = _prefix_attention_o_proj_impl(q, v, v, cos, sin, mask, scaling, num_heads, 1, w_o, residual,
+                                                  warm, return_out, kv_mfma=kv_mfma)
+        return y, out
+
+    @_prefix_attention_o_proj_kv.register_fake
+    def _prefix_attention_o_proj_kv_fake(q, v, kv_mfma, cos, sin, mask, scaling, num_heads, w_o, residual, warm,
+                                         return_out):
+        b, s = q.shape[0], q.shape[1]
+        dropped = not return_out and num_heads * ATTN_HEAD_DIM == 2048
+        return (q.new_empty((b, s, w_o.shape[0])),
                 q.new_empty((0,) if dropped else (b, s, num_heads * ATTN_HEAD_DIM)))
 
     _op_registered = True
@@ -907,6 +1018,31 @@ def prefix_attention_o_proj(q, k, v, cos, sin, mask, scaling, num_heads, num_kv_
     return torch.ops.pi05_w4a4.prefix_attention_o_proj(q, k, v, cos, sin, mask, float(scaling), int(num_heads),
                                                        int(num_kv_heads), w_o, residual, list(warm or []),
                                                        bool(return_out))
+
+
+def rms_norm_int4_gemm3_rope(x, norm_weight, eps, w_q, w_k_rope, w_v, cos, sin, unit_offset=True):
+    """``rms_norm_int4_gemm3`` for one KV head of 256 with the attention prep in the GEMM
+    epilogue: (q [B, S, Nq], key states with RoPE [B, 1, S, 256], v [B, S, 256], K/V^T in
+    the attention kernel's fragment-major layout).  ``w_k_rope`` is ``rope_pair_weight`` of
+    the K weight; S must be a multiple of 8 (at most 1024).  The key states are the eager
+    ``apply_rotary_pos_emb`` keys bit for bit, as ``prefix_attention`` returns them."""
+    if _direct(x, norm_weight, w_q, w_k_rope, w_v, cos, sin):
+        return _rms_norm_qkv_rope_impl(x, norm_weight, float(eps), bool(unit_offset), w_q, w_k_rope, w_v, cos, sin)
+    return torch.ops.pi05_w4a4.rms_norm_int4_gemm3_rope(x, norm_weight, float(eps), bool(unit_offset), w_q, w_k_rope,
+                                                        w_v, cos, sin)
+
+
+def prefix_attention_o_proj_kv(q, v, kv_mfma, cos, sin, mask, scaling, num_heads, w_o, residual, warm=None,
+                               return_out=True):
+    """``prefix_attention_o_proj`` for one KV head with K and V^T already laid out by
+    ``rms_norm_int4_gemm3_rope`` (no K/V prep launch): (residual + o_proj(attention), out)."""
+    if _direct(q, v, kv_mfma, cos, sin, mask, w_o, residual):
+        y, _, out = _prefix_attention_o_proj_impl(q, v, v, cos, sin, mask, float(scaling), int(num_heads), 1, w_o,
+                                                  residual, warm, bool(return_out), kv_mfma=kv_mfma)
+        return y, out
+    return torch.ops.pi05_w4a4.prefix_attention_o_proj_kv(q, v, kv_mfma, cos, sin, mask, float(scaling),
+                                                          int(num_heads), w_o, residual, list(warm or []),
+                                                          bool(return_out))
 
 
 def preload() -> None:

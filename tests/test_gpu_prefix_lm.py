@@ -52,7 +52,8 @@ class _Recorder:
     """Wraps the extension ops (and the name linear.py imported) to record every call."""
 
     NAMES = ("int4_gemm", "int4_gemm_tiled", "int4_gemm2", "int4_gemm2_tiled", "int4_gemm3", "int4_gemm2_gelu",
-             "rms_norm_int4_gemm3", "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj")
+             "rms_norm_int4_gemm3", "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj",
+             "rms_norm_int4_gemm3_rope", "prefix_attention_o_proj_kv")
 
     def __init__(self, monkeypatch):
         from pi05_fast.w4a4 import extension, linear
@@ -93,17 +94,67 @@ def _oracle_h(x: np.ndarray, w: torch.Tensor, k: int) -> np.ndarray:
     return orc.int4_gemm_ref(x, _row_major(w, k))
 
 
+# GEMM column gc of the RoPE-pair-ordered K weight is key dimension 16 P + 128 h + c
+# (gc = 32 P + 16 h + c): extension.rope_pair_weight.
+ROPE_PAIR_DIM = np.array([(gc // 32) * 16 + 128 * ((gc // 16) % 2) + gc % 16 for gc in range(256)])
+
+
+def _check_qkv_rope(cuda, i, args, kwargs, outs) -> None:
+    """rms_norm_int4_gemm3_rope: q and v against the oracle; the key states against
+    transformers' apply_rotary_pos_emb of the oracle's k; the fragment-major K/V^T against
+    the K/V prep kernel run on the oracle's k and v (that kernel's own test pins it)."""
+    from transformers.models.gemma.modeling_gemma import apply_rotary_pos_emb
+
+    from pi05_fast.w4a4 import extension as ext
+
+    x, norm_w, eps, w_q, w_k, w_v, cos, sin = args[:8]
+    b, s, k = x.shape
+    xn = orc.rms_norm_lanes(x.reshape(-1, k).cpu().numpy(), norm_w.cpu().numpy(), eps,
+                            unit_offset=kwargs.get("unit_offset", True))
+    q_got, kr_got, v_got, kv_got = outs
+    for nm, w, o in (("q", w_q, q_got), ("v", w_v, v_got)):
+        want = _oracle_h(xn, w, k)
+        nbad = int(np.count_nonzero(o.reshape(want.shape).cpu().numpy().view(np.int16) != want.view(np.int16)))
+        assert nbad == 0, f"call {i} (rms_norm_int4_gemm3_rope {nm}): {nbad}/{want.size} fp16 outputs differ"
+    kp = _oracle_h(xn, w_k, k)
+    k_want = np.empty_like(kp)
+    k_want[:, ROPE_PAIR_DIM] = kp
+    kt = torch.from_numpy(k_want).to(cuda).view(b, s, 1, 256)
+    vt = torch.from_numpy(_oracle_h(xn, w_v, k)).to(cuda).view(b, s, 1, 256)
+    cs, sn = ext._rope_tables(cos, sin, b, s)
+    _, kr_want = apply_rotary_pos_emb(kt.transpose(1, 2), kt.transpose(1, 2), cs, sn)
+    assert torch.equal(kr_got, kr_want.contiguous()), f"call {i}: key states differ from apply_rotary_pos_emb"
+    lib = ext.load_int4_gemm()
+    kr_prep = torch.empty_like(kr_got)
+    kv_prep = torch.empty_like(kv_got)
+    ktc, vtc = kt.contiguous(), vt.contiguous()
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.pi05w4a4_attn_kv_prep(ktc.data_ptr(), vtc.data_ptr(), 256, cs.data_ptr(), sn.data_ptr(), b, s, 1, 256,
+                                     kr_prep.data_ptr(), kv_prep.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert torch.equal(kv_got, kv_prep), f"call {i}: fragment-major K/V^T differ from the K/V prep kernel's"
+
+
 def _check_call(cuda, i, call) -> None:
     """One recorded W4A4 op against the oracle, bit for bit."""
     name, args, kwargs, outs = call
-    if name == "prefix_attention_o_proj":
+    if name == "rms_norm_int4_gemm3_rope":
+        _check_qkv_rope(cuda, i, args, kwargs, outs)
+        return
+    if name in ("prefix_attention_o_proj", "prefix_attention_o_proj_kv"):
         # the o projection of the attention output it returned (quantized inside the kernel)
-        w_o, res = args[9], args[10]
-        x2, out = outs[0], outs[2]
-        if out.numel() == 0:  # the fused layer drops the attention output: recompute it
-            from pi05_fast.w4a4 import extension as ext
+        from pi05_fast.w4a4 import extension as ext
 
-            out = ext.prefix_attention(*args[:9])[0]
+        if name == "prefix_attention_o_proj":
+            w_o, res = args[9], args[10]
+            x2, out = outs[0], outs[2]
+            if out.numel() == 0:  # the fused layer drops the attention output: recompute it
+                out = ext.prefix_attention(*args[:9])[0]
+        else:
+            q, v, kv, cos, sin, mask, scaling, heads, w_o, res = args[:10]
+            x2, out = outs
+            if out.numel() == 0:
+                out = ext._prefix_attention_impl(q, v, v, cos, sin, mask, scaling, heads, 1, kv_mfma=kv)[0]
         k = out.shape[-1]
         want = _oracle_h(out.reshape(-1, k).cpu().numpy(), w_o, k)
         want = (want.astype(np.float32) + res.reshape(want.shape).cpu().numpy().astype(np.float32)).astype(np.float16)
@@ -141,17 +192,20 @@ def _check_call(cuda, i, call) -> None:
 # batch-8 x 776 throughput point (M = 6208: 56 row tiles, a 7168-workgroup gate/up grid,
 # attention at batch 8), plus a deep short forward.
 FORWARDS = [
-    # layers, tokens, batch, fused decoder layer
-    (2, 776, 1, True), (2, 776, 1, False), (18, 128, 1, True), (18, 128, 1, False),
-    (2, 640, 1, True), (2, 768, 1, True), (1, 776, 8, True), (1, 776, 8, False),
+    # layers, tokens, batch, fused decoder layer, RoPE + K/V layout in the QKV epilogue
+    (2, 776, 1, True, True), (2, 776, 1, True, False), (2, 776, 1, False, False), (18, 128, 1, True, True),
+    (18, 128, 1, False, False), (2, 640, 1, True, True), (2, 768, 1, True, True), (1, 776, 8, True, True),
+    (1, 776, 8, True, False), (1, 776, 8, False, False),
 ]
 
 
-@pytest.mark.parametrize("layers,tokens,batch,fuse_layer", FORWARDS)
-def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, batch, fuse_layer):
+@pytest.mark.parametrize("layers,tokens,batch,fuse_layer,fuse_kv", FORWARDS)
+def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, batch, fuse_layer, fuse_kv):
     from pi05_fast.w4a4.prefix_lm import prefix_inputs
 
-    print(f"prefix LM forward: {layers} layers x {tokens} tokens x batch {batch}, fused layer {fuse_layer}", flush=True)
+    print(f"prefix LM forward: {layers} layers x {tokens} tokens x batch {batch}, fused layer {fuse_layer}, "
+          f"fused K/V prep {fuse_kv}", flush=True)
+    monkeypatch.setenv("PI05_W4A4_FUSE_KV", "1" if fuse_kv else "0")
     model, _ = _build(cuda, layers, fuse_gelu=True, fuse_layer=fuse_layer)
     rec = _Recorder(monkeypatch)
     x = prefix_inputs(batch, tokens, cuda)
@@ -165,9 +219,11 @@ def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, b
     assert isinstance(model.layers[0].input_layernorm, FusedRMSNorm)
     kinds = [c[0] for c in rec.calls]
     if fuse_layer:
-        assert kinds.count("rms_norm_int4_gemm3") == layers  # input norm + QKV
+        qkv, attn = ("rms_norm_int4_gemm3_rope", "prefix_attention_o_proj_kv") if fuse_kv else \
+            ("rms_norm_int4_gemm3", "prefix_attention_o_proj")
+        assert kinds.count(qkv) == layers  # input norm + QKV (+ RoPE and the K/V layout)
         assert kinds.count("rms_norm_int4_gemm2_gelu") == layers  # post norm + gate/up + GELU*up
-        assert kinds.count("prefix_attention_o_proj") == layers  # attention, o + residual add
+        assert kinds.count(attn) == layers  # attention, o + residual add
         assert kinds.count("int4_gemm_residual") == layers  # down + residual add
     else:
         assert kinds.count("int4_gemm3") == layers  # QKV
