@@ -339,6 +339,20 @@ def test_attention_abi_validation_without_gpu(lib):
     assert attn(h=16, kvh=2, qc=p) == 1 and "one KV head" in _err(lib)
     assert attn(qc=p) == 1 and "q_scales" in _err(lib)
 
+    # the QKV GEMMs with the attention prep: M = B * S with S a multiple of 8 in [8, 1024],
+    # one KV head of 256 (the weights' N is fixed), everything 16-byte aligned
+    def qkv_rope(m=776, b=1, s=776, n_q=2048, out=p, cos=p):
+        return lib.pi05w4a4_gemm_qkv_rope(p, p, m, 2048, p, n_q, p, p, cos, p, b, s, p, out, p, p, vp(0))
+
+    assert qkv_rope(m=20, s=20) == 1 and "multiple of 8" in _err(lib)
+    assert qkv_rope(m=776, b=2) == 1 and "M = B * S" in _err(lib)
+    assert qkv_rope(m=2056, s=1028, b=2) == 1
+    assert qkv_rope(n_q=2040) == 1 and "multiple of 16" in _err(lib)
+    assert qkv_rope(out=vp(0)) == 1 and "null" in _err(lib)
+    assert qkv_rope(cos=vp(264)) == 1 and "16-byte aligned" in _err(lib)
+    assert lib.pi05w4a4_permute_rope_pairs(p, 2048, p, vp(0)) == 1 and "not in place" in _err(lib)
+    assert lib.pi05w4a4_permute_rope_pairs(p, 100, vp(512), vp(0)) == 1 and "multiple of 64" in _err(lib)
+
     # the cache-warming variant: up to 4 buffers, 16-byte aligned, sizes multiples of 16;
     # the attention arguments are validated the same way
     def warm(ptrs, sizes, n=None, ld_q=2048):
@@ -383,6 +397,16 @@ def test_custom_ops_registered_with_fakes():
         assert tuple(b.shape) == (2, 776, 256)
         g, u = torch.ops.pi05_w4a4.int4_gemm2_tiled(x, w, w)
         assert tuple(u.shape) == (2, 776, 2560)
+        # QKV with the attention prep: q, key states [B, 1, S, 256], v, K/V^T (keys padded to 64)
+        nw = torch.empty(2048, dtype=torch.float16)
+        cos = torch.empty(2, 776, 256, dtype=torch.float16)
+        q, kr, v, kv = torch.ops.pi05_w4a4.rms_norm_int4_gemm3_rope(x, nw, 1e-6, True, w[:2048], w[:256], w[:256],
+                                                                  cos, cos)
+        assert (tuple(q.shape), tuple(kr.shape), tuple(v.shape)) == ((2, 776, 2048), (2, 1, 776, 256), (2, 776, 256))
+        assert kv.numel() == 2 * 2 * 832 * 256
+        y, out = torch.ops.pi05_w4a4.prefix_attention_o_proj_kv(q, v, kv, cos, cos, None, 0.0625, 8, w[:2048], q, [],
+                                                                False)
+        assert tuple(y.shape) == (2, 776, 2048) and out.numel() == 0
 
 
 def test_ops_reject_cpu_tensors_with_reference_message():
