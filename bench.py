@@ -58,10 +58,8 @@ METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
-# HBM-side traffic per launch of the W4A4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE summary);
-# the plain gate/up GEMM (--unfused-gelu) has its own.
+# HBM-side traffic per launch of the W4A4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE summary).
 TRAFFIC_FILE = ROOT / "profiles" / "w4a4_kernels_776tok_traffic.md"
-TRAFFIC_FILE_GATE_UP = ROOT / "profiles" / "gate_up_gemm_776x2048x32768_traffic.md"
 
 
 def parse_args():
@@ -468,13 +466,10 @@ def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
 
 def read_traffic(kernel: str) -> tuple[float | None, str | None]:
     """HBM bytes per launch of a kernel class from the committed rocprofv3 summary."""
-    path = TRAFFIC_FILE_GATE_UP if kernel == "gate_up" else TRAFFIC_FILE
+    path = TRAFFIC_FILE
     if not path.is_file():
         return None, None
-    text = path.read_text()
-    m = re.search(rf"traffic_bytes_per_launch\[{kernel}\]:\s*([0-9.eE+]+)", text)
-    if m is None and kernel == "gate_up":
-        m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    m = re.search(rf"traffic_bytes_per_launch\[{kernel}\]:\s*([0-9.eE+]+)", path.read_text())
     if not m:
         return None, None
     return float(m.group(1)), str(path.relative_to(ROOT))

@@ -153,8 +153,9 @@ __device__ __forceinline__ int64_t vfrag_slot(int d, int t0, int nst) {
   return (static_cast<int64_t>((d >> 4) * nst + (t0 >> 5))) * 64 + 16 * ((t0 & 31) >> 3) + (d & 15);
 }
 
-template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE>
+template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
+  static_assert(!(GELU && QKV_PREP), "the attention prep is a fp16 epilogue");
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
@@ -345,7 +346,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // values are fetched now so that their latency hides under the main loop.  The loads
   // are unconditional (other waves read a fixed in-bounds word of the codes) to keep the
   // vmcnt bookkeeping exact.
-  constexpr bool kRopePre = !GELU && MI * (NI / 2) <= 2;
+  constexpr bool kRopePre = QKV_PREP && MI * (NI / 2) <= 2;
   half4 rpre[kRopePre ? MI : 1][kRopePre ? NI / 2 : 1][4];
   if constexpr (kRopePre) {
     const bool rope_wave = p.rope_group == gsel + 1;
@@ -514,8 +515,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // Residual (one-group fp16 mode): y = fp16(y + res), the rounding of torch's fp16 add.
     static_assert(GELU || (LPR == RLPR && RPI == RRPI), "residual pieces follow the store layout");
     // Attention prep (QKV): this wave's group is K in RoPE-pair order, or V.
-    const bool rope = !GELU && p.rope_group == gsel + 1;
-    const bool vtr = !GELU && p.vt_group == gsel + 1;
+    const bool rope = QKV_PREP && p.rope_group == gsel + 1;
+    const bool vtr = QKV_PREP && p.vt_group == gsel + 1;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       half4 ob[GELU ? 1 : NI];
@@ -787,6 +788,8 @@ hipError_t launch_cfg(const GemmParams& p, hipStream_t stream) {
                   static_cast<unsigned>(p.ksplit));
   if (p.mode == kEpiGeluUp || (p.mode == kEpiPartial && p.gelu_pair_n > 0))
     gemm_w4a4_kernel<MI, NI, NWAVES, KW, true, RING, WPE><<<grid, 64 * NWAVES, 0, stream>>>(p);
+  else if (p.rope_group > 0)
+    gemm_w4a4_kernel<MI, NI, NWAVES, KW, false, RING, WPE, true><<<grid, 64 * NWAVES, 0, stream>>>(p);
   else
     gemm_w4a4_kernel<MI, NI, NWAVES, KW, false, RING, WPE><<<grid, 64 * NWAVES, 0, stream>>>(p);
   return hipGetLastError();
