@@ -37,10 +37,14 @@
 //   phase 3  O^T = V^T P^T, each wave owning 32 of the 256 output dimensions over all
 //            keys (V^T fragments from HBM, P from LDS).  Each lane ends with 4
 //            consecutive dimensions of one query row.
+// The memory phases are kept fed ahead of time: the first two K blocks of every wave are
+// requested in phase 0, and the first 8 V^T steps of its 8-deep ring during the softmax.
 //
 // Bound: each workgroup streams all of K and V (2 x keys x 512 B) through its CU's vector
 // memory path, about 64 B per clock, ~13k clocks at 776 keys; the softmax is VALU work
-// (a wave64 VALU instruction occupies its SIMD for 4 clocks).
+// (a wave64 VALU instruction occupies its SIMD for 4 clocks).  Measured inside the
+// 776-token forward (per-workgroup timestamps, medians): query load + RoPE 3.7 us,
+// scores 4.0, softmax 3.0, PV 3.7, o-proj quant 3.6.
 
 #include "cache_warm.h"
 #include "quant_row.h"
@@ -177,9 +181,32 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   const int rows = S * n_rep;
   const int row0 = blockIdx.x * kRows;
 
+  // Phase 1's K blocks: wave w takes the 16-key blocks w, w + 8, ... through a 3-deep
+  // register ring.  MFMA operand A is K[key 16*j + L%16][32*t + 8*(L/16) + 0..7].  Every
+  // K (and mask) load is unconditional, with its block clamped into the buffer, so that
+  // the compiler's vmcnt waits stay exact (a load under a branch makes every later wait
+  // assume the path with fewer loads in flight); a wave without blocks (s_pad < 128)
+  // loads one it never uses.
+  const int nblk = s_pad / 16;
+  const _Float16* kf = p.kv_mfma + (b * p.kvh + g) * 2 * static_cast<int64_t>(s_pad) * kD + 8 * lane;
+  const int jlast = w + ((nblk - 1 - w) / kWaves) * kWaves;  // this wave's last block (w < nblk)
+  const int jcap = min(jlast, nblk - 1);
+  auto load_k = [&](int j, half8 (&kk)[8]) {
+    const _Float16* kr = kf + min(j, jcap) * (8 * 512);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) kk[t] = ld8(kr + 512 * t);
+  };
+  half8 k0[8], k1[8], k2[8];
+  const bool has_mask = p.mask != nullptr;
+  uint4 mraw[SCH];  // the softmax phase's mask chunks (raw bits; zeroed there without a mask)
+
   // ---- phase 0: the 32 query rows with RoPE, once per workgroup, into LDS.  Thread t
   // takes row t / 16 and the element pairs (c, c + 128), c = 8 * (t % 16).  Rows past the
-  // group are clamped (loaded, never stored).
+  // group are clamped (loaded, never stored).  After the query rows, the loads of the
+  // softmax's mask chunks (thread t: row t / 16, the 8-key chunks 8 * (t % 16 + 16 * ch))
+  // and of the wave's first two K blocks are issued, so that their latency overlaps this
+  // phase: loads complete in issue order, and the RoPE below waits for the query loads
+  // only.
   {
     const int r = tid >> 4;
     const int c = (tid & 15) * 8;
@@ -189,35 +216,38 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     const _Float16* cr = p.cosb + tk * kD;
     const _Float16* sr = p.sinb + tk * kD;
     half8 lo = ld8(qr + c), hi = ld8(qr + 128 + c);
-    rope_pair(lo, hi, ld8(cr + c), ld8(cr + 128 + c), ld8(sr + c), ld8(sr + 128 + c));
+    const half8 clo = ld8(cr + c), chi = ld8(cr + 128 + c), slo = ld8(sr + c), shi = ld8(sr + 128 + c);
+    // Every wave's query loads reach the CU's memory pipeline before any of the loads
+    // below (which would otherwise queue ahead of a slower wave's query rows).
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      // Without a mask the loads read the first query elements (the bits are dropped).  The
+      // row pointer is a global-address-space one, so that these are global (not flat)
+      // loads, which count in vmcnt only.
+      typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+      typedef const __attribute__((address_space(1))) u32x2* gptr2;
+      const int64_t moff = has_mask ? b * p.mask_bs + static_cast<int64_t>(rr / n_rep) * p.mask_rs : 0;
+      const _Float16* mrow = (has_mask ? p.mask : p.q) + moff;
+      const int mlast = has_mask ? p.mask_len - 4 : 0;
+      const int mc = tid & 15;
+#pragma unroll
+      for (int ch = 0; ch < SCH; ++ch) {
+        const int kc = 8 * (mc + 16 * ch);  // chunks at or past s_pad are never used
+        const u32x2 mv0 = *(gptr2)(mrow + min(kc, mlast));
+        const u32x2 mv1 = *(gptr2)(mrow + min(kc + 4, mlast));
+        mraw[ch] = uint4{mv0.x, mv0.y, mv1.x, mv1.y};
+      }
+    }
+    load_k(w, k0);
+    load_k(w + kWaves, k1);
+    __builtin_amdgcn_sched_barrier(0);
+    rope_pair(lo, hi, clo, chi, slo, shi);
     st8(qs + r * kQld + c, lo);
     st8(qs + r * kQld + 128 + c, hi);
   }
   __syncthreads();
-
-  // The softmax phase's mask chunks, loaded now so that their latency hides under phase 1
-  // (after phase 0, whose query loads they would delay): thread t takes row t / 16 and the
-  // 8-key chunks 8 * (t % 16 + 16 * ch).
-  const bool has_mask = p.mask != nullptr;
-  half8 mk[SCH];
-  {
-    const int r = tid >> 4;
-    const int c = tid & 15;
-    const int rr = min(row0 + r, rows - 1);
-    const _Float16* mrow =
-        has_mask ? p.mask + b * p.mask_bs + static_cast<int64_t>(rr / n_rep) * p.mask_rs : nullptr;
-    const int mlast = p.mask_len - 4;
-#pragma unroll
-    for (int ch = 0; ch < SCH; ++ch) {
-      const int k0 = 8 * (c + 16 * ch);
-      mk[ch] = half8{};
-      if (has_mask && k0 < s_pad) {
-        const half4 mv0 = *reinterpret_cast<const half4*>(mrow + min(k0, mlast));
-        const half4 mv1 = *reinterpret_cast<const half4*>(mrow + min(k0 + 4, mlast));
-        mk[ch] = half8{mv0[0], mv0[1], mv0[2], mv0[3], mv1[0], mv1[1], mv1[2], mv1[3]};
-      }
-    }
-  }
 
   // MFMA operand B of S^T = K Q^T: lane L holds Q[row 16*qb + L%16][32*t + 8*(L/16) + 0..7].
   half8 qop[2][8];
@@ -226,21 +256,11 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
 #pragma unroll
     for (int t = 0; t < 8; ++t) qop[qb][t] = ld8(qs + (16 * qb + lr) * kQld + 32 * t + 8 * lg);
 
-  // ---- phase 1: scores.  Wave w takes the 16-key blocks w, w + 8, ... through a 3-deep
-  // register ring (K loads two blocks ahead).  MFMA operand A is
-  // K[key 16*j + L%16][32*t + 8*(L/16) + 0..7]; the result lane L holds
-  // S^T[key 16*j + 4*(L/16) + i][row 16*qb + L%16], i = 0..3, stored to LDS as
-  // fp16(fp16(q.k) * scaling), or -inf for the padding keys past S.  The mask is added in
-  // the softmax phase.
-  const int nblk = s_pad / 16;
-  const _Float16* kf = p.kv_mfma + (b * p.kvh + g) * 2 * static_cast<int64_t>(s_pad) * kD + 8 * lane;
+  // ---- phase 1: scores, the K ring loading two blocks ahead (the first two were requested
+  // in phase 0).  The result lane L holds S^T[key 16*j + 4*(L/16) + i][row 16*qb + L%16],
+  // i = 0..3, stored to LDS as fp16(fp16(q.k) * scaling), or -inf for the padding keys
+  // past S.  The mask is added in the softmax phase.
   if (w < nblk) {
-    const int jlast = w + ((nblk - 1 - w) / kWaves) * kWaves;  // this wave's last block
-    auto load_k = [&](int j, half8 (&kk)[8]) {
-      const _Float16* kr = kf + min(j, jlast) * (8 * 512);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) kk[t] = ld8(kr + 512 * t);
-    };
     auto scores = [&](const half8 (&kk)[8], int j) {
 #pragma clang fp contract(off)
       f4 acc[2] = {f4{0, 0, 0, 0}, f4{0, 0, 0, 0}};
@@ -261,9 +281,6 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
         *reinterpret_cast<half4*>(&sc[(16 * qb + lr) * sld + 16 * j + 4 * lg]) = sv;
       }
     };
-    half8 k0[8], k1[8], k2[8];
-    load_k(w, k0);
-    load_k(w + kWaves, k1);
     for (int j = w;; j += 3 * kWaves) {
       load_k(j + 2 * kWaves, k2);
       scores(k0, j);
@@ -277,6 +294,21 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     }
   }
   __syncthreads();
+
+  // Phase 3 streams V^T through a kVR-deep register ring; its first kVR steps are requested
+  // during the softmax (spread over its first chunk loop, so that the waves do not stall
+  // on a full memory queue before their softmax work), and their latency hides under it.  Wave w reads the V^T fragments of
+  // dimensions 32*w .. 32*w + 31: operand A lane L: V^T[d 32*w + 16*db + L%16][keys
+  // 32*t + 8*(L/16) + 0..7].
+  const int nst = s_pad / 32;
+  const _Float16* vf = kf + static_cast<int64_t>(s_pad) * kD + (2 * w) * nst * 512;
+  auto load_v = [&](int t, half8 (&va)[2]) {
+#pragma unroll
+    for (int db = 0; db < 2; ++db) va[db] = ld8(vf + (db * nst + t) * 512);
+  };
+  constexpr int kVR = 8;
+  half8 vr[kVR][2];
+  static_assert(kVR % SCH == 0 || SCH % kVR == 0, "ring steps spread evenly over the chunks");
 
   // ---- phase 2: softmax of row r = tid / 16 by its 16 threads, keys 8*(c + 16*ch) + 0..7:
   // s = fp16(score + mask) (padding keys are -inf), the row max (exact, in fp16), then
@@ -293,11 +325,15 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     for (int i = 0; i < 8; ++i) mx[i] = static_cast<_Float16>(-__builtin_inff());
 #pragma unroll
     for (int ch = 0; ch < SCH; ++ch) {
-      const int k0 = 8 * (c + 16 * ch);
+#pragma unroll
+      for (int i = ch * kVR / SCH; i < (ch + 1) * kVR / SCH; ++i) load_v(min(i, nst - 1), vr[i]);
+      const int kc = 8 * (c + 16 * ch);
       sv[ch] = mx;
-      if (k0 < s_pad) {
+      if (kc < s_pad) {
         // fp16 additions round exactly like torch's fp32-opmath fp16 add.
-        sv[ch] = ld8(&sc[r * sld + k0]) + mk[ch];
+        const uint32_t keep = has_mask ? 0xffffffffu : 0u;
+        const uint4 m4 = {mraw[ch].x & keep, mraw[ch].y & keep, mraw[ch].z & keep, mraw[ch].w & keep};
+        sv[ch] = ld8(&sc[r * sld + kc]) + __builtin_bit_cast(half8, m4);
         mx = __builtin_elementwise_max(mx, sv[ch]);
       }
     }
@@ -325,31 +361,26 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     const float rl = 1.0f / l;
 #pragma unroll
     for (int ch = 0; ch < SCH; ++ch) {
-      const int k0 = 8 * (c + 16 * ch);
-      if (k0 < s_pad) {
+      const int kc = 8 * (c + 16 * ch);
+      if (kc < s_pad) {
         half8 pv;
 #pragma unroll
         for (int i = 0; i < 8; ++i) pv[i] = static_cast<_Float16>(e[ch][i] * rl);
-        st8(&sc[r * sld + k0], pv);
+        st8(&sc[r * sld + kc], pv);
       }
     }
   }
   __syncthreads();
 
-  // ---- phase 3: O^T = V^T P^T for dimensions 32*w .. 32*w + 31 over all keys, V^T through
-  // a 4-deep register ring.  Operand A lane L: V^T[d 32*w + 16*db + L%16][keys
-  // 32*t + 8*(L/16) + 0..7]; operand B lane L: P[row 16*qb + L%16][the same keys].  Result
-  // lane L: O[row 16*qb + L%16][32*w + 16*db + 4*(L/16) + i].
-  const int nst = s_pad / 32;
-  const _Float16* vf = kf + static_cast<int64_t>(s_pad) * kD + (2 * w) * nst * 512;
+  // ---- phase 3: O^T = V^T P^T for dimensions 32*w .. 32*w + 31 over all keys.  Operand
+  // B lane L: P[row 16*qb + L%16][keys 32*t + 8*(L/16) + 0..7].  Result lane L:
+  // O[row 16*qb + L%16][32*w + 16*db + 4*(L/16) + i].  Each step refills its ring slot
+  // with the step kVR ahead.  The main loop's loads are unconditional, which keeps the
+  // compiler's vmcnt waits exact (one ring slot at a time); the last 2*kVR - 1 steps or
+  // fewer run after it, loading only what they still use.
   f4 o[2][2];
 #pragma unroll
   for (int db = 0; db < 2; ++db) o[db][0] = o[db][1] = f4{0, 0, 0, 0};
-  auto load_v = [&](int t, half8 (&va)[2]) {
-    const int tc = min(t, nst - 1);
-#pragma unroll
-    for (int db = 0; db < 2; ++db) va[db] = ld8(vf + (db * nst + tc) * 512);
-  };
   auto pv_step = [&](const half8 (&va)[2], int t) {
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
@@ -359,26 +390,22 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
         o[db][qb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[db], pb, o[db][qb], 0, 0, 0);
     }
   };
-  {
-    half8 v0[2], v1[2], v2[2], v3[2];
-    load_v(0, v0);
-    load_v(1, v1);
-    load_v(2, v2);
-    for (int t = 0;; t += 4) {
-      load_v(t + 3, v3);
-      pv_step(v0, t);
-      if (t + 1 >= nst) break;
-      load_v(t + 4, v0);
-      pv_step(v1, t + 1);
-      if (t + 2 >= nst) break;
-      load_v(t + 5, v1);
-      pv_step(v2, t + 2);
-      if (t + 3 >= nst) break;
-      load_v(t + 6, v2);
-      pv_step(v3, t + 3);
-      if (t + 4 >= nst) break;
+  int t0 = 0;
+  for (; t0 + 2 * kVR <= nst; t0 += kVR) {
+#pragma unroll
+    for (int j = 0; j < kVR; ++j) {
+      pv_step(vr[j], t0 + j);
+      load_v(t0 + j + kVR, vr[j]);
     }
   }
+#pragma unroll
+  for (int j = 0; j < kVR; ++j) {
+    if (t0 + j < nst) pv_step(vr[j], t0 + j);
+    if (t0 + j + kVR < nst) load_v(t0 + j + kVR, vr[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < kVR; ++j)
+    if (t0 + kVR + j < nst) pv_step(vr[j], t0 + kVR + j);
 
   if (p.out != nullptr) {
 #pragma unroll
