@@ -43,8 +43,8 @@
 // Bound: each workgroup streams all of K and V (2 x keys x 512 B) through its CU's vector
 // memory path, about 64 B per clock, ~13k clocks at 776 keys; the softmax is VALU work
 // (a wave64 VALU instruction occupies its SIMD for 4 clocks).  Measured inside the
-// 776-token forward (per-workgroup timestamps, medians): query load + RoPE 3.7 us,
-// scores 4.0, softmax 3.0, PV 3.7, o-proj quant 3.6.
+// 776-token forward (per-workgroup timestamps, medians): query load + RoPE 3.8 us,
+// scores 4.4, softmax 3.0, PV 3.9, o-proj quant 3.5 (mostly the codes' store latency).
 
 #include "cache_warm.h"
 #include "quant_row.h"
@@ -426,8 +426,9 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
   // ---- phase 4 (one KV head of 8 query heads): the workgroup's 32 rows are 4 whole
   // tokens of the o-proj input (8 heads x 256 = 2048), so it quantizes them itself, as the
   // K = 2048 activation quant would: the fp16 rows are staged in LDS over the
-  // probabilities and waves 0-3 each rotate and quantize one token in registers
-  // (fwht_quant_row_wave).
+  // probabilities and waves 2i, 2i + 1 rotate and quantize token i in registers, 16
+  // elements per lane (fwht_quant_row_2wave: the last butterfly stage and the row's max
+  // and code sum through LDS, behind the staged rows).
   if (p.qcodes != nullptr) {
     __syncthreads();  // every wave is done reading P
     _Float16* otile = sc;                                   // [4][kOld] fp16
@@ -443,17 +444,23 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
       }
     }
     __syncthreads();
-    const int tok = (row0 >> 3) + w;
-    if (w < 4 && tok < S) {
-      float v[32];
+    const int tl = w >> 1;  // token of this wave pair
+    const int tok = (row0 >> 3) + tl;
+    const int t = (w & 1) * 64 + lane;
+    float v[16];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const half8 h = ld8(otile + w * kOld + 32 * lane + 8 * c);
+    for (int c = 0; c < 2; ++c) {
+      const half8 h = ld8(otile + tl * kOld + 16 * t + 8 * c);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
-      }
-      fwht_quant_row_wave<11>(v, lane, b * S + tok, p.qcodes, p.qscales, p.qcorr, p.inv_sqrt_k);
+      for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
     }
+    float* xch = reinterpret_cast<float*>(otile + 4 * kOld);  // [4][2 * 64 * 16] floats
+    float* redf = xch + 4 * 2 * 64 * 16;                       // [4][2]
+    int* redi = reinterpret_cast<int*>(redf + 8);              // [4][2]
+    // Every wave takes part (the pair synchronises with the workgroup); rows past S are
+    // computed from the clamped duplicates staged above and not stored.
+    fwht_quant_row_2wave<11>(v, t, xch + tl * 2 * 64 * 16, redf + 2 * tl, redi + 2 * tl, tok < S,
+                             b * S + min(tok, S - 1), p.qcodes, p.qscales, p.qcorr, p.inv_sqrt_k);
   }
 }
 
@@ -481,7 +488,9 @@ hipError_t launch_prefix_attention(const AttnParams& p_in, hipStream_t stream) {
                   static_cast<unsigned>(p.b));
   size_t sc_bytes = static_cast<size_t>(kRows) * (p.s_pad + 8) * sizeof(_Float16);
   if (p.qcodes != nullptr) {
-    const size_t q_bytes = 4 * kOld * sizeof(_Float16);
+    // the 4 staged fp16 rows, then the quantizer's exchange (4 x 2 x 64 x 16 floats) and
+    // its 16 words of reductions
+    const size_t q_bytes = 4 * kOld * sizeof(_Float16) + (4 * 2 * 64 * 16 + 16) * sizeof(float);
     if (q_bytes > sc_bytes) sc_bytes = q_bytes;
   }
   const size_t lds = static_cast<size_t>(kRows) * kQld * sizeof(_Float16) + sc_bytes;

@@ -384,5 +384,102 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
   s16 = wave_sum_dpp(s16);
   if (t == 0) qcorr[row] = -8 * s16;
 }
+
+// ---- Two waves per row (T = 128): thread t = 64 h + lane (h = the wave of the pair) holds
+// R = K / 128 consecutive elements t*R .. t*R + R - 1.  Element bits 0 .. r+5 are the
+// one-wave form's (registers, then lane bits 0-5); the last stage, over the wave bit h,
+// exchanges the halves through LDS: lane L of the lower wave keeps a + b, of the upper
+// wave a - b, with a the lower wave's value.  The row max and the odd-code sum combine the
+// two waves' through LDS too.  xch: 2 * 64 * R floats of LDS for this row; redf / redi: 2
+// words each.  Every wave of the workgroup calls it together (three workgroup barriers);
+// with `store` false the pair computes but writes nothing (a row past the matrix).
+template <int LOGK>
+__device__ __forceinline__ void fwht_quant_row_2wave(float (&v)[1 << (LOGK - 7)], int t, float* xch, float* redf,
+                                                     int* redi, bool store, int64_t row, int32_t* __restrict__ q,
+                                                     float* __restrict__ sa, int32_t* __restrict__ qcorr,
+                                                     float inv_sqrt_k) {
+  constexpr int K = 1 << LOGK;
+  constexpr int r = LOGK - 7;
+  constexpr int R = 1 << r;
+  static_assert(r >= 4 && R % 4 == 0, "runs of >= 16 consecutive elements per lane");
+  const int lane = t & 63;
+  const int h = t >> 6;
+#pragma unroll
+  for (int b = 0; b < r; ++b) {
+    if (b == 0) reg_stage<0>(v);
+    else if (b == 1) reg_stage<1>(v);
+    else if (b == 2) reg_stage<2>(v);
+    else if (b == 3) reg_stage<3>(v);
+    else if (b == 4) reg_stage<4>(v);
+    else if (b == 5) reg_stage<5>(v);
+    else if (b == 6) reg_stage<6>(v);
+  }
+  lane_stage<0>(v, lane);
+  lane_stage<1>(v, lane);
+  lane_stage<2>(v, lane);
+  lane_stage<3>(v, lane);
+  swap_lane_bit<16, 0>(v);
+  reg_stage<0>(v);  // element bit r + 4
+  swap_lane_bit<32, 1>(v);
+  reg_stage<1>(v);  // element bit r + 5
+  swap_lane_bit<32, 1>(v);
+  swap_lane_bit<16, 0>(v);
+  // element bit r + 6: the other wave's value of the same register and lane
+#pragma unroll
+  for (int j = 0; j < R; j += 4)
+    *reinterpret_cast<float4*>(xch + (h * 64 + lane) * R + j) = make_float4(v[j], v[j + 1], v[j + 2], v[j + 3]);
+  __syncthreads();
+  const float* px = xch + ((h ^ 1) * 64 + lane) * R;
+#pragma unroll
+  for (int j = 0; j < R; j += 4) {
+    const float4 o4 = *reinterpret_cast<const float4*>(px + j);
+    const float o[4] = {o4.x, o4.y, o4.z, o4.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[j + e] = h == 0 ? __fadd_rn(v[j + e], o[e]) : __fsub_rn(o[e], v[j + e]);
+  }
+
+  float amax = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  amax = wave_max_dpp(amax);
+  if (lane == 0) redf[h] = amax;
+  __syncthreads();
+  amax = fmaxf(redf[0], redf[1]);
+  const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
+  if (store && t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
+  uint32_t words[R / 8];
+  bool near_tie = false;
+  const float rcp = __builtin_amdgcn_rcpf(sdiv);
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) {
+    float c8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+    words[u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+  }
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+#pragma unroll
+    for (int u = 0; u < R / 8; ++u) {
+      float c8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+      words[u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+    }
+  }
+  if (store) {
+#pragma unroll
+    for (int u = 0; u < R / 8; u += 2) {
+      const uint2 wd = make_uint2(words[u] ^ kObFlipLo, words[u + 1] ^ kObFlipLo);
+      *reinterpret_cast<uint2*>(&q[frag_word_index(row, (t * R) / 8 + u, kblocks128(K))]) = wd;
+    }
+  }
+  int s16 = 0;
+#pragma unroll
+  for (int u = 0; u < R / 8; ++u) s16 += odd_code_sum16(words[u]);
+  s16 = wave_sum_dpp(s16);
+  if (lane == 0) redi[h] = s16;
+  __syncthreads();
+  if (store && t == 0) qcorr[row] = -8 * (redi[0] + redi[1]);
+}
 }  // namespace
 }  // namespace w4a4
