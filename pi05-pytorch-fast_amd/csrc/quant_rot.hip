@@ -152,9 +152,9 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
   int s16 = 0;
 #pragma unroll
   for (int j = 0; j < J; ++j) {
-    const uint32_t w = static_cast<uint32_t>(quant_pack8(v[j], sdiv));
+    const uint32_t w = quant_pack8(v[j], sdiv);
     s16 += odd_code_sum16(w);
-    q[frag_word_index(row, t + T * j, kblocks128(K))] = static_cast<int32_t>(w ^ kObFlipLo);
+    q[frag_word_index(row, t + T * j, kblocks128(K))] = static_cast<int32_t>(w);
   }
   s16 = row_sum<T>(s16, ired);
   if (t == 0) qcorr[row] = -8 * s16;
@@ -271,9 +271,9 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
     float v[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) v[e] = static_cast<float>(h[e]);
-    const uint32_t w = static_cast<uint32_t>(quant_pack8(v, sdiv));
+    const uint32_t w = quant_pack8(v, sdiv);
     s16 += odd_code_sum16(w);
-    q[frag_word_index(row, c, kblocks128(k))] = static_cast<int32_t>(w ^ kObFlipLo);
+    q[frag_word_index(row, c, kblocks128(k))] = static_cast<int32_t>(w);
   }
   s16 = row_sum<256>(s16, ired);
   if (t == 0) qcorr[row] = -8 * s16;

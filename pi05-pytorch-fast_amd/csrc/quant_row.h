@@ -50,37 +50,41 @@ __device__ __forceinline__ int row_sum(int v, int* red) {
   return v;
 }
 
-// Eight codes clamp(rint(v / sdiv), -7, 7) packed as nibbles 0..7 of one word (two's
-// complement; the stores flip the low nibbles to offset binary).
-__device__ __forceinline__ int32_t quant_pack8(const float (&v)[8], float sdiv) {
+// Eight codes c = clamp(rint(v / sdiv), -7, 7) packed as nibbles 0..7 of one word in the
+// stored form: low nibble of each byte c + 8 (offset binary), high nibble c & 0xF (two's
+// complement).  Each code is computed as c + 8, in [1, 15], and placed with one
+// shift-or; the final xor turns the high nibbles from offset binary to two's complement
+// ((c + 8) ^ 8 == c & 0xF).  A NaN quotient gives -7 (the clamp keeps the non-NaN bound).
+__device__ __forceinline__ uint32_t quant_pack8(const float (&v)[8], float sdiv) {
   uint32_t word = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     float r = __builtin_rintf(__fdiv_rn(v[e], sdiv));
-    r = fminf(fmaxf(r, -7.0f), 7.0f);
-    word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFu) << (4 * e);
+    r = fminf(fmaxf(r, -7.0f), 7.0f) + 8.0f;
+    word |= static_cast<uint32_t>(r) << (4 * e);
   }
-  return static_cast<int32_t>(word);
+  return word ^ kObFlipHi;
 }
 
-// Same eight codes without a division per element.  qa = v * rcp(sdiv) differs from the
-// exact quotient q = v / sdiv by less than 2e-6 (|q| <= 7 and the hardware reciprocal
-// and the product each round within an ulp or two), so rint(qa) == rint(q) unless q lies
-// within 2e-6 of a half-integer.  Any lane that sees qa within 1e-5 of one raises
-// `near_tie`; the caller then redoes the row's codes with quant_pack8 (exact division).
-// Both paths therefore produce the reference's round-half-even codes bit for bit.
-__device__ __forceinline__ int32_t quant_pack8_rcp(const float (&v)[8], float rcp,
-                                                   bool& near_tie) {
+// Same eight codes without a division per element.  qa = fl(v * rcp(sdiv) + 8) (one
+// fused rounding) differs from the exact q + 8, q = v / sdiv, by less than 1.5e-6 (|q| <= 7;
+// the hardware reciprocal is within an ulp, the fma rounds once at an ulp of at most
+// 2^-20), and rint(q + 8) == rint(q) + 8 (8 is even, so ties still go to even), so
+// rint(qa) - 8 == rint(q) unless q lies within 1.5e-6 of a half-integer.  Any lane that
+// sees qa within 1e-5 of one raises `near_tie`; the caller then redoes the row's codes
+// with quant_pack8 (exact division).  Both paths therefore produce the reference's
+// round-half-even codes bit for bit.
+__device__ __forceinline__ uint32_t quant_pack8_rcp(const float (&v)[8], float rcp, bool& near_tie) {
   uint32_t word = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float qa = v[e] * rcp;
+    const float qa = __builtin_fmaf(v[e], rcp, 8.0f);
     float r = __builtin_rintf(qa);
     near_tie |= fabsf(qa - r) > 0.49999f;
-    r = fminf(fmaxf(r, -7.0f), 7.0f);
-    word |= (static_cast<uint32_t>(static_cast<int>(r)) & 0xFu) << (4 * e);
+    r = fminf(fmaxf(r, 1.0f), 15.0f);
+    word |= static_cast<uint32_t>(r) << (4 * e);
   }
-  return static_cast<int32_t>(word);
+  return word ^ kObFlipHi;
 }
 
 // Rotation, quantization and stores of one row of K = 2^LOGK values held by T = 2^LOGT
@@ -192,7 +196,7 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
     for (int u = 0; u < RUN / 8; ++u) {
       float c8[8];
       gather8(g, u, c8);
-      words[g * (RUN / 8) + u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+      words[g * (RUN / 8) + u] = quant_pack8_rcp(c8, rcp, near_tie);
     }
   if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
 #pragma unroll
@@ -201,7 +205,7 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
       for (int u = 0; u < RUN / 8; ++u) {
         float c8[8];
         gather8(g, u, c8);
-        words[g * (RUN / 8) + u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+        words[g * (RUN / 8) + u] = quant_pack8(c8, sdiv);
       }
   }
 #pragma unroll
@@ -209,7 +213,7 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
 #pragma unroll
     for (int u = 0; u < RUN / 8; u += 2) {
       const int e0 = elem(PASSES - 1, t, g + (1 << LAST_W) * 8 * u);
-      const uint2 wd = make_uint2(words[g * (RUN / 8) + u] ^ kObFlipLo, words[g * (RUN / 8) + u + 1] ^ kObFlipLo);
+      const uint2 wd = make_uint2(words[g * (RUN / 8) + u], words[g * (RUN / 8) + u + 1]);
       *reinterpret_cast<uint2*>(&q[frag_word_index(row, e0 >> 3, kblocks128(K))]) = wd;
     }
   int s16 = 0;
@@ -362,7 +366,7 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
     float c8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-    words[u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+    words[u] = quant_pack8_rcp(c8, rcp, near_tie);
   }
   if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
 #pragma unroll
@@ -370,12 +374,12 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
       float c8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-      words[u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+      words[u] = quant_pack8(c8, sdiv);
     }
   }
 #pragma unroll
   for (int u = 0; u < R / 8; u += 2) {
-    const uint2 wd = make_uint2(words[u] ^ kObFlipLo, words[u + 1] ^ kObFlipLo);
+    const uint2 wd = make_uint2(words[u], words[u + 1]);
     *reinterpret_cast<uint2*>(&q[frag_word_index(row, (t * R) / 8 + u, kblocks128(K))]) = wd;
   }
   int s16 = 0;
@@ -455,7 +459,7 @@ __device__ __forceinline__ void fwht_quant_row_2wave(float (&v)[1 << (LOGK - 7)]
     float c8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-    words[u] = static_cast<uint32_t>(quant_pack8_rcp(c8, rcp, near_tie));
+    words[u] = quant_pack8_rcp(c8, rcp, near_tie);
   }
   if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
 #pragma unroll
@@ -463,13 +467,13 @@ __device__ __forceinline__ void fwht_quant_row_2wave(float (&v)[1 << (LOGK - 7)]
       float c8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-      words[u] = static_cast<uint32_t>(quant_pack8(c8, sdiv));
+      words[u] = quant_pack8(c8, sdiv);
     }
   }
   if (store) {
 #pragma unroll
     for (int u = 0; u < R / 8; u += 2) {
-      const uint2 wd = make_uint2(words[u] ^ kObFlipLo, words[u + 1] ^ kObFlipLo);
+      const uint2 wd = make_uint2(words[u], words[u + 1]);
       *reinterpret_cast<uint2*>(&q[frag_word_index(row, (t * R) / 8 + u, kblocks128(K))]) = wd;
     }
   }

@@ -92,6 +92,7 @@ __host__ __device__ inline int64_t frag_word_index(int64_t r, int32_t kw, int32_
 constexpr uint32_t kLoNib = 0x0F0F0F0Fu;
 constexpr uint32_t kHiNib = 0xF0F0F0F0u;
 constexpr uint32_t kObFlipLo = 0x08080808u;  // tc <-> ob on the low nibbles
+constexpr uint32_t kObFlipHi = 0x80808080u;  // tc <-> ob on the high nibbles
 
 // Words of activation codes for M rows (fragments of ceil(M/16) row blocks), followed by
 // qcorr for every row of those blocks.
