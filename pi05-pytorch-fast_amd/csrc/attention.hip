@@ -297,9 +297,9 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
 
   // Phase 3 streams V^T through a kVR-deep register ring; its first kVR steps are requested
   // during the softmax (spread over its first chunk loop, so that the waves do not stall
-  // on a full memory queue before their softmax work), and their latency hides under it.  Wave w reads the V^T fragments of
-  // dimensions 32*w .. 32*w + 31: operand A lane L: V^T[d 32*w + 16*db + L%16][keys
-  // 32*t + 8*(L/16) + 0..7].
+  // on a full memory queue before their softmax work), and their latency hides under it.
+  // Wave w reads the V^T fragments of dimensions 32*w .. 32*w + 31: operand A lane L:
+  // V^T[d 32*w + 16*db + L%16][keys 32*t + 8*(L/16) + 0..7].
   const int nst = s_pad / 32;
   const _Float16* vf = kf + static_cast<int64_t>(s_pad) * kD + (2 * w) * nst * 512;
   auto load_v = [&](int t, half8 (&va)[2]) {
