@@ -208,8 +208,10 @@ def counter_table(paths: list[str], match: str | None = None) -> str:
         name, wgs, wg = key
         med = {c: statistics.median(v) for c, v in cs.items()}
         n = len(cs["_dur_ns"])
-        out.append(f"### `{name}`  ({wgs} workgroups x {wg}; {n} dispatches; VGPR {med['_vgpr']:.0f}, "
-                   f"AGPR {med['_agpr']:.0f}, LDS {med['_lds']:.0f} B)")
+        # rocprofv3's VGPR_Count / Accum_VGPR_Count fields as recorded (its own granularity,
+        # not the kernel descriptor's register count)
+        out.append(f"### `{name}`  ({wgs} workgroups x {wg}; {n} dispatches; rocprofv3 VGPR_Count "
+                   f"{med['_vgpr']:.0f}, Accum_VGPR_Count {med['_agpr']:.0f}, LDS {med['_lds']:.0f} B)")
         out.append("")
         out.append("| counter | median per dispatch |")
         out.append("|---|---:|")
