@@ -46,21 +46,35 @@ __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
 // Corrections: the exact result's fp16 bit pattern minus the fast one's, for the inputs
 // where they differ (gelu_tanh_fix.inc, generated on the GPU from these two functions by
 // gelu_fix_gen.hip; the exhaustive test compares every fp16 input with torch).  They all
-// lie in the window |x| bits in [kGeluFixAbsBase, kGeluFixAbsBase + kGeluFixHalf - 1), and
-// the int8 table holds one half of kGeluFixHalf entries per sign, indexed by the |x| bits
-// minus the base; the last entry of each half is 0 and takes every input outside the
-// window (the index is clamped, and |x| bits below the base wrap to large values).
+// lie in the window |x| bits in [kGeluFixAbsBase, kGeluFixAbsBase + kGeluFixHalf - 1).
+// The int8 table is indexed by the fp16 bits minus the base, clamped: positive inputs of
+// the window land in [0, kGeluFixHalf - 1), negative ones in [kGeluFixNeg,
+// kGeluFixNeg + kGeluFixHalf - 1) (kGeluFixNeg = 0x8000, the sign bit), and every input
+// outside the window reads a zero entry: positive ones above it land in the zero run
+// [kGeluFixHalf - 1, kGeluFixNeg), negative ones below it too (their bits minus the base
+// lie in [0x8000 - base, 0x8000)), and the others wrap or run past the negative half and
+// are clamped to its last (zero) entry.  The index is two ALU instructions; the zero run
+// between the halves is filled, not copied, where the table is staged in LDS.
 constexpr uint32_t kGeluFixAbsBase = 0x2c00u;
 constexpr uint32_t kGeluFixHalf = 6656u;
-constexpr int kGeluFixEntries = 2 * kGeluFixHalf;  // 13 KB
+constexpr uint32_t kGeluFixNeg = 0x8000u;
+constexpr uint32_t kGeluFixLast = kGeluFixNeg + kGeluFixHalf - 1;  // zero entry
+constexpr int kGeluFixEntries = 39 * 1024;                          // > kGeluFixLast, 1 KB pieces
+static_assert(kGeluFixLast < static_cast<uint32_t>(kGeluFixEntries), "the clamp stays in the table");
 
-// Table slot of fp16 bit pattern xb (zero-extended): four ALU instructions.
+// Table slot of fp16 bit pattern xb (zero-extended).
 __host__ __device__ constexpr uint32_t gelu_fix_index(uint32_t xb) {
-  const uint32_t off = (xb & 0x7fffu) - kGeluFixAbsBase;
-  return (off < kGeluFixHalf - 1 ? off : kGeluFixHalf - 1) + (xb >> 15) * kGeluFixHalf;
+  const uint32_t off = xb - kGeluFixAbsBase;
+  return off < kGeluFixLast ? off : kGeluFixLast;
 }
 __host__ __device__ constexpr bool gelu_fix_in_window(uint32_t xb) {
   return ((xb & 0x7fffu) - kGeluFixAbsBase) < kGeluFixHalf - 1;
 }
+// The 1 KB pieces of the table that can hold nonzero entries: [0, kGeluFixPosPieces) and
+// [kGeluFixNeg / 1024, kGeluFixEntries / 1024); the pieces between are all zero.
+constexpr int kGeluFixPosPieces = (kGeluFixHalf + 1023) / 1024;
+constexpr int kGeluFixNegPiece0 = kGeluFixNeg / 1024;
+static_assert(kGeluFixNegPiece0 * 1024 + kGeluFixHalf <= static_cast<uint32_t>(kGeluFixEntries),
+              "the negative half fits the table");
 
 }  // namespace w4a4

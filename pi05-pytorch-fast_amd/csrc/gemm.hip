@@ -181,20 +181,41 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   const int nt = tile / p.mtiles;
   const int ks = blockIdx.y;
 
-  // GELU: the correction table goes to LDS for the epilogue's per-lane lookups, copied by
-  // direct global-to-LDS loads (no registers; lane L of a wave writes bytes 16L..16L+15 of
-  // the wave's 1 KB piece).  They complete under the main loop; a vmcnt(0) wait and the
-  // barrier ahead of the epilogue order them before the reads.
-  __shared__ __align__(16) int8_t fix_lds[GELU ? kGeluFixEntries : 16];
+  // GELU: the correction table goes to LDS for the epilogue's per-lane lookups.  Its two
+  // halves are copied by direct global-to-LDS loads (no registers; lane L of a wave writes
+  // bytes 16L..16L+15 of the wave's 1 KB piece).  Without a k fold (KW == 1) the table
+  // keeps its global layout, the zero run between the halves filled in place, so that a
+  // lookup is gelu_fix_index's two instructions; with a fold, whose LDS buffer leaves no
+  // room for 39 KB, the halves are packed back to back (kFixCompact) and the lookup adds
+  // the sign's half offset.  The copies complete under the main loop; a vmcnt(0) wait and
+  // the barrier ahead of the epilogue order them (and the fill) before the reads.
+  constexpr bool kFixWide = KW == 1;
+  constexpr int kFixPieces = kGeluFixPosPieces + (kGeluFixEntries / 1024 - kGeluFixNegPiece0);
+  constexpr int kFixCompact = kFixPieces * 1024;
+  __shared__ __align__(16) int8_t fix_lds[GELU ? (kFixWide ? kGeluFixEntries : kFixCompact) : 16];
   if constexpr (GELU) {
-    constexpr int kPieces = kGeluFixEntries / 1024;
     static_assert(kGeluFixEntries % 1024 == 0, "the table is copied in 1 KB pieces");
-    for (int piece = wave; piece < kPieces; piece += NWAVES) {
+    for (int c = wave; c < kFixPieces; c += NWAVES) {
+      const int piece = c < kGeluFixPosPieces ? c : kGeluFixNegPiece0 + (c - kGeluFixPosPieces);
       __builtin_amdgcn_global_load_lds(
           (const __attribute__((address_space(1))) void*)(kGeluFix.v + piece * 1024 + lane * 16),
-          (__attribute__((address_space(3))) void*)(fix_lds + piece * 1024), 16, 0, 0);
+          (__attribute__((address_space(3))) void*)(fix_lds + (kFixWide ? piece : c) * 1024), 16, 0, 0);
+    }
+    if constexpr (kFixWide) {
+      constexpr int kZero0 = kGeluFixPosPieces * 1024, kZero1 = kGeluFixNegPiece0 * 1024;
+      for (int i = kZero0 + tid * 16; i < kZero1; i += 64 * NWAVES * 16)
+        *reinterpret_cast<int4*>(fix_lds + i) = int4{0, 0, 0, 0};
     }
   }
+  // LDS slot of the correction of fp16 bits xb.
+  auto fix_slot = [](uint32_t xb) -> uint32_t {
+    if constexpr (kFixWide) {
+      return gelu_fix_index(xb);
+    } else {
+      const uint32_t off = (xb & 0x7fffu) - kGeluFixAbsBase;
+      return (off < kGeluFixHalf - 1 ? off : kGeluFixHalf - 1) + (xb >> 15) * (kGeluFixPosPieces * 1024);
+    }
+  };
 
   // Group selection with scalar selects (no dynamic indexing of the argument struct).
   const int32_t* W = p.g[0].w;
@@ -539,7 +560,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
           for (int r = 0; r < 4; ++r) {
             g16[r] = dequant(s[r], sv[mi], swv[r]);
             u16[r] = dequant(su[r], sv[mi], swu[r]);
-            fix[r] = fix_lds[gelu_fix_index(__builtin_bit_cast(uint16_t, g16[r]))];
+            fix[r] = fix_lds[fix_slot(__builtin_bit_cast(uint16_t, g16[r]))];
           }
           half4 gl;
 #pragma unroll
