@@ -22,23 +22,24 @@ __device__ __forceinline__ float gelu_tanh_exact(float x) {
   return y;
 }
 
-// fp16 bits of the fast evaluation: tanh(u) = 1 - 2 / (1 + 2^(2u log2 e)) from the
-// hardware exp2 and reciprocal, with 2u log2 e = x * (K0 + K1 x^2) (K0 = 2 log2(e)
-// sqrt(2/pi), K1 = K0 * 0.044715), and y = (0.5 x)(1 + tanh(u)) as in the exact
-// expression, so that the cancellation of 1 + tanh for negative x and the rounding of
-// 0.5 x for tiny x follow it.  Every operation is a single IEEE fp32 operation or one
-// hardware instruction, so the result is the same in every kernel that inlines this.  It
-// differs from the exact expression's fp16 result on a few hundred of the 65536 fp16
-// inputs, all with |x| in [2^-4, 5.3) (mostly negative x in [-5.2, -2], where 1 + tanh
-// cancels to a few ulps), by at most a few ulps: gelu_tanh_fix.inc lists them.
+// fp16 bits of the fast evaluation: y = x (1 - r), r = 1 / (1 + 2^q), from the hardware
+// exp2 and reciprocal, with q = 2u log2 e = x * (K0 + K1 x^2) (K0 = 2 log2(e) sqrt(2/pi),
+// K1 = K0 * 0.044715): (0.5 x)(1 + tanh(u)) = x (1 - 1 / (1 + e^(2u))).  Every operation is
+// a single IEEE fp32 operation or one hardware instruction, so the result is the same in
+// every kernel that inlines this.  It differs from the exact expression's fp16 result on
+// a few hundred of the 65536 fp16 inputs, all with |x| in [2^-4, 5.3) (mostly negative x
+// in [-5.2, -2], where 1 - r cancels to a few ulps), by at most a few ulps:
+// gelu_tanh_fix.inc lists them.  (The earlier form (0.5 x)(1 + (1 - 2r)), two more
+// instructions, gives the same fp16 bits on every input: the generator's correction
+// lists for the two are identical.)
 constexpr float kGeluK0 = 2.3022081983184814f;   // 2 log2(e) sqrt(2/pi)
 constexpr float kGeluK1 = 0.10294324159622192f;  // K0 * 0.044715
 __device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
 #pragma clang fp contract(off)
   const float q = x * __builtin_fmaf(x * x, kGeluK1, kGeluK0);  // 2 log2(e) * inner
   const float e = __builtin_amdgcn_exp2f(q);                     // exp(2 inner)
-  const float t = __builtin_fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + e), 1.0f);
-  float y = (0.5f * x) * (1.0f + t);
+  const float r = __builtin_amdgcn_rcpf(1.0f + e);
+  float y = x * (1.0f - r);
   asm volatile("" : "+v"(y));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(y));
 }
