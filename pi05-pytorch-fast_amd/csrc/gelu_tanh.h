@@ -24,23 +24,30 @@ __device__ __forceinline__ float gelu_tanh_exact(float x) {
 
 // fp16 bits of the fast evaluation: y = x (1 - r), r = 1 / (1 + 2^q), from the hardware
 // exp2 and reciprocal, with q = 2u log2 e = x * (K0 + K1 x^2) (K0 = 2 log2(e) sqrt(2/pi),
-// K1 = K0 * 0.044715): (0.5 x)(1 + tanh(u)) = x (1 - 1 / (1 + e^(2u))).  Every operation is
-// a single IEEE fp32 operation or one hardware instruction, so the result is the same in
-// every kernel that inlines this.  It differs from the exact expression's fp16 result on
-// a few hundred of the 65536 fp16 inputs, all with |x| in [2^-4, 5.3) (mostly negative x
-// in [-5.2, -2], where 1 - r cancels to a few ulps), by at most a few ulps:
-// gelu_tanh_fix.inc lists them.  (The earlier form (0.5 x)(1 + (1 - 2r)), two more
-// instructions, gives the same fp16 bits on every input: the generator's correction
-// lists for the two are identical.)
+// K1 = K0 * 0.044715): (0.5 x)(1 + tanh(u)) = x (1 - 1 / (1 + e^(2u))).  The products with
+// x read the fp16 input directly (v_fma_mix), so x is never converted to fp32:
+//   s = x * x + 0           exact (an fp16 square fits fp32 and is never -0),
+//   q = x * (K0 + K1 s) + 0 the sign of a zero product is lost, and 2^(+-0) = 1 either way,
+//   y = x * (1 - r) - 0     one fp32 rounding, as a plain fp32 multiply; the -0 addend
+//                           keeps the sign of a zero product (gelu(-0) = -0),
+// then y is rounded to fp16.  Every step is a single IEEE fp32 operation or one hardware
+// instruction, so the result is the same in every kernel that inlines this.  It differs
+// from the exact expression's fp16 result on a few hundred of the 65536 fp16 inputs, all
+// with |x| in [2^-4, 5.3) (mostly negative x in [-5.2, -2], where 1 - r cancels to a few
+// ulps), by at most a few ulps: gelu_tanh_fix.inc lists them.  (The form with y = x r and
+// r = 1 / (1 + 2^-q), one instruction fewer, is closer to the exact values but gives 2^-24
+// for the input 2^-24, whose exact result is a tie rounded to 0, outside the table.)
 constexpr float kGeluK0 = 2.3022081983184814f;   // 2 log2(e) sqrt(2/pi)
 constexpr float kGeluK1 = 0.10294324159622192f;  // K0 * 0.044715
-__device__ __forceinline__ uint16_t gelu_tanh_fast_bits(float x) {
+__device__ __forceinline__ uint16_t gelu_tanh_fast_bits(_Float16 xh) {
 #pragma clang fp contract(off)
-  const float q = x * __builtin_fmaf(x * x, kGeluK1, kGeluK0);  // 2 log2(e) * inner
-  const float e = __builtin_amdgcn_exp2f(q);                     // exp(2 inner)
-  const float r = __builtin_amdgcn_rcpf(1.0f + e);
-  float y = x * (1.0f - r);
-  asm volatile("" : "+v"(y));
+  const float x = static_cast<float>(xh);
+  const float s = __builtin_fmaf(x, x, 0.0f);
+  const float q = __builtin_fmaf(x, __builtin_fmaf(s, kGeluK1, kGeluK0), 0.0f);
+  const float c = 1.0f - __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(q));
+  // fma(x, c, -0.0f) would be folded into a multiply that converts x to fp32 first.
+  float y;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(y) : "v"(xh), "v"(c), "s"(-0.0f));
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(y));
 }
 

@@ -109,7 +109,7 @@ static_assert(gelu_fixes_in_window(), "every GELU correction lies in the table w
 __device__ __forceinline__ _Float16 gelu_tanh_f16(_Float16 xh, const int8_t* fix) {
   const uint32_t xb = __builtin_bit_cast(uint16_t, xh);
   const int d = fix[gelu_fix_index(xb)];
-  const uint32_t fb = gelu_tanh_fast_bits(static_cast<float>(xh));
+  const uint32_t fb = gelu_tanh_fast_bits(xh);
   return __builtin_bit_cast(_Float16, static_cast<uint16_t>(fb + d));
 }
 
@@ -565,7 +565,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
           half4 gl;
 #pragma unroll
           for (int r = 0; r < 4; ++r)
-            gl[r] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(gelu_tanh_fast_bits(static_cast<float>(g16[r])) + fix[r]));
+            gl[r] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(gelu_tanh_fast_bits(g16[r]) + fix[r]));
           o = gl * u16;
         } else {
 #pragma unroll
