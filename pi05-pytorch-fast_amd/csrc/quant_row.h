@@ -12,22 +12,71 @@ namespace {
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
+constexpr int kDppXor1 = 0xB1;       // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;       // quad_perm [2,3,0,1]
+constexpr int kDppRev4 = 0x1B;       // quad_perm [3,2,1,0]: lane i^3 within the quad
+constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i^7 within 8
+constexpr int kDppRor8 = 0x128;      // row_ror:8: lane i^8 within the 16-lane row
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+// x of lane (this lane ^ (1 << K)), K = 0..3.
+template <int K>
+__device__ __forceinline__ float lane_xor_f(float x) {
+  if constexpr (K == 0) return dpp_f<kDppXor1>(x);
+  else if constexpr (K == 1) return dpp_f<kDppXor2>(x);
+  else if constexpr (K == 2) return dpp_f<kDppHalfMirror>(dpp_f<kDppRev4>(x));
+  else return dpp_f<kDppRor8>(x);
+}
+template <int K>
+__device__ __forceinline__ int lane_xor_i(int x) {
+  if constexpr (K == 0) return dpp_i<kDppXor1>(x);
+  else if constexpr (K == 1) return dpp_i<kDppXor2>(x);
+  else if constexpr (K == 2) return dpp_i<kDppHalfMirror>(dpp_i<kDppRev4>(x));
+  else return dpp_i<kDppRor8>(x);
+}
+// Max / sum over the 64 lanes, the result in every lane.
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, lane_xor_f<0>(v));
+  v = fmaxf(v, lane_xor_f<1>(v));
+  v = fmaxf(v, lane_xor_f<2>(v));
+  v = fmaxf(v, lane_xor_f<3>(v));
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += lane_xor_i<0>(v);
+  v += lane_xor_i<1>(v);
+  v += lane_xor_i<2>(v);
+  v += lane_xor_i<3>(v);
+  auto r16 = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  v = static_cast<int>(r16[0]) + static_cast<int>(r16[1]);
+  auto r32 = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
+  return static_cast<int>(r32[0]) + static_cast<int>(r32[1]);
+}
+// The same reductions under the names the quantizers use.  Max and integer sums do not
+// depend on the order.  The fp32 sum keeps the xor butterfly 32, 16, 8, 4, 2, 1 (each
+// step v + partner, and fp32 addition is commutative), so it equals the LDS-permute
+// loop v += shfl_xor(v, o) for o = 32 .. 1 bit for bit, without its six LDS round trips.
+__device__ __forceinline__ float wave_max(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ int wave_sum(int v) { return wave_sum_dpp(v); }
 __device__ __forceinline__ float wave_sum_f(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-__device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __fadd_rn(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __fadd_rn(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  v = __fadd_rn(v, lane_xor_f<3>(v));
+  v = __fadd_rn(v, lane_xor_f<2>(v));
+  v = __fadd_rn(v, lane_xor_f<1>(v));
+  return __fadd_rn(v, lane_xor_f<0>(v));
 }
 
 // 16 * (sum of the four codes in the high nibbles of w, the odd-k codes): a signed dot
@@ -238,56 +287,6 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
 //                             exchange that register bit with the lane bit, the stage runs
 //                             in registers, and the swaps are undone afterwards.
 // No LDS and no barrier; the wave max and sum use the same DPP / swap exchanges.
-constexpr int kDppXor1 = 0xB1;       // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4E;       // quad_perm [2,3,0,1]
-constexpr int kDppRev4 = 0x1B;       // quad_perm [3,2,1,0]: lane i^3 within the quad
-constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i^7 within 8
-constexpr int kDppRor8 = 0x128;      // row_ror:8: lane i^8 within the 16-lane row
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
-}
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int x) {
-  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
-}
-// x of lane (this lane ^ (1 << K)), K = 0..3.
-template <int K>
-__device__ __forceinline__ float lane_xor_f(float x) {
-  if constexpr (K == 0) return dpp_f<kDppXor1>(x);
-  else if constexpr (K == 1) return dpp_f<kDppXor2>(x);
-  else if constexpr (K == 2) return dpp_f<kDppHalfMirror>(dpp_f<kDppRev4>(x));
-  else return dpp_f<kDppRor8>(x);
-}
-template <int K>
-__device__ __forceinline__ int lane_xor_i(int x) {
-  if constexpr (K == 0) return dpp_i<kDppXor1>(x);
-  else if constexpr (K == 1) return dpp_i<kDppXor2>(x);
-  else if constexpr (K == 2) return dpp_i<kDppHalfMirror>(dpp_i<kDppRev4>(x));
-  else return dpp_i<kDppRor8>(x);
-}
-// Max / sum over the 64 lanes, the result in every lane.
-__device__ __forceinline__ float wave_max_dpp(float v) {
-  v = fmaxf(v, lane_xor_f<0>(v));
-  v = fmaxf(v, lane_xor_f<1>(v));
-  v = fmaxf(v, lane_xor_f<2>(v));
-  v = fmaxf(v, lane_xor_f<3>(v));
-  auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-  auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-}
-__device__ __forceinline__ int wave_sum_dpp(int v) {
-  v += lane_xor_i<0>(v);
-  v += lane_xor_i<1>(v);
-  v += lane_xor_i<2>(v);
-  v += lane_xor_i<3>(v);
-  auto r16 = __builtin_amdgcn_permlane16_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-  v = static_cast<int>(r16[0]) + static_cast<int>(r16[1]);
-  auto r32 = __builtin_amdgcn_permlane32_swap(static_cast<unsigned>(v), static_cast<unsigned>(v), false, false);
-  return static_cast<int>(r32[0]) + static_cast<int>(r32[1]);
-}
 // Register pairs (v[j], v[j | 2^B]) exchange register bit B with lane bit 4 (SW = 16) or
 // lane bit 5 (SW = 32); applying it twice restores the layout.
 template <int SW, int B, int R>
