@@ -340,8 +340,11 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
     float m = static_cast<float>(mx[0]);
 #pragma unroll
     for (int i = 1; i < 8; ++i) m = fmaxf(m, static_cast<float>(mx[i]));
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    // Row max and sum over the 16 lanes of a row (lane xor 1, 2, 4, 8) through DPP.
+    m = fmaxf(m, lane_xor_f<0>(m));
+    m = fmaxf(m, lane_xor_f<1>(m));
+    m = fmaxf(m, lane_xor_f<2>(m));
+    m = fmaxf(m, lane_xor_f<3>(m));
     constexpr float kLog2e = 1.4426950408889634f;
     const float ml = m * kLog2e;
     float e[SCH][8];
@@ -356,8 +359,10 @@ __global__ __launch_bounds__(kThreads) void prefix_attention_kernel(const AttnPa
         }
       }
     }
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) l += __shfl_xor(l, o, 64);
+    l += lane_xor_f<0>(l);
+    l += lane_xor_f<1>(l);
+    l += lane_xor_f<2>(l);
+    l += lane_xor_f<3>(l);
     const float rl = 1.0f / l;
 #pragma unroll
     for (int ch = 0; ch < SCH; ++ch) {
