@@ -159,6 +159,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
+  // One column block split over 8 k parts (the long-K tiles): the k parts are summed by a
+  // reduce-scatter instead of a fold into one wave, and wave w then finishes row block
+  // mi = w of the tile, so that seven waves share the epilogue.
+  constexpr bool kSpread = KW == 8 && NW == 1 && MI <= KW;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -462,11 +466,12 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   uint4 resv[GELU ? 1 : MI][GELU ? 1 : RJ];
   const bool has_res = !GELU && p.res != nullptr && p.mode == kEpiFp16;
   if constexpr (!GELU) {
-    if (has_res && wk == 0) {
+    if (has_res && (kSpread || wk == 0)) {
 #pragma unroll
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int j = 0; j < RJ; ++j) {
+          if (kSpread && mi != wk) continue;
           const int rr = min(j * RRPI + lane / RLPR, 15);
           const int64_t row = min(m0 + mi * 16 + rr, M - 1);
           const int col = min(wcol + (lane % RLPR) * 8, N - 8);
@@ -475,9 +480,39 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     }
   }
 
-  // ---- k-part reduction through LDS (KW > 1): pairs of k parts are folded until part 0
-  // of every column block holds the full sum; the other waves are done after that.
-  if constexpr (KW > 1) {
+  // ---- k-part reduction through LDS (KW > 1).  Spread tiles: in phases of PM row blocks,
+  // every wave stores its parts of the phase's row blocks and the owner of each row block
+  // (wave mi) sums the KW parts of its fragments (int32: any order gives the same sum).
+  // Otherwise pairs of k parts are folded until part 0 of every column block holds the
+  // full sum; the other waves are done after that.
+  if constexpr (kSpread) {
+    constexpr int PM = (MI + 1) / 2;
+    __shared__ __align__(16) v4i red[KW * PM * NI * 64];
+#pragma unroll
+    for (int ph = 0; ph * PM < MI; ++ph) {
+#pragma unroll
+      for (int i = 0; i < PM; ++i) {
+        if (ph * PM + i >= MI) continue;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) red[((wk * PM + i) * NI + ni) * 64 + lane] = acc[ph * PM + i][ni];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < PM; ++i) {
+        const int mi = ph * PM + i;
+        if (mi >= MI || mi != wk) continue;
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          v4i sum = red[(i * NI + ni) * 64 + lane];
+#pragma unroll
+          for (int w = 1; w < KW; ++w) sum += red[((w * PM + i) * NI + ni) * 64 + lane];
+          acc[mi][ni] = sum;
+        }
+      }
+      if ((ph + 1) * PM < MI) __syncthreads();
+    }
+    if (wk >= MI) return;
+  } else if constexpr (KW > 1) {
     constexpr int FR = MI * NI * 64;  // v4i per wave
     __shared__ __align__(16) v4i red[(KW / 2) * NW * FR];
     auto put = [&](int slot) {
@@ -528,8 +563,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     constexpr int LPR = OCW / 8;                  // lanes per row, 16 bytes each
     constexpr int RPI = 64 / LPR;                 // rows per store instruction
     static_assert(16 % RPI == 0 || RPI % 16 == 0, "store rows must tile the 16-row block");
-    __shared__ __align__(16) _Float16 stage_all[NW * 16 * LSR];
-    _Float16* stage = stage_all + wn * (16 * LSR);
+    __shared__ __align__(16) _Float16 stage_all[(kSpread ? KW : NW) * 16 * LSR];
+    _Float16* stage = stage_all + (kSpread ? wk : wn) * (16 * LSR);
     // Stores address the wave's output block through a scalar base and a 32-bit lane
     // offset (the block spans at most 16*MI rows of N columns).
     char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
@@ -540,6 +575,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     const bool vtr = QKV_PREP && p.vt_group == gsel + 1;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
+      if (kSpread && mi != wk) continue;  // another wave's row block
       half4 ob[GELU ? 1 : NI];
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
@@ -662,7 +698,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       __builtin_amdgcn_wave_barrier();
     }
     if constexpr (!GELU) {
-      if (rope || vtr) {
+      if ((rope || vtr) && (!kSpread || wk == 0)) {
         // Keys seq .. s_pad - 1 of every batch whose last token lies in this tile: zeros.
         const int npad = p.s_pad - p.seq;
         const int64_t mend = min(m0 + 16 * MI, M);
@@ -706,7 +742,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const int64_t row = m0 + mi * 16 + lrow;
-      if (row >= M) continue;
+      if ((kSpread && mi != wk) || row >= M) continue;
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
         if (!bvalid[ni]) continue;

@@ -254,14 +254,17 @@ def test_int4_gemm2_gate_up(ext, cuda, m):
 
 
 # Tile configurations of the fused epilogue: 4x2 (M = 776 and 64 at N = 2048), 2x2 (17),
-# 1x2 with the k fold (16, 1) and 7x4 with the k fold (200 x 16384); the folding ones stage
-# the GELU correction table compactly, the others in its global layout.
-@pytest.mark.parametrize("m,n", [(776, 2048), (64, 2048), (17, 2048), (16, 2048), (1, 2048), (200, 16384)])
-def test_int4_gemm2_gelu_matches_unfused(ext, cuda, m, n):
+# 1x2 with the k fold (16, 1), 7x4 with the k fold (200 x 16384) and 7x4 with eight k parts
+# summed by the reduce-scatter, each wave finishing one row block (200 x 2048, K = 8192);
+# the folding ones stage the GELU correction table compactly, the others in its global
+# layout.
+@pytest.mark.parametrize("m,n,k", [(776, 2048, 2048), (64, 2048, 2048), (17, 2048, 2048), (16, 2048, 2048),
+                                   (1, 2048, 2048), (200, 16384, 2048), (200, 2048, 8192)])
+def test_int4_gemm2_gelu_matches_unfused(ext, cuda, m, n, k):
     gen = inp.generator(300 + m)
-    x = inp.activations(gen, m, 2048).to(cuda)
-    wg = ext.repack_weight(inp.packed_weight(gen, n, 2048).to(cuda))
-    wu = ext.repack_weight(inp.packed_weight(gen, n, 2048).to(cuda))
+    x = inp.activations(gen, m, k).to(cuda)
+    wg = ext.repack_weight(inp.packed_weight(gen, n, k).to(cuda))
+    wu = ext.repack_weight(inp.packed_weight(gen, n, k).to(cuda))
     h = ext.int4_gemm2_gelu(x, wg, wu)
     g, u = ext.int4_gemm2(x, wg, wu)
     h_eager = torch.nn.functional.gelu(g, approximate="tanh") * u
