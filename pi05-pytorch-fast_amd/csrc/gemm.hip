@@ -20,8 +20,9 @@
 // Tiling.  A wave owns a (16*MI) x (16*NI) tile = MI x NI accumulators of 16x16.  The
 // NWAVES waves of a workgroup are arranged NW along N times KW along K: with KW > 1 the
 // waves of one column block split the workgroup's k range into KW contiguous parts and
-// fold their accumulators together through LDS at the end, which gives narrow GEMMs
-// (QKV, o, down) enough waves without a global split-K workspace.
+// sum their accumulators through LDS at the end (a reduce-scatter, after which each wave
+// finishes its share of the row blocks), which gives narrow GEMMs (QKV, o, down) enough
+// waves without a global split-K workspace.
 // Both operands live in HBM in the same MFMA-fragment-major layout (frag_word_index: one
 // 1 KB fragment per 16 rows/columns x 128 k; lane L loads slot L = 32 codes of row/
 // column L%16, the operands of the block's two MFMAs), so every operand fetch is one
@@ -159,10 +160,11 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
-  // One column block split over 8 k parts (the long-K tiles): the k parts are summed by a
-  // reduce-scatter instead of a fold into one wave, and wave w then finishes row block
-  // mi = w of the tile, so that seven waves share the epilogue.
-  constexpr bool kSpread = KW == 8 && NW == 1 && MI <= KW;
+  // K split over the waves (one column block, KW k parts): the k parts are summed by a
+  // reduce-scatter, after which wave w finishes the row blocks mi = w (mod KW), so that the
+  // waves share the epilogue.
+  static_assert(KW == 1 || NW == 1, "a K split covers one column block");
+  constexpr bool kSpread = KW > 1;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -187,10 +189,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 
   // GELU: the correction table goes to LDS for the epilogue's per-lane lookups.  Its two
   // halves are copied by direct global-to-LDS loads (no registers; lane L of a wave writes
-  // bytes 16L..16L+15 of the wave's 1 KB piece).  Without a k fold (KW == 1) the table
+  // bytes 16L..16L+15 of the wave's 1 KB piece).  Without a k split (KW == 1) the table
   // keeps its global layout, the zero run between the halves filled in place, so that a
-  // lookup is gelu_fix_index's two instructions; with a fold, whose LDS buffer leaves no
-  // room for 39 KB, the halves are packed back to back (kFixCompact) and the lookup adds
+  // lookup is gelu_fix_index's two instructions; with one, whose reduction buffer leaves
+  // no room for 39 KB in the 8-part tiles, the halves are packed back to back (kFixCompact) and the lookup adds
   // the sign's half offset.  The copies complete under the main loop; a vmcnt(0) wait and
   // the barrier ahead of the epilogue order them (and the fill) before the reads.
   constexpr bool kFixWide = KW == 1;
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   }
 
   // A wave without k blocks never waited for its correction-table loads (see the first
-  // step above): it waits now, before the barrier below (or the k fold's) publishes the
+  // step above): it waits now, before the barrier below (or the k reduction's) publishes the
   // table to the other waves.
   if constexpr (GELU) {
     if (nkb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -453,11 +455,11 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   __shared__ __align__(16) float epi_sw[NCOL];   // column scales of the tile
   if (tid < TROWS) epi_sa[tid] = e_sa * 0.0625f;
   if (tid < NCOL) epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
-  if constexpr (KW == 1) __syncthreads();  // KW > 1: the fold below synchronises
+  if constexpr (KW == 1) __syncthreads();  // KW > 1: the k reduction below synchronises
 
   // Residual (fp16 mode, one group): the 16-byte row pieces this wave's epilogue stores
   // (see the store loop below) are loaded now, so that their latency hides under the k
-  // fold and the staging instead of stalling every store.  Addresses are clamped into the
+  // reduction and the staging instead of stalling every store.  Addresses are clamped into the
   // matrix; pieces outside it are never stored.
   constexpr int ROCW = 16 * NI;
   constexpr int RLPR = ROCW / 8;
@@ -471,7 +473,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int j = 0; j < RJ; ++j) {
-          if (kSpread && mi != wk) continue;
+          if (kSpread && mi % KW != wk) continue;
           const int rr = min(j * RRPI + lane / RLPR, 15);
           const int64_t row = min(m0 + mi * 16 + rr, M - 1);
           const int col = min(wcol + (lane % RLPR) * 8, N - 8);
@@ -480,13 +482,14 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     }
   }
 
-  // ---- k-part reduction through LDS (KW > 1).  Spread tiles: in phases of PM row blocks,
-  // every wave stores its parts of the phase's row blocks and the owner of each row block
-  // (wave mi) sums the KW parts of its fragments (int32: any order gives the same sum).
-  // Otherwise pairs of k parts are folded until part 0 of every column block holds the
-  // full sum; the other waves are done after that.
+  // ---- k-part reduction through LDS (KW > 1): in phases of PM row blocks, every wave
+  // stores its parts of the phase's row blocks and the owner of each row block (wave
+  // mi mod KW) sums the KW parts of its fragments (int32: any order gives the same sum).
   if constexpr (kSpread) {
-    constexpr int PM = (MI + 1) / 2;
+    // Row blocks per phase: the 8-part tiles (one workgroup per CU) take half the tile at
+    // a time; the 4-part ones keep the buffer at 32 KB (two workgroups per CU).
+    constexpr int PM0 = KW == 8 ? (MI + 1) / 2 : (32 / (KW * NI) > 0 ? 32 / (KW * NI) : 1);
+    constexpr int PM = PM0 < MI ? PM0 : MI;
     __shared__ __align__(16) v4i red[KW * PM * NI * 64];
 #pragma unroll
     for (int ph = 0; ph * PM < MI; ++ph) {
@@ -500,7 +503,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
       for (int i = 0; i < PM; ++i) {
         const int mi = ph * PM + i;
-        if (mi >= MI || mi != wk) continue;
+        if (mi >= MI || mi % KW != wk) continue;
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           v4i sum = red[(i * NI + ni) * 64 + lane];
@@ -511,31 +514,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       }
       if ((ph + 1) * PM < MI) __syncthreads();
     }
-    if (wk >= MI) return;
-  } else if constexpr (KW > 1) {
-    constexpr int FR = MI * NI * 64;  // v4i per wave
-    __shared__ __align__(16) v4i red[(KW / 2) * NW * FR];
-    auto put = [&](int slot) {
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) red[(slot * NW + wn) * FR + (mi * NI + ni) * 64 + lane] = acc[mi][ni];
-    };
-    auto add = [&](int slot) {
-#pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] += red[(slot * NW + wn) * FR + (mi * NI + ni) * 64 + lane];
-    };
-#pragma unroll
-    for (int active = KW; active > 1; active /= 2) {
-      const int half = active / 2;
-      if (wk >= half && wk < active) put(wk - half);
-      __syncthreads();
-      if (wk < half) add(wk);
-      __syncthreads();
-    }
-    if (wk != 0) return;
+    if (wk >= MI) return;  // no row block to finish
   }
 
   // ---- epilogue.  Lane L holds rows 16*mi + L%16 and columns 16*ni + 4*(L/16) + 0..3.
@@ -575,7 +554,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     const bool vtr = QKV_PREP && p.vt_group == gsel + 1;
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
-      if (kSpread && mi != wk) continue;  // another wave's row block
+      if (kSpread && mi % KW != wk) continue;  // another wave's row block
       half4 ob[GELU ? 1 : NI];
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
@@ -742,7 +721,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi) {
       const int64_t row = m0 + mi * 16 + lrow;
-      if ((kSpread && mi != wk) || row >= M) continue;
+      if ((kSpread && mi % KW != wk) || row >= M) continue;
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
         if (!bvalid[ni]) continue;
