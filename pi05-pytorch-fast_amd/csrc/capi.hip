@@ -97,7 +97,7 @@ struct Plan {
 //      9.3 us, against 10.1 and 12.0 with 4 waves splitting K of 112 x 64 tiles, and 9.0
 //      and 10.1 with 64 x 128 tiles), else 64 x 128 tiles, else the K split.
 //  * M <= 64 (weight streaming): 16-, 32- or 64-row tiles of 32 columns whose four waves
-//    split K and fold their sums through LDS, so that one launch streams the weights
+//    split K and sum their parts through LDS, so that one launch streams the weights
 //    (QKV at M = 1: 3.0 us, against 5.8 us for 16 x 128 tiles with a global K split and
 //    its reduce launch).  A global split stays for long K (down), with at least 4 k blocks
 //    per wave.  The paired gate/up GELU GEMM uses them up to M = 16 only, and 4-waves-
