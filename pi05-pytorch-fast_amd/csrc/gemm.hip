@@ -192,9 +192,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // bytes 16L..16L+15 of the wave's 1 KB piece).  Without a k split (KW == 1) the table
   // keeps its global layout, the zero run between the halves filled in place, so that a
   // lookup is gelu_fix_index's two instructions; with one, whose reduction buffer leaves
-  // no room for 39 KB in the 8-part tiles, the halves are packed back to back (kFixCompact) and the lookup adds
-  // the sign's half offset.  The copies complete under the main loop; a vmcnt(0) wait and
-  // the barrier ahead of the epilogue order them (and the fill) before the reads.
+  // no room for 39 KB in the 8-part tiles, the halves are packed back to back
+  // (kFixCompact) and the lookup adds the sign's half offset.  The copies complete under
+  // the main loop; a vmcnt(0) wait and the barrier ahead of the epilogue order them (and
+  // the fill) before the reads.
   constexpr bool kFixWide = KW == 1;
   constexpr int kFixPieces = kGeluFixPosPieces + (kGeluFixEntries / 1024 - kGeluFixNegPiece0);
   constexpr int kFixCompact = kFixPieces * 1024;
@@ -445,8 +446,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   }
 
   // A wave without k blocks never waited for its correction-table loads (see the first
-  // step above): it waits now, before the barrier below (or the k reduction's) publishes the
-  // table to the other waves.
+  // step above): it waits now, before the barrier below (or the k reduction's) publishes
+  // the table to the other waves.
   if constexpr (GELU) {
     if (nkb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
@@ -459,8 +460,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 
   // Residual (fp16 mode, one group): the 16-byte row pieces this wave's epilogue stores
   // (see the store loop below) are loaded now, so that their latency hides under the k
-  // reduction and the staging instead of stalling every store.  Addresses are clamped into the
-  // matrix; pieces outside it are never stored.
+  // reduction and the staging instead of stalling every store.  Addresses are clamped into
+  // the matrix; pieces outside it are never stored.
   constexpr int ROCW = 16 * NI;
   constexpr int RLPR = ROCW / 8;
   constexpr int RRPI = 64 / RLPR;
