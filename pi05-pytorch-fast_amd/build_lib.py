@@ -63,7 +63,10 @@ def build(arch: str = "gfx950", verbose: bool = False) -> Path:
     ] + shlex.split(os.environ.get("PI05_W4A4_EXTRA_CFLAGS", ""))
     with tempfile.TemporaryDirectory(prefix="pi05w4a4_build_") as work:
         objs = [str(Path(work) / (Path(src).stem + ".o")) for src in SOURCES]
-        cmds = [[hipcc()] + common + UNIT_FLAGS.get(src, []) + ["-c", str(CSRC / src), "-o", obj]
+        # An explicit compilation-unit ID per unit (the default one hashes the command line,
+        # which names the temporary object) keeps the library byte-identical between builds.
+        cmds = [[hipcc()] + common + UNIT_FLAGS.get(src, [])
+                + [f"-cuid=pi05w4a4_{Path(src).stem}", "-c", str(CSRC / src), "-o", obj]
                 for src, obj in zip(SOURCES, objs)]
         workers = max(1, min(len(cmds), os.cpu_count() or 1))
         with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
