@@ -1,7 +1,7 @@
 """GPU parity of the gfx950 W4A4 path against the CPU oracle (through the C ABI).
 
 Bar: activation codes, scales, int32 accumulators and fp16 outputs bit-identical to the
-oracle (which is itself pinned to the reference's golden vectors).  The north-star
+oracle (which is itself pinned to the reference's golden vectors).  The path's looser
 tolerances (codes +-1 on <= 0.01% of elements, fp16 rel-L2 <= 1e-2) are reported by the
 assertion messages, but the tests require exact equality.
 """
