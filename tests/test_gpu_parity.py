@@ -179,6 +179,9 @@ GEMM_SHAPES = [
     (48, 2048, 4096),
     (1, 2048, 16384),
     (64, 2048, 16384),
+    # 112 x 64 tiles with four k parts (neither narrow tile fits two per CU): the k parts'
+    # reduce-scatter leaves two row blocks to three of the waves and one to the fourth
+    (2200, 2048, 2048),
 ]
 
 
