@@ -184,7 +184,18 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     tile = x * q + min(x, r) + (tile >> 3);
   }
   const int mt = tile % p.mtiles;
-  const int nt = tile / p.mtiles;
+  int nt = tile / p.mtiles;
+  if constexpr (QKV_PREP) {
+    // The K and V n-tiles (the groups after Q) carry the attention prep and so the longer
+    // epilogue; they are spread evenly through the n order (one in every s positions), so
+    // that no XCD's contiguous run of tiles is made of them only.  A bijection on the
+    // n-tiles whenever their count divides the total.
+    const int light = p.g[1].tile_begin, heavy = p.ntiles - light;
+    if (p.rope_group > 0 && heavy > 0 && p.ntiles % heavy == 0) {
+      const int s = p.ntiles / heavy, pos = nt;
+      nt = (pos % s == s / 2) ? light + pos / s : pos - pos / s - (pos % s > s / 2 ? 1 : 0);
+    }
+  }
   const int ks = blockIdx.y;
 
   // GELU: the correction table goes to LDS for the epilogue's per-lane lookups.  Its two
