@@ -257,12 +257,14 @@ def test_int4_gemm2_gate_up(ext, cuda, m):
 
 
 # Tile configurations of the fused epilogue: 4x2 (M = 776 and 64 at N = 2048), 2x2 (17),
-# 1x2 with the k fold (16, 1), 7x4 with the k fold (200 x 16384) and 7x4 with eight k parts
-# summed by the reduce-scatter, each wave finishing one row block (200 x 2048, K = 8192);
-# the folding ones stage the GELU correction table compactly, the others in its global
-# layout.
+# 1x2 with four k parts (16, 1), 7x4 with four k parts (200 and 113 x 16384: the second row
+# tile of 113 rows holds one row), 7x4 with eight k parts, each wave finishing one row block
+# (200 x 2048, K = 8192), and 7x4 over 1024 tiles whose last row tile holds one row
+# (785 x 16384); the K-split ones stage the GELU correction table compactly, the others in
+# its global layout.
 @pytest.mark.parametrize("m,n,k", [(776, 2048, 2048), (64, 2048, 2048), (17, 2048, 2048), (16, 2048, 2048),
-                                   (1, 2048, 2048), (200, 16384, 2048), (200, 2048, 8192)])
+                                   (1, 2048, 2048), (200, 16384, 2048), (113, 16384, 2048), (200, 2048, 8192),
+                                   (785, 16384, 2048)])
 def test_int4_gemm2_gelu_matches_unfused(ext, cuda, m, n, k):
     gen = inp.generator(300 + m)
     x = inp.activations(gen, m, k).to(cuda)
