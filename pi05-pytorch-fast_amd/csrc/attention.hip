@@ -484,8 +484,9 @@ hipError_t launch_prefix_attention(const AttnParams& p_in, hipStream_t stream) {
   AttnParams p = p_in;
   const int64_t rows = static_cast<int64_t>(p.s) * (p.h / p.kvh);
   p.row_blocks = static_cast<int32_t>((rows + kRows - 1) / kRows);
-  // Cache warming uses the CUs that the attention leaves idle (one workgroup per CU fits
-  // by LDS): none when the attention alone fills the device's CUs.
+  // Cache warming uses the CUs that the attention leaves idle (one workgroup of 8 waves
+  // per CU: at ~200 VGPRs a SIMD holds two of its waves, while its ~71 KB of LDS would
+  // allow two workgroups): none when the attention alone fills the device's CUs.
   const int64_t kCUs = device_cu_count();
   const int64_t attn_wgs = static_cast<int64_t>(p.row_blocks) * p.kvh * p.b;
   const int64_t warm_x = (p.warm.nbuf > 0 && attn_wgs < kCUs) ? (kCUs - attn_wgs) / (static_cast<int64_t>(p.kvh) * p.b) : 0;
