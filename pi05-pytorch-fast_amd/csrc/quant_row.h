@@ -116,20 +116,25 @@ __device__ __forceinline__ uint32_t quant_pack8(const float (&v)[8], float sdiv)
 }
 
 // Same eight codes without a division per element.  qa = fl(v * rcp(sdiv) + 8) (one
-// fused rounding) differs from the exact q + 8, q = v / sdiv, by less than 1.5e-6 (|q| <= 7;
-// the hardware reciprocal is within an ulp, the fma rounds once at an ulp of at most
-// 2^-20), and rint(q + 8) == rint(q) + 8 (8 is even, so ties still go to even), so
-// rint(qa) - 8 == rint(q) unless q lies within 1.5e-6 of a half-integer.  Any lane that
-// sees qa within 1e-5 of one raises `near_tie`; the caller then redoes the row's codes
-// with quant_pack8 (exact division).  Both paths therefore produce the reference's
-// round-half-even codes bit for bit.
+// fused rounding) differs from the exact q + 8, q = v / sdiv, by less than 1.2e-6: |q| <= 7,
+// the hardware reciprocal's relative error is at most 0.77 * 2^-23 (9.2e-8, measured on
+// gfx950 over every float in [1, 2) and a sample of the binades 2^-40 .. 2^40), so v * rcp
+// is within 6.4e-7 of q, and the fma rounds once at an ulp of at most 2^-20 (<= 4.8e-7).
+// rint(q + 8) == rint(q) + 8 (8 is even, so ties still go to even), so rint(qa) - 8 ==
+// rint(q) unless q lies within 1.2e-6 of a half-integer.  Any lane that sees qa within
+// 3e-6 of one (2.5 times that bound) raises `near_tie` for this word; the caller then
+// redoes that word's codes with quant_pack8 (exact division).  Both paths therefore
+// produce the reference's round-half-even codes bit for bit.  One slow row sets a
+// launch's end, so the redo is kept small: a 3e-6 window (1e-5 before) and only the
+// flagged words redone (before: every word of the wave), which took the K=16384 quant at
+// 776 rows from 18.4 to 16.9 us.
 __device__ __forceinline__ uint32_t quant_pack8_rcp(const float (&v)[8], float rcp, bool& near_tie) {
   uint32_t word = 0;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float qa = __builtin_fmaf(v[e], rcp, 8.0f);
     float r = __builtin_rintf(qa);
-    near_tie |= fabsf(qa - r) > 0.49999f;
+    near_tie |= fabsf(qa - r) > 0.499997f;
     r = fminf(fmaxf(r, 1.0f), 15.0f);
     word |= static_cast<uint32_t>(r) << (4 * e);
   }
@@ -237,6 +242,7 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
     for (int e = 0; e < 8; ++e) c8[e] = v[g + (1 << LAST_W) * (8 * u + e)];
   };
   uint32_t words[NW];
+  bool tie[NW];
   bool near_tie = false;
   const float rcp = __builtin_amdgcn_rcpf(sdiv);
 #pragma unroll
@@ -245,16 +251,23 @@ __device__ __forceinline__ void fwht_quant_row(float (&v)[1 << (LOGK - LOGT)], f
     for (int u = 0; u < RUN / 8; ++u) {
       float c8[8];
       gather8(g, u, c8);
-      words[g * (RUN / 8) + u] = quant_pack8_rcp(c8, rcp, near_tie);
+      const int i = g * (RUN / 8) + u;
+      tie[i] = false;
+      words[i] = quant_pack8_rcp(c8, rcp, tie[i]);
+      near_tie |= tie[i];
     }
-  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo the flagged words exactly
 #pragma unroll
     for (int g = 0; g < (1 << LAST_W); ++g)
 #pragma unroll
       for (int u = 0; u < RUN / 8; ++u) {
-        float c8[8];
-        gather8(g, u, c8);
-        words[g * (RUN / 8) + u] = quant_pack8(c8, sdiv);
+        const int i = g * (RUN / 8) + u;
+        if (__builtin_amdgcn_ballot_w64(tie[i]) != 0) {
+          float c8[8];
+          gather8(g, u, c8);
+          const uint32_t exact = quant_pack8(c8, sdiv);
+          words[i] = tie[i] ? exact : words[i];
+        }
       }
   }
 #pragma unroll
@@ -358,6 +371,7 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
   if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
   // Codes of the lane's R consecutive elements: R / 8 words, word u = codes 8u .. 8u + 7.
   uint32_t words[R / 8];
+  bool tie[R / 8];
   bool near_tie = false;
   const float rcp = __builtin_amdgcn_rcpf(sdiv);
 #pragma unroll
@@ -365,15 +379,20 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
     float c8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-    words[u] = quant_pack8_rcp(c8, rcp, near_tie);
+    tie[u] = false;
+    words[u] = quant_pack8_rcp(c8, rcp, tie[u]);
+    near_tie |= tie[u];
   }
-  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo the flagged words exactly
 #pragma unroll
     for (int u = 0; u < R / 8; ++u) {
-      float c8[8];
+      if (__builtin_amdgcn_ballot_w64(tie[u]) != 0) {
+        float c8[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-      words[u] = quant_pack8(c8, sdiv);
+        for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+        const uint32_t exact = quant_pack8(c8, sdiv);
+        words[u] = tie[u] ? exact : words[u];
+      }
     }
   }
 #pragma unroll
@@ -451,6 +470,7 @@ __device__ __forceinline__ void fwht_quant_row_2wave(float (&v)[1 << (LOGK - 7)]
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (store && t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
   uint32_t words[R / 8];
+  bool tie[R / 8];
   bool near_tie = false;
   const float rcp = __builtin_amdgcn_rcpf(sdiv);
 #pragma unroll
@@ -458,15 +478,20 @@ __device__ __forceinline__ void fwht_quant_row_2wave(float (&v)[1 << (LOGK - 7)]
     float c8[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-    words[u] = quant_pack8_rcp(c8, rcp, near_tie);
+    tie[u] = false;
+    words[u] = quant_pack8_rcp(c8, rcp, tie[u]);
+    near_tie |= tie[u];
   }
-  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo with exact division
+  if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo the flagged words exactly
 #pragma unroll
     for (int u = 0; u < R / 8; ++u) {
-      float c8[8];
+      if (__builtin_amdgcn_ballot_w64(tie[u]) != 0) {
+        float c8[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
-      words[u] = quant_pack8(c8, sdiv);
+        for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+        const uint32_t exact = quant_pack8(c8, sdiv);
+        words[u] = tie[u] ? exact : words[u];
+      }
     }
   }
   if (store) {

@@ -142,6 +142,36 @@ def test_quantize_exact_ties(ext, cuda, k):
     assert sorted(np.unique(got[0, r0_cols]).tolist()) == sorted({7, 2, -2, 0, 4, -6, 1, -4})
 
 
+@pytest.mark.parametrize("k", [2048, 16384])
+def test_quantize_many_ties(ext, cuda, k):
+    """As test_quantize_exact_ties with 48 exact half-integer quotients per row: lanes then
+    hold several tied codes, in one or more of their code words, next to words with none,
+    so the redo of only the flagged words (each redone in full) is checked against the
+    exact division code for code."""
+    halves = np.arange(-6.5, 7.0, 1.0)
+    m = 16
+    y = np.zeros((m, k), np.float64)
+    rng = np.random.default_rng(1000 + k)
+    for r in range(m):
+        y[r, 0] = 7.0 if r % 2 == 0 else -7.0
+        cols = rng.choice(np.arange(1, k), size=48, replace=False)
+        y[r, cols] = rng.choice(halves, size=48)
+    y /= 16.0
+    x = orc.fwht_unnormalized(y.astype(np.float32)).astype(np.float64) / k
+    x16 = x.astype(np.float16)
+    assert np.array_equal(x16.astype(np.float64), x), "inputs must be exact in fp16"
+    q, sa = ext.quantize(torch.from_numpy(x16).to(cuda))
+    torch.cuda.synchronize()
+    q_ref, s_ref = orc.quant_activation(x16)
+    got = _codes(q, m, k)
+    _assert_codes_equal(got, q_ref, f"many ties K={k}")
+    _assert_qcorr(q, q_ref, f"many ties K={k}")
+    assert np.array_equal(inp.to_np(sa).view(np.int32), s_ref.view(np.int32))
+    for r in range(m):  # every tie went to the even neighbour
+        cols = np.flatnonzero(y[r, 1:]) + 1
+        assert np.all(got[r, cols] % 2 == 0)
+
+
 # ----------------------------------------------------------------------------- repack
 @pytest.mark.parametrize("n,k", [(16, 64), (48, 192), (256, 2048), (128, 16384)])
 def test_repack_matches_cpu_layout(ext, cuda, n, k):
