@@ -19,7 +19,10 @@ Pinning (each function is checked by ``tests/test_oracle.py``):
   * ``preshuffle_wmma_weight`` golden vector + inverse round trip.
   * ``int4_gemm_ref`` / ``gemm_acc_int32``  golden vectors + int64 brute force.
   * ``dequant_fp16``        golden vectors through ``int4_gemm_ref``.
-  * ``gelu_tanh_up``        float64 closed form of GELU-tanh (tolerance only).
+  * ``gelu_tanh``           torch.nn.functional.gelu(approximate="tanh") in float64 on the CPU
+                            (transformers' GELUTanh, the reference MLP's act_fn), to 1e-15
+                            relative plus the float64 cancellation of 1 + tanh near -1;
+                            a wrong constant or the erf form fails it.
   * ``rms_norm_lanes``      transformers' GemmaRMSNorm (torch fp32 on the CPU) to one fp16
                             ulp; constant rows (closed form); the wave-order sum against
                             float64 (it is a restatement of an fp32 summation order, so
@@ -199,16 +202,12 @@ def unshuffle_wmma_weight(tiled: np.ndarray, k: int) -> np.ndarray:
 
 
 def gelu_tanh(x: np.ndarray) -> np.ndarray:
-    """GELU, tanh approximation, in float64 (transformers GELUTanh = F.gelu(approximate='tanh'))."""
+    """GELU, tanh approximation, in float64: the reference MLP's act_fn (apply.py:135-138,
+    transformers' GELUTanh = F.gelu(approximate='tanh')).  The GPU's fused GELU*up is
+    checked bit for bit against torch's eager fp16 ops on the same GPU instead (every fp16
+    gate); this float64 form serves tolerance checks."""
     x = np.asarray(x, dtype=np.float64)
     return 0.5 * x * (1.0 + np.tanh(math.sqrt(2.0 / math.pi) * (x + 0.044715 * x**3)))
-
-
-def gelu_tanh_up(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
-    """h = fp16(gelu_tanh(gate)) * up with fp16 rounding of each op, as the eager fp16
-    sequence ``act_fn(gate) * up`` of apply.py:138 rounds (values in float64 math)."""
-    g = gelu_tanh(np.asarray(gate, np.float16).astype(np.float64)).astype(np.float16)
-    return (g.astype(np.float64) * np.asarray(up, np.float16).astype(np.float64)).astype(np.float16)
 
 
 def rms_norm_lanes(x: np.ndarray, weight: np.ndarray, eps: float, unit_offset: bool = True,

@@ -20,12 +20,14 @@ import functools
 import json
 import os
 import types
+import weakref
 from pathlib import Path
 from typing import Iterable
 
 import torch
 import torch.nn as nn
 
+from pi05_fast.w4a4.extension import register_cache_clearer
 from pi05_fast.w4a4.linear import W4A4Linear
 from pi05_fast.w4a4.pack import MFMA_MARKER_WORDS, preshuffle_wmma_weight, should_rotate
 
@@ -398,9 +400,11 @@ def _k_rope_weight(attn: nn.Module, x: torch.Tensor):
     """The RoPE-pair-ordered copy of the K weight (``extension.rope_pair_weight``) when the
     QKV call can take the attention prep in its epilogue: one KV head of 256, MFMA-layout
     q/k/v weights, a token count that is a multiple of 8; else None.  The copy is kept on
-    the module and rebuilt when the K weight tensor is replaced or modified in place (in
-    eager calls; a compiled graph uses the copy an eager call built, else the separate prep).
-    ``PI05_W4A4_FUSE_KV=0`` keeps the separate K/V prep launch."""
+    the module and rebuilt when the K weight tensor is replaced, modified in place through
+    itself or given new storage (``.data = ...``), in eager calls; a compiled graph uses the
+    copy an eager call built, else the separate prep.  A write through ``.data`` needs
+    ``extension.clear_weight_caches()``.  ``PI05_W4A4_FUSE_KV=0`` keeps the separate K/V
+    prep launch."""
     if os.environ.get("PI05_W4A4_FUSE_KV", "1") == "0" or int(x.size(1)) % 8:
         return None
     wk = attn.k_proj.packed
@@ -414,15 +418,29 @@ def _k_rope_weight(attn: nn.Module, x: torch.Tensor):
     if torch.compiler.is_compiling():
         # a traced graph uses the copy an eager call built; it builds none itself
         return hit[2] if hit is not None and hit[0] is wk else None
-    if hit is not None and hit[0] is wk and hit[1] == wk._version:
+    if hit is not None and hit[0] is wk and hit[1] == wk._version and hit[3] == wk.data_ptr():
         return hit[2]
     if not wk.is_cuda:
         return None
     from pi05_fast.w4a4.extension import rope_pair_weight
 
     out = rope_pair_weight(wk)
-    attn._w4a4_k_rope = (wk, wk._version, out)
+    attn._w4a4_k_rope = (wk, wk._version, out, wk.data_ptr())
+    _K_ROPE_HOLDERS.add(attn)
     return out
+
+
+# Attention modules holding a RoPE-pair K copy, for extension.clear_weight_caches().
+_K_ROPE_HOLDERS: weakref.WeakSet = weakref.WeakSet()
+
+
+def _clear_k_rope_copies() -> None:
+    for attn in list(_K_ROPE_HOLDERS):
+        attn.__dict__.pop("_w4a4_k_rope", None)
+    _K_ROPE_HOLDERS.clear()
+
+
+register_cache_clearer(_clear_k_rope_copies)
 
 
 def fuse_decoder_layers(model: nn.Module) -> int:

@@ -49,17 +49,41 @@ def library_path() -> Path:
     return Path(__file__).resolve().parent / "_lib" / _LIB_NAME
 
 
+def _build_library(path: Path) -> None:
+    """Compile the library to ``path`` with hipcc (``build_lib.py`` beside the package:
+    offload target from PYTORCH_ROCM_ARCH / GPU_ARCHS, commands shown with
+    PI05_W4A4_VERBOSE=1), as the reference's loader JIT-builds on first use."""
+    import importlib.util
+
+    script = Path(__file__).resolve().parents[2] / "build_lib.py"
+    if not script.is_file():
+        raise RuntimeError(f"W4A4 HIP library not found at {path}, and no build script at {script}")
+    spec = importlib.util.spec_from_file_location("_pi05_w4a4_build_lib", script)
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if mod.verbose_from_env():
+        print(f"w4a4: building {path} for {','.join(mod.target_archs())}", flush=True)
+    mod.build(out=path)
+
+
 def load_int4_gemm():
-    """Load the gfx950 C-ABI library (the reference JIT-built a pybind module here)."""
+    """Load the gfx950 C-ABI library, building it first when it is absent (the reference
+    JIT-builds its pybind module here, extension.py:15-75).  ``PI05_W4A4_NO_BUILD=1``
+    turns the build off: a missing library then raises."""
     global _lib
     if _lib is not None:
         return _lib
     path = library_path()
     if not path.is_file():
-        raise RuntimeError(
-            f"W4A4 HIP library not found at {path}; build it first "
-            "(python -c 'import __graft_entry__ as g; g.build()' from the repository root)"
-        )
+        if os.environ.get("PI05_W4A4_NO_BUILD", "0") == "1":
+            raise RuntimeError(
+                f"W4A4 HIP library not found at {path} (PI05_W4A4_NO_BUILD=1); build it first "
+                "(python pi05-pytorch-fast_amd/build_lib.py, or __graft_entry__.build())"
+            )
+        try:
+            _build_library(path)
+        except Exception as e:  # noqa: BLE001 - surfaced with the path
+            raise RuntimeError(f"W4A4 HIP library not found at {path}, and building it failed: {e}") from e
     lib = ctypes.CDLL(str(path))
     vp, i32, i64, sz = ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_size_t
     sig = {
@@ -307,9 +331,30 @@ def repack_weight(w: torch.Tensor, k: int | None = None, tiled: bool | None = No
 
 # Repacked copies of weights that arrive in a reference layout (L1/L2/L3), one per source
 # tensor object: the repack runs on the first call only.  An entry is dropped when its
-# source tensor is freed, and it is rebuilt when the tensor is modified in place (its
-# version counter moves) or used with another K.
+# source tensor is freed, and it is rebuilt when the tensor is modified in place through
+# itself (its version counter moves), when its storage is replaced (``w.data = new``: the
+# data pointer moves) or when it is used with another K.  An in-place write through
+# ``w.data`` (``w.data.copy_(new)``) moves neither: after one, call
+# ``clear_weight_caches()``.
 _MFMA_CACHE: dict[int, tuple] = {}
+# Other per-weight caches (the fused layer's RoPE-pair K copies) register a function that
+# drops them; clear_weight_caches() runs every one.
+_CACHE_CLEARERS: list = []
+
+
+def clear_weight_caches() -> None:
+    """Drop every derived copy of a weight that the ops keep (the repacked L1/L2/L3
+    weights and the RoPE-pair K weights of fused decoder layers), so that the next call
+    rebuilds them from the current weights.  Needed after writing a weight in place
+    through ``.data`` (which bypasses the version counter the caches check)."""
+    _MFMA_CACHE.clear()
+    for fn in _CACHE_CLEARERS:
+        fn()
+
+
+def register_cache_clearer(fn) -> None:
+    """Add ``fn`` (no arguments) to what clear_weight_caches() runs."""
+    _CACHE_CLEARERS.append(fn)
 
 
 def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
@@ -320,8 +365,8 @@ def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
     key = id(w)
     hit = _MFMA_CACHE.get(key)
     if hit is not None:
-        ref, version, hk, htiled, out = hit
-        if ref() is w and version == w._version and hk == k and htiled == tiled:
+        ref, version, ptr, hk, htiled, out = hit
+        if ref() is w and version == w._version and ptr == w.data_ptr() and hk == k and htiled == tiled:
             return out, n
     if tiled:
         out = repack_weight(w, k, tiled=True)
@@ -330,7 +375,8 @@ def _as_mfma(w: torch.Tensor, k: int, tiled: bool) -> tuple[torch.Tensor, int]:
         if n % 16 != 0:
             src = torch.nn.functional.pad(w.contiguous(), (0, 0, 0, 16 - n % 16))
         out = repack_weight(src, k, tiled=False)
-    _MFMA_CACHE[key] = (weakref.ref(w, lambda _r, key=key: _MFMA_CACHE.pop(key, None)), w._version, k, tiled, out)
+    _MFMA_CACHE[key] = (weakref.ref(w, lambda _r, key=key: _MFMA_CACHE.pop(key, None)), w._version, w.data_ptr(),
+                        k, tiled, out)
     return out, n
 
 
@@ -865,16 +911,18 @@ _register_custom_op()
 
 # Eager calls skip the torch.ops dispatcher (tens of microseconds of host time per call,
 # several per decoder layer) when nothing needs it: plain tensors, no autograd graph to
-# record, no Dynamo trace, no dispatch or function mode.  The direct and the dispatched
-# route run the same implementation.
+# record, no Dynamo trace, no torch.jit.trace (whose graph only sees dispatched ops), no
+# dispatch or function mode.  The direct and the dispatched route run the same
+# implementation.
 _is_compiling = torch.compiler.is_compiling
+_jit_tracing = torch._C._get_tracing_state
 _dispatch_modes = torch._C._len_torch_dispatch_stack
 _function_modes = torch._C._is_torch_function_mode_enabled
 _PLAIN = (torch.Tensor, torch.nn.Parameter)
 
 
 def _direct(*ts) -> bool:
-    if _is_compiling() or _dispatch_modes() or _function_modes():
+    if _is_compiling() or _jit_tracing() is not None or _dispatch_modes() or _function_modes():
         return False
     grad = torch.is_grad_enabled()
     for t in ts:

@@ -451,3 +451,25 @@ def test_reference_layout_repack_runs_once_per_weight(ext, cuda, monkeypatch):
     torch.cuda.synchronize()
     assert len(calls) == 4
     _assert_f16_equal(inp.to_np(y1b), orc.int4_gemm_ref(x.cpu().numpy(), w1.cpu().numpy()), "after update")
+
+
+def test_reference_layout_cache_sees_data_updates(ext, cuda):
+    """Weight updates that bypass the version counter: ``w.data = new`` is caught by the
+    cache's data-pointer check; ``w.data.copy_(new)`` needs clear_weight_caches(), after
+    which the output follows the new weight again (both against the oracle)."""
+    gen = inp.generator(11)
+    x = inp.activations(gen, 64, 2048).to(cuda)
+    w = inp.random_packed(gen, 256, 2048).to(cuda)
+    xn = x.cpu().numpy()
+    y0 = ext.int4_gemm(x, w)
+    torch.cuda.synchronize()
+    _assert_f16_equal(inp.to_np(y0), orc.int4_gemm_ref(xn, w.cpu().numpy()), "first call")
+    w.data = inp.random_packed(gen, 256, 2048).to(cuda)  # same object and version, new storage
+    y1 = ext.int4_gemm(x, w)
+    torch.cuda.synchronize()
+    _assert_f16_equal(inp.to_np(y1), orc.int4_gemm_ref(xn, w.cpu().numpy()), "after w.data = new")
+    w.data.copy_(inp.random_packed(gen, 256, 2048).to(cuda))  # bypasses the version counter
+    ext.clear_weight_caches()
+    y2 = ext.int4_gemm(x, w)
+    torch.cuda.synchronize()
+    _assert_f16_equal(inp.to_np(y2), orc.int4_gemm_ref(xn, w.cpu().numpy()), "after copy_ + clear_weight_caches")

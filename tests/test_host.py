@@ -14,7 +14,9 @@ from __future__ import annotations
 
 import ctypes
 import json
+import os
 import re
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -23,6 +25,8 @@ import torch
 from oracle import w4a4_oracle as orc
 from tests import w4a4_inputs as inp
 from tests.conftest import ROOT
+
+PKG_ROOT = ROOT / "pi05-pytorch-fast_amd"
 
 
 @pytest.fixture(scope="module")
@@ -263,6 +267,51 @@ def test_direct_route_only_for_plain_untraced_calls():
     with _Mode():
         assert not ext._direct(x)
 
+    # torch.jit.trace records only dispatched ops: inside a trace the call must take
+    # torch.ops, or the traced graph would replay uninitialised outputs.
+    seen = []
+
+    def probe(t):
+        seen.append(ext._direct(t, w))
+        return t * 2
+
+    torch.jit.trace(probe, (x,), check_trace=False)
+    assert seen == [False]
+    assert ext._direct(x, w)
+
+
+def test_weight_caches_follow_data_rebinding_and_clear():
+    """The per-tensor repack cache (and the RoPE-pair K copies) key on the tensor, its
+    version counter and its data pointer: ``w.data = new`` (same object, same version,
+    new storage) is seen; ``w.data.copy_`` is not, and clear_weight_caches() drops every
+    entry.  CPU-side bookkeeping only: the entries here are planted, nothing is launched."""
+    from pi05_fast.w4a4 import apply, extension as ext
+
+    w = torch.zeros(16, 9, dtype=torch.int32)
+    key = id(w)
+    sentinel = torch.ones(1)
+    ext._MFMA_CACHE[key] = (ext.weakref.ref(w), w._version, w.data_ptr(), 64, False, sentinel)
+    try:
+        hit = ext._MFMA_CACHE[key]
+        assert hit[0]() is w and hit[1] == w._version and hit[2] == w.data_ptr()
+        w.data = torch.ones(16, 9, dtype=torch.int32)  # new storage, same object and version
+        assert ext._MFMA_CACHE[key][2] != w.data_ptr()  # the lookup in _as_mfma misses
+        w.data.copy_(torch.full((16, 9), 3, dtype=torch.int32))  # bypasses the version counter
+        assert ext._MFMA_CACHE[key][1] == w._version
+        ext.clear_weight_caches()
+        assert key not in ext._MFMA_CACHE
+    finally:
+        ext._MFMA_CACHE.pop(key, None)
+
+    class _Attn(torch.nn.Module):
+        pass
+
+    attn = _Attn()
+    attn._w4a4_k_rope = (w, w._version, sentinel, w.data_ptr())
+    apply._K_ROPE_HOLDERS.add(attn)
+    ext.clear_weight_caches()
+    assert not hasattr(attn, "_w4a4_k_rope")
+
 
 def test_workspace_sizing(lib):
     n1 = (ctypes.c_int32 * 1)(2048)
@@ -449,9 +498,76 @@ def test_library_missing_fails_loudly(monkeypatch, tmp_path):
     from pi05_fast.w4a4 import extension
 
     monkeypatch.setenv("PI05_W4A4_LIB", str(tmp_path / "nope.so"))
+    monkeypatch.setenv("PI05_W4A4_NO_BUILD", "1")
     monkeypatch.setattr(extension, "_lib", None)
     with pytest.raises(RuntimeError, match="HIP library not found"):
         extension.load_int4_gemm()
+    # a build that cannot run (no hipcc) surfaces as the same error, never as a fallback
+    monkeypatch.setenv("PI05_W4A4_NO_BUILD", "0")
+    monkeypatch.setenv("ROCM_PATH", str(tmp_path / "no_rocm"))
+    with pytest.raises(RuntimeError, match="building it failed"):
+        extension.load_int4_gemm()
+    assert extension._lib is None
+
+
+def _build_lib_module():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("_build_lib_under_test", PKG_ROOT / "build_lib.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def test_build_knobs_reach_hipcc(monkeypatch, tmp_path):
+    """GPU_ARCHS / PYTORCH_ROCM_ARCH pick the offload targets (PYTORCH_ROCM_ARCH first, as
+    the reference's setdefault does), PI05_W4A4_EXTRA_CFLAGS is appended to every unit and
+    PI05_W4A4_VERBOSE=1 turns the command echo on."""
+    bl = _build_lib_module()
+    monkeypatch.delenv("PYTORCH_ROCM_ARCH", raising=False)
+    monkeypatch.delenv("GPU_ARCHS", raising=False)
+    assert bl.target_archs() == ["gfx950"]
+    monkeypatch.setenv("GPU_ARCHS", "gfx950;gfx942")
+    assert bl.target_archs() == ["gfx950", "gfx942"]
+    monkeypatch.setenv("PYTORCH_ROCM_ARCH", "gfx950")
+    assert bl.target_archs() == ["gfx950"]
+    assert bl.target_archs("gfx942") == ["gfx942"]
+    monkeypatch.setenv("PI05_W4A4_EXTRA_CFLAGS", "-DPI05_PROBE=1 -g0")
+    cmds, objs = bl.compile_commands(bl.target_archs("gfx950,gfx942"), tmp_path)
+    assert len(cmds) == len(bl.SOURCES) == len(objs)
+    for c in cmds:
+        assert "--offload-arch=gfx950" in c and "--offload-arch=gfx942" in c
+        assert c[-6:-4] == ["-DPI05_PROBE=1", "-g0"] or ("-DPI05_PROBE=1" in c and "-g0" in c)
+    monkeypatch.setenv("PI05_W4A4_VERBOSE", "1")
+    assert bl.verbose_from_env()
+    monkeypatch.setenv("PI05_W4A4_VERBOSE", "0")
+    assert not bl.verbose_from_env()
+
+
+def test_missing_library_is_built_on_first_load(monkeypatch, tmp_path, capsys):
+    """load_int4_gemm() with no library at its path builds one there with hipcc (for the
+    GPU_ARCHS target, echoing the commands under PI05_W4A4_VERBOSE=1) and loads it; the
+    result exports every symbol the header declares.  (No GPU needed: only the loader runs.)"""
+    import shutil
+
+    from pi05_fast.w4a4 import extension
+
+    if shutil.which(str(Path(os.environ.get("ROCM_PATH", "/opt/rocm")) / "bin" / "hipcc")) is None:
+        pytest.skip("no hipcc here")
+    out = tmp_path / "built" / "libpi05_w4a4.so"
+    monkeypatch.setenv("PI05_W4A4_LIB", str(out))
+    monkeypatch.delenv("PI05_W4A4_NO_BUILD", raising=False)
+    monkeypatch.delenv("PYTORCH_ROCM_ARCH", raising=False)
+    monkeypatch.setenv("GPU_ARCHS", "gfx950")
+    monkeypatch.setenv("PI05_W4A4_VERBOSE", "1")
+    monkeypatch.setattr(extension, "_lib", None)
+    lib = extension.load_int4_gemm()
+    printed = capsys.readouterr().out
+    assert out.is_file()
+    assert "--offload-arch=gfx950" in printed and "capi.hip" in printed
+    for sym in _declared_symbols():
+        assert hasattr(lib, sym), sym
+    monkeypatch.setattr(extension, "_lib", None)  # the next user reloads the in-tree library
 
 
 # ----------------------------------------------------------------------------- module / apply

@@ -234,6 +234,57 @@ def test_checks_catch_planted_mistakes(golden):
     assert not np.array_equal(_bits(y_bad), _bits(golden["gemm_y_8x16x2048"]))
 
 
+# ----------------------------------------------------------------------------- GELU
+def _gelu_inputs() -> np.ndarray:
+    x = np.concatenate([np.linspace(-12.0, 12.0, 240001), np.random.default_rng(5).standard_normal(50000) * 3.0,
+                        [0.0, -0.0, 1e-30, -1e-30, 6e-8, -6e-8, 40.0, -40.0, 65504.0, -65504.0]])
+    # every finite fp16 value too: the GPU epilogue's inputs are fp16 gates
+    f16 = np.arange(2**16, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    return np.concatenate([x, f16[np.isfinite(f16)].astype(np.float64)])
+
+
+def _gelu_close(a: np.ndarray, b: np.ndarray, x: np.ndarray) -> np.ndarray:
+    """float64 agreement: gelu = 0.5 x (1 + tanh(u)) loses absolute precision in 1 + tanh(u)
+    near tanh = -1 (about 2^-53 |x| per rounding), hence the |x|-scaled absolute term."""
+    return np.abs(a - b) <= 1e-14 * np.abs(b) + 1e-15 * np.abs(x)
+
+
+def test_gelu_tanh_matches_torch_float64():
+    """gelu_tanh is torch.nn.functional.gelu(approximate="tanh") (transformers' GELUTanh,
+    the act_fn of the reference MLP, apply.py:138) in float64 on the CPU."""
+    import torch
+
+    x = _gelu_inputs()
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    got = orc.gelu_tanh(x)
+    assert _gelu_close(got, want, x).all()
+    assert np.array_equal(np.signbit(got[x == 0]), np.signbit(x[x == 0]))  # gelu(-0) = -0
+
+
+def test_gelu_tanh_closed_forms():
+    """gelu(0) = 0, gelu(x) -> x for large x and -> 0 for large negative x, and the odd
+    part: gelu(x) - gelu(-x) = x exactly in real arithmetic (tanh is odd)."""
+    assert orc.gelu_tanh(np.array([0.0]))[0] == 0.0
+    assert orc.gelu_tanh(np.array([30.0]))[0] == 30.0
+    assert abs(orc.gelu_tanh(np.array([-30.0]))[0]) < 1e-300 or orc.gelu_tanh(np.array([-30.0]))[0] == 0.0
+    x = np.linspace(-6.0, 6.0, 1201)
+    assert np.allclose(orc.gelu_tanh(x) - orc.gelu_tanh(-x), x, rtol=0, atol=1e-14)
+
+
+def test_gelu_planted_mistakes_fail():
+    """A wrong cubic coefficient, the erf form or a dropped 1/2 each fail the torch check."""
+    import torch
+
+    x = _gelu_inputs()
+    want = torch.nn.functional.gelu(torch.from_numpy(x), approximate="tanh").numpy()
+    c = math.sqrt(2.0 / math.pi)
+    bad_coeff = 0.5 * x * (1.0 + np.tanh(c * (x + 0.0447 * x**3)))
+    bad_erf = torch.nn.functional.gelu(torch.from_numpy(x)).numpy()
+    bad_half = x * (1.0 + np.tanh(c * (x + 0.044715 * x**3)))
+    for bad in (bad_coeff, bad_erf, bad_half):
+        assert not _gelu_close(bad, want, x).all()
+
+
 # ----------------------------------------------------------------------------- RMSNorm
 def _torch_gemma_rms_norm(x16: np.ndarray, w16: np.ndarray, eps: float) -> np.ndarray:
     """transformers' GemmaRMSNorm on the CPU (fp32 inside, (1 + w), fp16 out)."""
