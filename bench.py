@@ -213,6 +213,37 @@ class KernelBench:
                 "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb}
 
 
+    def gelu_quant(self, m, k=2048, n=16384, fused=True):
+        """Gate/up with the GELU-tanh*up epilogue and the down projection's activation quant
+        of its output: one launch (pi05w4a4_gemm_gelu_up_quant) or, with fused=False, the
+        GEMM then pi05w4a4_quantize (two launches)."""
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        gen = torch.Generator(device=self.dev).manual_seed(20261203 + m)
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        self._check(lib.pi05w4a4_quantize(P(x), m, k, P(q), P(sa), self._stream()))
+        wg, wu = self._packed(n, k, gen), self._packed(n, k, gen)
+        h = torch.empty(m, n, dtype=torch.float16, device=self.dev)
+        dq = torch.empty(int(lib.pi05w4a4_q_words(m, n)), dtype=torch.int32, device=self.dev)
+        dsa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        ctl = torch.zeros(int(lib.pi05w4a4_mlp_ctl_words(m)), dtype=torch.int32, device=self.dev)
+        if fused:
+            fn = lambda: self._check(lib.pi05w4a4_gemm_gelu_up_quant(  # noqa: E731
+                P(q), P(sa), m, k, P(wg), P(wu), n, P(h), P(dq), P(dsa), P(ctl), None, None, 0, 0, 0,
+                self._stream()))
+        else:
+            def fn():
+                self._check(lib.pi05w4a4_gemm_gelu_up(P(q), P(sa), m, k, P(wg), P(wu), n, P(h), None, 0,
+                                                      self._stream()))
+                self._check(lib.pi05w4a4_quantize(P(h), m, n, P(dq), P(dsa), self._stream()))
+        us = self._time(fn)
+        if lib.pi05w4a4_mlp_status(0) != 0:
+            raise RuntimeError("a bounded wait of the fused gate/up + down quant ran out")
+        ops = 2.0 * m * 2 * n * k
+        return {"m": m, "k": k, "n": 2 * n, "avg_us": round(us, 3), "ops": ops, "launches": 1 if fused else 2,
+                "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+
     def qkv_rope(self, b, s, h=2048):
         """The QKV GEMMs with RoPE and the attention's K/V layout in the epilogue
         (pi05w4a4_gemm_qkv_rope, one KV head of 256) at B x S tokens."""
@@ -425,6 +456,8 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
         "rmsnorm_quant_k2048": lambda: kb.rmsnorm_quant(m),
         "qkv_rope": lambda: kb.qkv_rope(1, m),
+        "gate_up_gelu_quant": lambda: kb.gelu_quant(m),
+        "gate_up_gelu_then_quant": lambda: kb.gelu_quant(m, fused=False),
     }
 
     def copy():  # calibration for the HBM traffic counters: a plain 64 MiB copy

@@ -160,6 +160,45 @@ int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t 
                           void* h_fp16, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pi05w4a4_gemm_gelu_up followed by the down projection's activation quant of its output:
+ * h as above, then dq / dsa = pi05w4a4_quantize(h, M, K = n) (codes, row corrections and
+ * scales bit for bit; dq holds pi05w4a4_q_words(M, n) words).  Replaces the MLP's
+ * `act_fn(gate) * up` followed by the down projection's quantize_x (apply.py:135-141,
+ * int4_gemm.cu:496-531).  At n = 16384 with M > 64 both run in one launch: workgroups
+ * appended to the GEMM tiles quantize each 112-row block of h as soon as all of its
+ * columns are stored, in the slots the GEMM's partial last round leaves idle (other
+ * shapes: two launches, same results).
+ * ctl: int32 control block of pi05w4a4_mlp_ctl_words(M) words in device memory, zeroed
+ * once by the caller before its first use; every call that completes leaves it zeroed.
+ * Calls that share one control block must be stream-ordered (calls that overlap race).
+ * warm_*: up to 4 buffers read into the Infinity Cache by quant workgroups that find no
+ * row left (pi05w4a4_quantize_warm's argument form).
+ * The quant workgroups wait for the GEMM tiles of their row block with a bounded wait
+ * (spin_limit rounds of about 4 us; 0 = the default of 2^20) that never deadlocks (see
+ * the kernel); one that runs out leaves its row unquantized and sets a host-visible status
+ * word, read by pi05w4a4_mlp_status: the outputs of that call are invalid and ctl must be
+ * zeroed again.  wait_extra (0 in normal use; tests pass 1) makes every wait expect one
+ * completion more than exists, which forces that path.
+ * No counterpart in the reference (an optional fusion of two of its steps).
+ */
+int pi05w4a4_gemm_gelu_up_quant(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                                const int32_t* w_gate_mfma, const int32_t* w_up_mfma, int32_t n,
+                                void* h_fp16, int32_t* dq, float* dsa, int32_t* ctl,
+                                const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                                int32_t spin_limit, int32_t wait_extra, void* stream);
+
+/* Words of the control block of pi05w4a4_gemm_gelu_up_quant for M rows (0 for M <= 0). */
+size_t pi05w4a4_mlp_ctl_words(int64_t m);
+
+/*
+ * Number of bounded waits of pi05w4a4_gemm_gelu_up_quant that ran out since the last
+ * clear (a pinned host word the kernels write; reading it does not synchronize, so it
+ * covers the calls that have completed).  clear != 0 resets it.  -1 when the word cannot
+ * be allocated (no device).  No counterpart in the reference.
+ */
+int64_t pi05w4a4_mlp_status(int32_t clear);
+
+/*
  * GEMM with a residual add in the epilogue: y = fp16(fp16((acc * sa[m]) * sw[n]) + r[m, n])
  * for residual r fp16 [M, N] (16-byte aligned; y may alias r).  The second rounding is
  * that of the decoder's fp16 `residual + hidden_states` (modeling_gemma.py

@@ -501,6 +501,110 @@ int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t 
                   static_cast<hipStream_t>(stream));
 }
 
+size_t pi05w4a4_mlp_ctl_words(int64_t m) {
+  if (m <= 0) return 0;
+  // header, then one 128-byte line per possible m-tile (at most one per 16 rows)
+  return static_cast<size_t>(w4a4::kMlpCtlHeader + w4a4::kMlpCtlStride * cdiv(m, 16));
+}
+
+namespace {
+// Host-visible word set by a bounded wait of the fused gate/up + down-quant launch that ran
+// out (pinned, mapped host memory shared by every device; allocated once).
+std::mutex g_status_mu;
+uint32_t* g_status_host = nullptr;
+uint32_t* g_status_dev = nullptr;
+
+uint32_t* mlp_status_device_word() {
+  std::lock_guard<std::mutex> lk(g_status_mu);
+  if (g_status_dev != nullptr) return g_status_dev;
+  void* hp = nullptr;
+  if (hipHostMalloc(&hp, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) return nullptr;
+  void* dp = nullptr;
+  if (hipHostGetDevicePointer(&dp, hp, 0) != hipSuccess) {
+    (void)hipHostFree(hp);
+    return nullptr;
+  }
+  g_status_host = static_cast<uint32_t*>(hp);
+  *reinterpret_cast<volatile uint32_t*>(g_status_host) = 0;
+  g_status_dev = static_cast<uint32_t*>(dp);
+  return g_status_dev;
+}
+}  // namespace
+
+int64_t pi05w4a4_mlp_status(int32_t clear) {
+  if (mlp_status_device_word() == nullptr) return -1;
+  volatile uint32_t* w = g_status_host;
+  const uint32_t v = *w;
+  if (clear) *w = 0;
+  return static_cast<int64_t>(v);
+}
+
+int pi05w4a4_gemm_gelu_up_quant(const int32_t* q, const float* sa, int64_t m, int32_t k,
+                                const int32_t* w_gate_mfma, const int32_t* w_up_mfma, int32_t n,
+                                void* h_fp16, int32_t* dq, float* dsa, int32_t* ctl,
+                                const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+                                int32_t spin_limit, int32_t wait_extra, void* stream) {
+  int rc = validate_gemm_common(q, sa, m, k);
+  if (rc) return rc;
+  rc = validate_weight(w_gate_mfma, n, "gate weight");
+  if (rc) return rc;
+  rc = validate_weight(w_up_mfma, n, "up weight");
+  if (rc) return rc;
+  if (n % 64 != 0) return fail(PI05W4A4_EINVAL, "the down-projection quant needs N %% 64 == 0, got %d", n);
+  if (spin_limit < 0 || wait_extra < 0) return fail(PI05W4A4_EINVAL, "spin_limit and wait_extra must be >= 0");
+  w4a4::CacheWarmParams warm;
+  rc = collect_warm(warm_ptrs, warm_bytes, warm_n, &warm);
+  if (rc) return rc;
+  if (m == 0) return ok();
+  if (h_fp16 == nullptr || dq == nullptr || dsa == nullptr || ctl == nullptr)
+    return fail(PI05W4A4_EINVAL, "null output, codes, scales or control block");
+  if (!aligned(h_fp16, 16) || !aligned(dq, 16) || !aligned(dsa, 4) || !aligned(ctl, 4))
+    return fail(PI05W4A4_EINVAL, "h and the codes must be 16-byte aligned, scales and control block 4-byte aligned");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int32_t* ws[2] = {w_gate_mfma, w_up_mfma};
+  const int32_t ns[2] = {n, n};
+  const Plan pl = make_plan(m, k, 2, ns, true, true);
+  const float inv_sqrt_n = static_cast<float>(1.0 / std::sqrt(static_cast<double>(n)));
+  const bool fused = pl.cfg.id == w4a4::kCfg7x4 && pl.ksplit == 1 && n == 16384 && pl.mtiles <= 65535;
+  if (!fused) {
+    // Any other plan: the GEMM, then the standalone quantizer (same codes, two launches).
+    void* ys[2] = {h_fp16, h_fp16};
+    rc = run_gemm(q, sa, m, k, 2, ws, ns, ys, w4a4::kEpiGeluUp, nullptr, 0, st);  // no K split at N = 16384
+    if (rc) return rc;
+    return hip_status(w4a4::launch_quantize(h_fp16, m, n, dq, dsa, inv_sqrt_n, st, &warm), "quantize launch");
+  }
+  uint32_t* status = mlp_status_device_word();
+  if (status == nullptr) return fail(PI05W4A4_EHIP, "gemm_gelu_up_quant: no host-visible status word");
+  w4a4::GemmParams p{};
+  p.q = q;
+  p.sa = sa;
+  p.m = m;
+  p.k = k;
+  p.ngroups = 2;
+  p.g[0] = w4a4::GemmGroup{w_gate_mfma, h_fp16, n, 0};
+  p.g[1] = w4a4::GemmGroup{w_up_mfma, h_fp16, n, static_cast<int32_t>(cdiv(n, pl.cfg.cols(false)))};
+  p.ntiles = static_cast<int32_t>(pl.ntiles);
+  p.mtiles = static_cast<int32_t>(pl.mtiles);
+  p.ksplit = 1;
+  p.kblocks_per_split = pl.kblocks;
+  p.mblocks = static_cast<int32_t>(cdiv(m, 16));
+  p.n_total = 2 * n;
+  p.gelu_pair_n = n;
+  p.mode = w4a4::kEpiGeluUp;
+  p.dq = dq;
+  p.dsa = dsa;
+  p.qctl = ctl;
+  p.qstatus = status;
+  p.dinv_sqrt_k = inv_sqrt_n;
+  // ~2^20 rounds of s_sleep 127 (about 4 us each): seconds, far beyond any real wait.
+  p.spin_limit = spin_limit > 0 ? spin_limit : (1 << 20);
+  p.wait_extra = wait_extra;
+  p.warm = warm;
+  const int nquant = static_cast<int>(std::min<int64_t>(m, 2 * static_cast<int64_t>(w4a4::device_cu_count())));
+  return hip_status(w4a4::launch_gemm_gelu_quant(p, nquant, st), "gemm_gelu_up_quant launch");
+}
+
 int pi05w4a4_gemm_acc(const int32_t* q, int64_t m, int32_t k, const int32_t* w_mfma,
                       int32_t n, int32_t* acc, void* stream) {
   static const float kDummy = 0.0f;

@@ -55,7 +55,9 @@
 // accumulators, and paired gate/up tiles finished exactly as the eager
 // `gelu(gate, approximate="tanh") * up` on the fp16 gate and up (apply.py:135-138).
 
+#include "cache_warm.h"
 #include "gelu_tanh.h"
+#include "quant_row.h"
 #include "w4a4_internal.h"
 
 namespace w4a4 {
@@ -154,7 +156,103 @@ __device__ __forceinline__ int64_t vfrag_slot(int d, int t0, int nst) {
   return (static_cast<int64_t>((d >> 4) * nst + (t0 >> 5))) * 64 + 16 * ((t0 & 31) >> 3) + (d & 15);
 }
 
-template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false>
+// ---- Down-projection quant in the gate/up launch (QFUSE).  The MLP's down projection
+// quantizes h = gelu(gate) * up (K = 16384) right after the gate/up GEMM writes it
+// (apply.py:138-141 -> int4_gemm.cu:496-531).  Rows of h can be rotated only once all of
+// their 16384 columns are stored, i.e. once every n-tile of their m-tile is done, so the
+// launch appends quant workgroups to the GEMM tiles: a GEMM workgroup counts its m-tile's
+// completion after its stores (release at agent scope: the workgroups of one row block run
+// on all eight XCDs), and a quant workgroup takes rows in increasing order from a shared
+// counter, waits (bounded) for the row's m-tile, acquires, and runs the row through the
+// K = 16384 quantizer of the standalone kernel (fwht_quant_row, 256 threads, one 68 KB LDS
+// row), so the codes are those of pi05w4a4_quantize bit for bit.  The tiles are dealt
+// m-tile-major within each XCD, so the first round of tiles completes whole row blocks and
+// the quant workgroups that fill the slots left idle by the partial last round of tiles
+// have rows to work on while it runs.
+// No deadlock: a GEMM workgroup never waits, and each XCD dispatches its workgroups in
+// index order, so a quant workgroup (index >= every GEMM tile's) only takes a slot on an
+// XCD whose GEMM tiles have all been dispatched; those finish, so every counter reaches its
+// target.  The wait is bounded anyway (spin_limit rounds of s_sleep): one that runs out
+// leaves the row unquantized, sets *qstatus for the host and the workgroup leaves.
+constexpr int kQuantLogK = 14;
+constexpr int kQuantLogT = 8;
+constexpr int kQuantR = 1 << (kQuantLogK - kQuantLogT);                             // 64 values per thread
+constexpr int kQuantLrow = (1 << kQuantLogK) + 4 * ((1 << kQuantLogK) / kQuantR);   // LDS floats per row
+constexpr int kQuantLdsBytes = kQuantLrow * 4 + 64;                                 // + reductions, broadcast
+
+template <int TILE_ROWS>
+__device__ __forceinline__ void down_quant_role(const GemmParams& p, char* lds) {
+  float* const L = reinterpret_cast<float*>(lds);
+  float* const red = L + kQuantLrow;
+  int* const ired = reinterpret_cast<int*>(red + 4);
+  int* const bcast = ired + 4;
+  const int t = threadIdx.x;
+  const int64_t M = p.m;
+  const int nquant = static_cast<int>(gridDim.x) - p.ntiles * p.mtiles;
+  int32_t* const next_row = p.qctl;
+  int32_t* const exited = p.qctl + kMlpCtlExited;
+  int32_t* const done = p.qctl + kMlpCtlHeader;  // m-tile i at done[kMlpCtlStride * i]
+  const int target = p.ntiles + p.wait_extra;
+  const _Float16* const h = static_cast<const _Float16*>(p.g[0].y);
+  int32_t* const qcorr = p.dq + q_payload_words((M + 15) / 16, kblocks128(1 << kQuantLogK));
+  for (;;) {
+    if (t == 0) *bcast = __hip_atomic_fetch_add(next_row, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int row = *bcast;
+    __syncthreads();
+    if (row >= M) {
+      // No row left: the grab past the end is this workgroup's own warming slice.
+      if (p.warm.nbuf > 0 && row - M < nquant) cache_warm_part<256>(p.warm, row - M, nquant, t);
+      break;
+    }
+    const int mt = row / TILE_ROWS;
+    if (t == 0) {
+      int ready = 1;
+      int spins = 0;
+      // Long sleeps between polls: the polls bypass the caches, and at a round trip every
+      // 0.25 us the waiting workgroups slowed the GEMM tiles beside them by 2x.
+      while (__hip_atomic_load(done + kMlpCtlStride * mt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+        if (++spins > p.spin_limit) {
+          ready = 0;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(127);
+      }
+      *bcast = ready;
+    }
+    __syncthreads();
+    if (*bcast == 0) {
+      if (t == 0 && p.qstatus != nullptr)
+        __hip_atomic_store(p.qstatus, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      break;
+    }
+    // The row block's stores happen-before the counts this thread saw: acquire them.
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    float v[kQuantR];
+    const _Float16* xr = h + static_cast<int64_t>(row) * (1 << kQuantLogK) + t * kQuantR;
+#pragma unroll
+    for (int c = 0; c < kQuantR / 8; ++c) {
+      const half8 hv = *reinterpret_cast<const half8*>(xr + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(hv[e]);
+    }
+    fwht_quant_row<kQuantLogK, kQuantLogT>(v, L, red, ired, t, row, p.dq, p.dsa, qcorr, p.dinv_sqrt_k);
+    __syncthreads();  // the next row reuses L, red and bcast
+  }
+  // The last quant workgroup to leave returns the control block to zero for the next launch
+  // (every GEMM tile has counted by then, unless a wait ran out: the host then clears it).
+  if (t == 0) {
+    const int before = __hip_atomic_fetch_add(exited, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == nquant - 1) {
+      for (int i = 0; i < p.mtiles; ++i)
+        __hip_atomic_store(done + kMlpCtlStride * i, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(next_row, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(exited, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false, bool QFUSE = false>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!(GELU && QKV_PREP), "the attention prep is a fp16 epilogue");
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
@@ -165,6 +263,41 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // waves share the epilogue.
   static_assert(KW == 1 || NW == 1, "a K split covers one column block");
   constexpr bool kSpread = KW > 1;
+
+  // ---- LDS: one pool carved at fixed offsets (the correction table, the tile's scales,
+  // the k-reduction buffer, the output staging rows).  With QFUSE the down-projection
+  // quant workgroups of the same launch reuse the pool for their row transposes.
+  constexpr bool kFixWide = KW == 1;
+  constexpr int kFixPieces = kGeluFixPosPieces + (kGeluFixEntries / 1024 - kGeluFixNegPiece0);
+  constexpr int kFixCompact = kFixPieces * 1024;
+  constexpr int TROWS = 16 * MI;
+  constexpr int NCOL = 16 * NI * NW;  // GELU: the gate and the up columns of the tile
+  // k reduction: row blocks per phase.  The 8-part tiles (one workgroup per CU) take half
+  // the tile at a time; the 4-part ones keep the buffer at 32 KB (two workgroups per CU).
+  constexpr int PM0 = KW == 8 ? (MI + 1) / 2 : (32 / (KW * NI) > 0 ? 32 / (KW * NI) : 1);
+  constexpr int PM = PM0 < MI ? PM0 : MI;
+  constexpr int OCW = GELU ? 8 * NI : 16 * NI;  // output columns of a wave
+  constexpr int LSR = OCW + 8;                  // staged row stride in halves (pad)
+  constexpr int kLdsFix = 0;
+  constexpr int kLdsSa = kLdsFix + ((GELU ? (kFixWide ? kGeluFixEntries : kFixCompact) : 16) + 15) / 16 * 16;
+  constexpr int kLdsSw = kLdsSa + TROWS * 4;
+  constexpr int kLdsRed = kLdsSw + NCOL * 4;
+  constexpr int kLdsStage = kLdsRed + (kSpread ? KW * PM * NI * 64 * 16 : 0);
+  constexpr int kLdsGemm = kLdsStage + (kSpread ? KW : NW) * 16 * LSR * 2;
+  constexpr int kLdsPool = (QFUSE && kQuantLdsBytes > kLdsGemm) ? kQuantLdsBytes : kLdsGemm;
+  __shared__ __align__(16) char lds_pool[kLdsPool];
+  int8_t* const fix_lds = reinterpret_cast<int8_t*>(lds_pool + kLdsFix);
+  float* const epi_sa = reinterpret_cast<float*>(lds_pool + kLdsSa);  // row scales / 16 of the tile
+  float* const epi_sw = reinterpret_cast<float*>(lds_pool + kLdsSw);  // column scales of the tile
+
+  if constexpr (QFUSE) {
+    static_assert(GELU && KW == 1, "the down-projection quant rides on the paired gate/up tiles");
+    // Workgroups past the GEMM tiles quantize rows of h as their row blocks complete.
+    if (static_cast<int>(blockIdx.x) >= p.ntiles * p.mtiles) {
+      down_quant_role<16 * MI>(p, lds_pool);
+      return;
+    }
+  }
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -183,8 +316,17 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     const int x = tile & 7, q = total >> 3, r = total & 7;
     tile = x * q + min(x, r) + (tile >> 3);
   }
-  const int mt = tile % p.mtiles;
+  int mt = tile % p.mtiles;
   int nt = tile / p.mtiles;
+  if constexpr (QFUSE) {
+    // Row blocks complete early: XCD x owns the n-tiles [x*per, (x+1)*per) and runs them
+    // m-tile-major (a bijection whenever 8 divides the n-tile count).
+    if ((p.ntiles & 7) == 0) {
+      const int per = p.ntiles >> 3, i = static_cast<int>(blockIdx.x) >> 3;
+      mt = i / per;
+      nt = (static_cast<int>(blockIdx.x) & 7) * per + i % per;
+    }
+  }
   if constexpr (QKV_PREP) {
     // The K and V n-tiles (the groups after Q) carry the attention prep and so the longer
     // epilogue; they are spread evenly through the n order (one in every s positions), so
@@ -207,10 +349,6 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // (kFixCompact) and the lookup adds the sign's half offset.  The copies complete under
   // the main loop; a vmcnt(0) wait and the barrier ahead of the epilogue order them (and
   // the fill) before the reads.
-  constexpr bool kFixWide = KW == 1;
-  constexpr int kFixPieces = kGeluFixPosPieces + (kGeluFixEntries / 1024 - kGeluFixNegPiece0);
-  constexpr int kFixCompact = kFixPieces * 1024;
-  __shared__ __align__(16) int8_t fix_lds[GELU ? (kFixWide ? kGeluFixEntries : kFixCompact) : 16];
   if constexpr (GELU) {
     static_assert(kGeluFixEntries % 1024 == 0, "the table is copied in 1 KB pieces");
     for (int c = wave; c < kFixPieces; c += NWAVES) {
@@ -410,8 +548,6 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // under the main loop: thread t holds the row scale of tile row t % (16*MI) and the
   // column scale of tile column t % NCOL.  All indices are clamped, so every thread loads
   // unconditionally; columns past N get zero scales when staged to LDS after the loop.
-  constexpr int TROWS = 16 * MI;
-  constexpr int NCOL = 16 * NI * NW;  // GELU: the gate and the up columns of the tile
   float e_sa;
   float e_sw;
   bool e_colvalid;
@@ -463,8 +599,6 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     if (nkb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  __shared__ __align__(16) float epi_sa[TROWS];  // row scales / 16 of the tile
-  __shared__ __align__(16) float epi_sw[NCOL];   // column scales of the tile
   if (tid < TROWS) epi_sa[tid] = e_sa * 0.0625f;
   if (tid < NCOL) epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
   if constexpr (KW == 1) __syncthreads();  // KW > 1: the k reduction below synchronises
@@ -498,11 +632,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // stores its parts of the phase's row blocks and the owner of each row block (wave
   // mi mod KW) sums the KW parts of its fragments (int32: any order gives the same sum).
   if constexpr (kSpread) {
-    // Row blocks per phase: the 8-part tiles (one workgroup per CU) take half the tile at
-    // a time; the 4-part ones keep the buffer at 32 KB (two workgroups per CU).
-    constexpr int PM0 = KW == 8 ? (MI + 1) / 2 : (32 / (KW * NI) > 0 ? 32 / (KW * NI) : 1);
-    constexpr int PM = PM0 < MI ? PM0 : MI;
-    __shared__ __align__(16) v4i red[KW * PM * NI * 64];
+    v4i* const red = reinterpret_cast<v4i*>(lds_pool + kLdsRed);  // KW * PM * NI * 64
 #pragma unroll
     for (int ph = 0; ph * PM < MI; ++ph) {
 #pragma unroll
@@ -549,13 +679,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // four columns) and written back as whole rows with 16-byte stores: a wave row of
     // 64 (GELU: 32) fp16 columns is 128 (64) contiguous bytes.  The staging area is
     // private to the wave.
-    constexpr int OCW = GELU ? 8 * NI : 16 * NI;  // output columns of the wave
-    constexpr int LSR = OCW + 8;                  // staged row stride in halves (pad)
     constexpr int LPR = OCW / 8;                  // lanes per row, 16 bytes each
     constexpr int RPI = 64 / LPR;                 // rows per store instruction
     static_assert(16 % RPI == 0 || RPI % 16 == 0, "store rows must tile the 16-row block");
-    __shared__ __align__(16) _Float16 stage_all[(kSpread ? KW : NW) * 16 * LSR];
-    _Float16* stage = stage_all + (kSpread ? wk : wn) * (16 * LSR);
+    _Float16* const stage = reinterpret_cast<_Float16*>(lds_pool + kLdsStage) + (kSpread ? wk : wn) * (16 * LSR);
     // Stores address the wave's output block through a scalar base and a 32-bit lane
     // offset (the block spans at most 16*MI rows of N columns).
     char* yw = reinterpret_cast<char*>(static_cast<_Float16*>(Y) + m0 * N + wcol);
@@ -717,6 +844,18 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
         }
       }
     }
+    if constexpr (QFUSE) {
+      // This tile's part of h is stored: count it for its row block.  Each wave waits for
+      // its own stores to be acknowledged, the barrier gathers the waves, and one release
+      // at agent scope (the consumers run on any XCD) precedes the count.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        __hip_atomic_fetch_add(p.qctl + kMlpCtlHeader + kMlpCtlStride * mt, 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
   } else {
     // kEpiPartial: partial sums of 16 * acc, int32 [ksplit, M, n_total] at column
     // col_off + col (slice 0 carries the corrections);
@@ -864,6 +1003,14 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
     case kCfg4x2K4: return launch_cfg<4, 2, 4, 4, 4, 2>(p, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_gemm_gelu_quant(const GemmParams& p, int nquant, hipStream_t stream) {
+  if (p.mode != kEpiGeluUp || p.ksplit != 1 || p.gelu_pair_n != (1 << kQuantLogK) || nquant < 1)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles) + static_cast<unsigned>(nquant));
+  gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, true><<<grid, 256, 0, stream>>>(p);
+  return hipGetLastError();
 }
 
 hipError_t launch_gelu_up(const void* g, const void* u, int64_t n, void* y, hipStream_t stream) {

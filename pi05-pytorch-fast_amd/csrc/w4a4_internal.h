@@ -18,6 +18,16 @@ enum EpilogueMode : int {
   kEpiGeluUp = 3,   // paired gate/up tiles -> fp16(gelu_tanh(g) * u)
 };
 
+// Cache warming: up to kMaxWarmBuffers device buffers of n16[i] 16-byte words that a
+// kernel reads and discards with otherwise idle workgroups, so that the next kernel finds
+// them in the memory-side Infinity Cache.
+constexpr int kMaxWarmBuffers = 4;
+struct CacheWarmParams {
+  const void* ptr[kMaxWarmBuffers];
+  int64_t n16[kMaxWarmBuffers];
+  int32_t nbuf;
+};
+
 struct GemmGroup {
   const int32_t* w;  // MFMA-layout payload; fp32 scales at w + N*kblocks128(K)*16, wcorr after them
   void* y;           // fp16 [M, N] output (or int32 for kEpiAcc)
@@ -55,7 +65,30 @@ struct GemmParams {
   _Float16* kv;          // per batch: K then V^T fragments, keys padded to s_pad (zeroed here)
   int32_t seq;           // tokens per batch, a multiple of 8
   int32_t s_pad;         // attn_s_pad(seq)
+  // Down-projection quant riding on the paired gate/up GELU launch (gemm_w4a4_kernel with
+  // QFUSE): the workgroups past the GEMM tiles rotate and quantize the rows of h (group
+  // 0's output, K = gelu_pair_n) into dq / dsa (launch_quantize's layout) as soon as all
+  // n-tiles of a row's 16*MI-row block are stored.  qctl: the launch's control block in
+  // device memory (layout below), zero before the launch and left zero by it; qstatus: a
+  // host-visible word that a bounded wait which ran out sets (or null).
+  int32_t* dq;
+  float* dsa;
+  int32_t* qctl;
+  uint32_t* qstatus;
+  float dinv_sqrt_k;
+  int32_t spin_limit;    // s_sleep rounds a quant workgroup waits for one row block
+  int32_t wait_extra;    // completions waited for beyond ntiles (0; tests force timeouts with 1)
+  CacheWarmParams warm;  // read by the quant workgroups that find no row left
 };
+
+// Control block of the fused gate/up + down-quant launch, in 128-byte lines so that the
+// polled words do not share one (a hot line slows every memory request near it):
+// word 0 the next row to hand out, word 16 the quant workgroups that have left, then the
+// tiles-done counter of m-tile i at word kMlpCtlHeader + kMlpCtlStride * i.  The last
+// quant workgroup to leave resets it to zero.
+constexpr int kMlpCtlExited = 16;
+constexpr int kMlpCtlHeader = 32;
+constexpr int kMlpCtlStride = 32;
 
 // MFMA-fragment-major layout of packed INT4 codes, shared by the weights (r = output
 // column) and the quantized activations (r = row).  The codes of the 16-line block r/16
@@ -121,15 +154,6 @@ enum TileCfg : int {
   kCfg4x2K4 = 9,  // MI 4: 64 x 32
 };
 
-// Cache warming: up to kMaxWarmBuffers device buffers of n16[i] 16-byte words that a
-// kernel reads and discards with otherwise idle workgroups, so that the next kernel finds
-// them in the memory-side Infinity Cache.
-constexpr int kMaxWarmBuffers = 4;
-struct CacheWarmParams {
-  const void* ptr[kMaxWarmBuffers];
-  int64_t n16[kMaxWarmBuffers];
-  int32_t nbuf;
-};
 
 // Prefix attention (attention.hip): head_dim 256, grouped-query heads, fp16.
 constexpr int kAttnHeadDim = 256;
@@ -174,6 +198,9 @@ hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t 
                          int64_t src_stride, int32_t* dst, hipStream_t stream);
 // Chooses the tile configuration; returns the K split used (>= 1) through *ksplit_out.
 hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
+// The paired gate/up GELU GEMM (7x4 tiles, no K split) with the down-projection quant of
+// its output in the same launch (p.dq .. p.warm set; nquant extra workgroups).
+hipError_t launch_gemm_gelu_quant(const GemmParams& p, int nquant, hipStream_t stream);
 hipError_t launch_splitk_reduce(const GemmParams& p, hipStream_t stream);
 // y = fp16(gelu_tanh(g) * u) elementwise on n fp16 values (n >= 1).
 hipError_t launch_gelu_up(const void* g, const void* u, int64_t n, void* y, hipStream_t stream);

@@ -392,6 +392,11 @@ def _fused_decoder_layer_forward(
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)
+    if os.environ.get("PI05_W4A4_FUSE_DOWN_QUANT", "0") == "1":
+        # The down projection's activation quant in the gate/up launch (one launch fewer).
+        y, _ = ext.rms_norm_int4_mlp(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed,
+                                     x2, warm=[mlp.down_proj.packed] if warming else None, unit_offset=off2)
+        return y
     h = ext.rms_norm_int4_gemm2_gelu(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, unit_offset=off2)
     return ext.int4_gemm_residual(h, mlp.down_proj.packed, x2, warm=[mlp.down_proj.packed] if warming else None)
 

@@ -120,6 +120,11 @@ def load_int4_gemm():
         "pi05w4a4_gemm_qkv_rope": (
             ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, vp, i64, i32, vp, vp, vp, vp, vp]),
         "pi05w4a4_permute_rope_pairs": (ctypes.c_int, [vp, i32, vp, vp]),
+        "pi05w4a4_gemm_gelu_up_quant": (
+            ctypes.c_int, [vp, vp, i64, i32, vp, vp, i32, vp, vp, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(sz),
+                           i32, i32, i32, vp]),
+        "pi05w4a4_mlp_ctl_words": (sz, [i64]),
+        "pi05w4a4_mlp_status": (i64, [i32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -472,6 +477,75 @@ def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
         _check(lib.pi05w4a4_rmsnorm_quantize(x2.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0, m, k,
                                              q.data_ptr(), sa.data_ptr(), _stream(dev)), "pi05w4a4_rmsnorm_quantize")
     return q, sa
+
+
+# Control blocks of pi05w4a4_gemm_gelu_up_quant, one per (device, stream): zeroed when
+# allocated and left zeroed by every call that completes.  Calls on one stream are ordered,
+# so they can share one; calls on different streams get their own.
+_MLP_CTL: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _mlp_ctl(lib, device: torch.device, m: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch._C._cuda_getDevice(), _stream(device))
+    ctl = _MLP_CTL.get(key)
+    words = int(lib.pi05w4a4_mlp_ctl_words(m))
+    if ctl is None or ctl.numel() < words:
+        ctl = _MLP_CTL[key] = torch.zeros(max(words, 64), dtype=torch.int32, device=device)
+    return ctl
+
+
+def _check_mlp_status(lib) -> None:
+    """Raise when a bounded wait of an earlier fused gate/up + down-quant call ran out (the
+    kernels set a pinned host word; reading it does not synchronize).  The control blocks
+    are zeroed again so that later calls start clean."""
+    if lib.pi05w4a4_mlp_status(0) > 0:
+        lib.pi05w4a4_mlp_status(1)
+        for ctl in _MLP_CTL.values():
+            ctl.zero_()
+        raise RuntimeError("pi05w4a4_gemm_gelu_up_quant: a bounded wait for a row block ran out in an "
+                           "earlier call; that call's outputs are invalid")
+
+
+def _gemm_gelu_quant_from_q(q, sa, k, w_gate, w_up, n, device, warm=None, spin_limit=0, wait_extra=0):
+    """h = fp16(gelu_tanh(gate) * up) and the down projection's quant of h (codes, scales),
+    from quantized activations (one launch at N = 16384, M > 64)."""
+    lib = _lib if _lib is not None else load_int4_gemm()
+    m = int(sa.size(0))
+    h = torch.empty((m, n), dtype=torch.float16, device=device)
+    dq = torch.empty((_q_words(m, n),), dtype=torch.int32, device=device)
+    dsa = torch.empty((m,), dtype=torch.float32, device=device)
+    wa = _warm_args(warm, "rms_norm_int4_mlp") if warm else None
+    wp, wb, wn = wa if wa is not None else (None, None, 0)
+    ctl = _mlp_ctl(lib, device, m)
+    _check(lib.pi05w4a4_gemm_gelu_up_quant(q.data_ptr(), sa.data_ptr(), m, k, w_gate.data_ptr(), w_up.data_ptr(), n,
+                                           h.data_ptr(), dq.data_ptr(), dsa.data_ptr(), ctl.data_ptr(), wp, wb, wn,
+                                           int(spin_limit), int(wait_extra), _stream(device)),
+           "pi05w4a4_gemm_gelu_up_quant")
+    _check_mlp_status(lib)
+    return h, dq, dsa
+
+
+def _rms_norm_mlp_impl(x, norm_weight, eps, unit_offset, w_gate, w_up, w_down, residual, warm):
+    """The Gemma MLP block of a decoder layer on W4A4 ops: post-attention RMSNorm fused into
+    the gate/up activation quant, gate/up with the GELU-tanh*up epilogue and the down
+    projection's activation quant in one launch, then down with the residual add in its
+    epilogue.  Returns (residual + down(h), h)."""
+    k = _check_x(x)
+    _check_gelu_weights(x, w_gate, w_up)
+    n = int(w_gate.size(0))
+    for w, kw, name in ((w_gate, k, "gate weight"), (w_up, k, "up weight"), (w_down, n, "down weight")):
+        _check_packed(w, kw, name)
+        if not is_mfma_layout(w, kw):
+            raise RuntimeError(f"rms_norm_int4_mlp takes MFMA-layout weights ({name}: [N, {kw // 8 + 16}] "
+                               f"with N % 16 == 0, got {tuple(w.shape)})")
+    _check_residual(residual, x.device, (*x.shape[:-1], int(w_down.size(0))))
+    q, sa = rms_norm_quantize(x, norm_weight, eps, unit_offset)
+    dev = x.device
+    with _on_device(dev):
+        h, dq, dsa = _gemm_gelu_quant_from_q(q, sa, k, w_gate, w_up, n, dev, warm=warm)
+        (y,) = _gemm_from_q(dq, dsa, n, [(w_down, int(w_down.size(0)))], tuple(x.shape[:-1]), dev, "int4_gemm",
+                            residual=residual)
+    return y, h.view(*x.shape[:-1], n)
 
 
 def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False,
@@ -838,6 +912,18 @@ def _register_custom_op() -> None:
     def _int4_gemm_residual_fake(x, packed_w, residual, warm):
         return _fake_out(x, packed_w)
 
+    # Not in the reference: the Gemma MLP block (post norm, gate/up + GELU*up with the down
+    # projection's activation quant in the same launch, down + residual); returns (y, h).
+    @torch.library.custom_op("pi05_w4a4::rms_norm_int4_mlp", mutates_args=())
+    def _rms_norm_int4_mlp(x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
+                           w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor, residual: torch.Tensor,
+                           warm: list[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor]:
+        return _rms_norm_mlp_impl(x, norm_weight, eps, unit_offset, w_gate, w_up, w_down, residual, warm)
+
+    @_rms_norm_int4_mlp.register_fake
+    def _rms_norm_int4_mlp_fake(x, norm_weight, eps, unit_offset, w_gate, w_up, w_down, residual, warm):
+        return _fake_out(x, w_down), _fake_out(x, w_gate)
+
     # Not in the reference: RoPE + attention between int4_gemm3 and o_proj in two kernels.
     @torch.library.custom_op("pi05_w4a4::prefix_attention", mutates_args=())
     def _prefix_attention(
@@ -1019,6 +1105,21 @@ def rms_norm_int4_gemm2_gelu(x, norm_weight, eps, w_gate, w_up, unit_offset=True
                     norm=(norm_weight, float(eps), bool(unit_offset)))[0]
     return torch.ops.pi05_w4a4.rms_norm_int4_gemm2_gelu(x, norm_weight, float(eps), bool(unit_offset),
                                                         w_gate, w_up)
+
+
+def rms_norm_int4_mlp(x, norm_weight, eps, w_gate, w_up, w_down, residual, warm=None, unit_offset=True):
+    """The decoder's MLP block, residual + down(gelu_tanh(gate(n)) * up(n)) with
+    n = rms_norm(x), on W4A4 ops: the norm fused into the gate/up activation quant, the
+    GELU-tanh*up epilogue, the down projection's activation quant in the gate/up launch
+    (``pi05w4a4_gemm_gelu_up_quant``) and the residual add in the down epilogue.  MFMA-layout
+    weights; ``warm``: buffers read into the Infinity Cache by the quant workgroups that
+    find no row left (the down weights, say).  Returns (y, h) with h = the fp16 GELU*up
+    output that the down projection quantized."""
+    if _direct(x, norm_weight, w_gate, w_up, w_down, residual):
+        return _rms_norm_mlp_impl(x, norm_weight, float(eps), bool(unit_offset), w_gate, w_up, w_down, residual,
+                                  warm)
+    return torch.ops.pi05_w4a4.rms_norm_int4_mlp(x, norm_weight, float(eps), bool(unit_offset), w_gate, w_up,
+                                                 w_down, residual, list(warm or []))
 
 
 def int4_gemm_residual(x: torch.Tensor, packed_w: torch.Tensor, residual: torch.Tensor,

@@ -53,7 +53,7 @@ class _Recorder:
 
     NAMES = ("int4_gemm", "int4_gemm_tiled", "int4_gemm2", "int4_gemm2_tiled", "int4_gemm3", "int4_gemm2_gelu",
              "rms_norm_int4_gemm3", "rms_norm_int4_gemm2_gelu", "int4_gemm_residual", "prefix_attention_o_proj",
-             "rms_norm_int4_gemm3_rope", "prefix_attention_o_proj_kv")
+             "rms_norm_int4_gemm3_rope", "prefix_attention_o_proj_kv", "rms_norm_int4_mlp")
 
     def __init__(self, monkeypatch):
         from pi05_fast.w4a4 import extension, linear
@@ -135,11 +135,36 @@ def _check_qkv_rope(cuda, i, args, kwargs, outs) -> None:
     assert torch.equal(kv_got, kv_prep), f"call {i}: fragment-major K/V^T differ from the K/V prep kernel's"
 
 
+def _check_mlp(cuda, i, args, kwargs, outs) -> None:
+    """rms_norm_int4_mlp: h = eager gelu*up of the oracle's gate and up of the oracle's norm
+    of x; y = fp16(oracle(h) @ down + residual), the oracle quantizing h itself."""
+    x, norm_w, eps, w_gate, w_up, w_down, res = args[:7]
+    k = x.shape[-1]
+    xn = orc.rms_norm_lanes(x.reshape(-1, k).cpu().numpy(), norm_w.cpu().numpy(), eps,
+                            unit_offset=kwargs.get("unit_offset", True))
+    g = torch.from_numpy(_oracle_h(xn, w_gate, k)).to(cuda)
+    u = torch.from_numpy(_oracle_h(xn, w_up, k)).to(cuda)
+    h_want = (torch.nn.functional.gelu(g, approximate="tanh") * u).cpu().numpy()
+    y_got, h_got = outs
+    h_np = h_got.reshape(h_want.shape).cpu().numpy()
+    nbad = int(np.count_nonzero(h_np.view(np.int16) != h_want.view(np.int16)))
+    assert nbad == 0, f"call {i} (rms_norm_int4_mlp h): {nbad}/{h_want.size} fp16 outputs differ"
+    n = h_want.shape[1]
+    y_want = _oracle_h(h_np, w_down, n)
+    y_want = (y_want.astype(np.float32) + res.reshape(y_want.shape).cpu().numpy().astype(np.float32)).astype(np.float16)
+    got = y_got.reshape(y_want.shape).cpu().numpy()
+    nbad = int(np.count_nonzero(got.view(np.int16) != y_want.view(np.int16)))
+    assert nbad == 0, f"call {i} (rms_norm_int4_mlp y): {nbad}/{got.size} fp16 outputs differ from the oracle"
+
+
 def _check_call(cuda, i, call) -> None:
     """One recorded W4A4 op against the oracle, bit for bit."""
     name, args, kwargs, outs = call
     if name == "rms_norm_int4_gemm3_rope":
         _check_qkv_rope(cuda, i, args, kwargs, outs)
+        return
+    if name == "rms_norm_int4_mlp":
+        _check_mlp(cuda, i, args, kwargs, outs)
         return
     if name in ("prefix_attention_o_proj", "prefix_attention_o_proj_kv"):
         # the o projection of the attention output it returned (quantized inside the kernel)
@@ -236,6 +261,34 @@ def test_prefix_lm_forward_ops_match_oracle(cuda, monkeypatch, layers, tokens, b
     for i, call in enumerate(rec.calls):
         _check_call(cuda, i, call)
         rec.calls[i] = None  # release the recorded tensors as soon as they are checked
+
+
+@pytest.mark.parametrize("layers,tokens,batch", [(2, 776, 1), (1, 776, 8), (2, 200, 1)])
+def test_prefix_lm_fused_down_quant_ops_match_oracle(cuda, monkeypatch, layers, tokens, batch):
+    """PI05_W4A4_FUSE_DOWN_QUANT=1: the MLP block runs as rms_norm_int4_mlp (the down
+    projection's activation quant in the gate/up launch); every call against the oracle,
+    and the forward equals the one without that fusion bit for bit."""
+    from pi05_fast.w4a4.prefix_lm import prefix_inputs
+
+    print(f"prefix LM forward, fused down quant: {layers} layers x {tokens} tokens x batch {batch}", flush=True)
+    monkeypatch.setenv("PI05_W4A4_FUSE_DOWN_QUANT", "1")
+    model, _ = _build(cuda, layers, fuse_gelu=True, fuse_layer=True)
+    rec = _Recorder(monkeypatch)
+    x = prefix_inputs(batch, tokens, cuda)
+    mask = torch.zeros(batch, 1, tokens, tokens, dtype=torch.float16, device=cuda)
+    with torch.no_grad():
+        y = model(x, mask)
+    torch.cuda.synchronize()
+    kinds = [c[0] for c in rec.calls]
+    assert kinds.count("rms_norm_int4_mlp") == layers and len(kinds) == 3 * layers
+    for i, call in enumerate(rec.calls):
+        _check_call(cuda, i, call)
+        rec.calls[i] = None
+    monkeypatch.setenv("PI05_W4A4_FUSE_DOWN_QUANT", "0")
+    with torch.no_grad():
+        y_unfused = model(x, mask)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_unfused)
 
 
 def test_prefix_lm_fused_gelu_is_bit_exact(cuda):
