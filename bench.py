@@ -26,8 +26,11 @@ launch) comes from the rocprofv3 FETCH_SIZE/WRITE_SIZE summary committed under p
 
 `in_forward` times the same kernels inside the real (eager) forward: HIP events around
 each library call, with a bounded spin kernel queued ahead so that the host has enqueued
-the whole forward before the GPU runs it (no host gaps between kernels);
-`roofline.in_forward` is the dominant kernel's figure from it.
+the whole forward before the GPU runs it (no host gaps between kernels).  What an event
+pair adds to a kernel's interval depends on the kernel, so each class is corrected by its
+own calibration: the same kernel launched alone, timed once by graph replay and once by
+event pairs around eager launches (`pair_offset_us`); `roofline.in_forward` is the
+dominant kernel's figure from it.
 
 `cpu_baseline` times the reference's W4A4 semantics in PyTorch on the host CPU (the
 oracle's torch restatement of pack.py:113-145, both integer matmul forms) on one decoder
@@ -129,7 +132,31 @@ class KernelBench:
             torch.cuda.synchronize()
             per_launch.append(e0.elapsed_time(e1) * 1e3 / iters)
         del graph
-        return statistics.median(per_launch)
+        us = statistics.median(per_launch)
+        self.last_pair_us = self._pair_us(fn)
+        self.last_pair_offset_us = round(self.last_pair_us - us, 3)
+        return us
+
+    def _pair_us(self, fn, reps: int = 40) -> float:
+        """Median interval of an event pair recorded around one eager launch of `fn`, with
+        the queue primed by a bounded spin kernel (the way in_forward_times times each call
+        of the real forward): the launch's time plus what the two markers add to it.  Its
+        difference to the graph-timed launch is the event-pair cost of this kernel, taken off
+        the in-forward times of its class."""
+        torch = self.torch
+        fn()
+        torch.cuda.synchronize()
+        torch.cuda._sleep(50_000_000)  # ~25 ms at ~2 GHz: longer than enqueuing the pairs
+        pairs = []
+        for _ in range(reps):
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            pairs.append((e0, e1))
+        torch.cuda.synchronize()
+        return statistics.median(a.elapsed_time(b) * 1e3 for a, b in pairs)
 
     def _check(self, rc):
         if rc != 0:
@@ -151,7 +178,7 @@ class KernelBench:
         nbytes = 2.0 * m * k + m * k / 2 + 4 * m
         gbs = nbytes / (us * 1e-6) / 1e9
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
-                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "pair_offset_us": self.last_pair_offset_us}
 
     def rmsnorm_quant(self, m, k=2048):
         torch, lib, P = self.torch, self.lib, self.ext._ptr
@@ -164,7 +191,7 @@ class KernelBench:
         nbytes = 2.0 * m * k + 2 * k + m * k / 2 + 4 * m
         gbs = nbytes / (us * 1e-6) / 1e9
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
-                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "pair_offset_us": self.last_pair_offset_us}
 
     def gemm(self, m, k, ns, gelu=False, residual=False, copies=1):
         """One W4A4 GEMM launch shape.  With `copies` > 1 (plain grouped GEMM only), that
@@ -210,7 +237,8 @@ class KernelBench:
         tops = ops / (us * 1e-6) / 1e12
         return {"m": m, "k": k, "n": n, "avg_us": round(us, 3), "ops": ops, "tops": round(tops, 1),
                 "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "bytes": nbytes,
-                "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb}
+                "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb,
+                "pair_offset_us": self.last_pair_offset_us}
 
 
     def gelu_quant(self, m, k=2048, n=16384, fused=True):
@@ -242,7 +270,7 @@ class KernelBench:
             raise RuntimeError("a bounded wait of the fused gate/up + down quant ran out")
         ops = 2.0 * m * 2 * n * k
         return {"m": m, "k": k, "n": 2 * n, "avg_us": round(us, 3), "ops": ops, "launches": 1 if fused else 2,
-                "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+                "tops": round(ops / (us * 1e-6) / 1e12, 1), "pair_offset_us": self.last_pair_offset_us}
 
     def qkv_rope(self, b, s, h=2048):
         """The QKV GEMMs with RoPE and the attention's K/V layout in the epilogue
@@ -267,7 +295,7 @@ class KernelBench:
             self._stream())))
         ops = 2.0 * m * 2560 * h
         return {"m": m, "k": h, "n": 2560, "avg_us": round(us, 3), "ops": ops,
-                "tops": round(ops / (us * 1e-6) / 1e12, 1)}
+                "tops": round(ops / (us * 1e-6) / 1e12, 1), "pair_offset_us": self.last_pair_offset_us}
 
     def attention(self, b, s, h=8, kvh=1):
         """The two prefix-attention kernels (K RoPE + V transpose, then attention) at one
@@ -293,6 +321,7 @@ class KernelBench:
         prep()
         us_prep = self._time(prep)
         us_attn = self._time(attn)
+        attn_offset = self.last_pair_offset_us
         flops = 4.0 * b * h * s * s * d
         s_pad = (s + 63) // 64 * 64
         # Bytes that cross each workgroup's vector-memory path: every workgroup streams all
@@ -303,7 +332,7 @@ class KernelBench:
         return {
             "attention": {"b": b, "s": s, "h": h, "kvh": kvh, "avg_us": round(us_attn, 3), "flops": flops,
                           "tflops": round(tflops, 2), "frac_fp16_peak": round(tflops / FP16_PEAK_TFLOPS, 4),
-                          "workgroups": wgs, "bytes_per_workgroup": per_wg,
+                          "workgroups": wgs, "bytes_per_workgroup": per_wg, "pair_offset_us": attn_offset,
                           "l2_to_cu_gbs": round(wgs * per_wg / (us_attn * 1e-6) / 1e9, 1)},
             "attn_kv_prep": {"avg_us": round(us_prep, 3),
                              "bytes": 2.0 * b * s * kvh * d * 2 * 2 + 2.0 * b * s * d * 2},
@@ -362,6 +391,8 @@ def _in_forward_label(fn_name: str, args: tuple, kwargs: dict) -> str:
         return "rmsnorm_quant_k2048"
     if fn_name == "_gemm_qkv_rope":
         return "qkv_rope"
+    if fn_name == "_gemm_gelu_quant_from_q":
+        return "gate_up_gelu_quant"
     return "attention" if kwargs.get("kv_mfma") is not None else "attention_with_kv_prep"
 
 
@@ -372,9 +403,10 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
     ahead of each forward holds the GPU until the host has enqueued the whole forward, so
     the kernels run back to back with no host gaps, in the cache state the forward leaves
     them (preceding kernels, weight cache warming) and the event pairs time the kernels
-    alone.  `avg_us` is the mean pair interval less that of an empty pair (`event_pair_us`,
-    the markers' own cost); `raw_avg_us` keeps it."""
-    names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl", "_gemm_qkv_rope")
+    alone.  `raw_avg_us` is the mean pair interval; `calibrate_in_forward` takes off it
+    the event-pair cost that the same kernel shows when launched alone (`avg_us`)."""
+    names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl", "_gemm_qkv_rope",
+             "_gemm_gelu_quant_from_q")
     orig = {n: getattr(ext, n) for n in names}
     records = []
 
@@ -421,8 +453,10 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
     finally:
         for n in names:
             setattr(ext, n, orig[n])
-    # An event pair costs time of its own (two marker packets on the queue): the interval
-    # of a pair with nothing between it, measured the same way, is taken off each call.
+    # An event pair costs time of its own (two marker packets on the queue; an empty pair's
+    # interval is reported as event_pair_us), but how much of it adds to a kernel's
+    # interval depends on the kernel: calibrate_in_forward corrects each class with its
+    # own isolated launches.
     torch.cuda.synchronize()
     torch.cuda._sleep(int(10.0 / ms_per_mcycle * 1e6))
     empty = []
@@ -436,10 +470,21 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
     per = {}
     for label, a, b in records:
         per.setdefault(label, []).append(a.elapsed_time(b) * 1e3)
-    out = {lab: {"calls_per_forward": len(v) // reps, "avg_us": round(statistics.fmean(v) - pair_us, 3),
-                 "raw_avg_us": round(statistics.fmean(v), 3)} for lab, v in per.items()}
+    out = {lab: {"calls_per_forward": len(v) // reps, "raw_avg_us": round(statistics.fmean(v), 3)}
+           for lab, v in per.items()}
     return {"kernels": out, "reps": reps, "queue_primed": primed, "spin_ms": round(spin_ms, 2),
             "event_pair_us": round(pair_us, 3)}
+
+
+def calibrate_in_forward(in_fwd: dict, offsets: dict) -> None:
+    """avg_us of each in-forward kernel class = its raw event-pair interval less the
+    event-pair cost its kernel shows alone (pair interval of an eager launch minus the
+    graph-timed launch, `pair_offset_us` of the kernel table; the attention class uses the
+    prefix-attention kernel's).  Classes without a calibration keep the raw interval."""
+    for label, rec in in_fwd["kernels"].items():
+        off = offsets.get(label)
+        rec["pair_offset_us"] = off
+        rec["avg_us"] = round(rec["raw_avg_us"] - (off or 0.0), 3)
 
 
 def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
@@ -702,6 +747,10 @@ def main() -> int:
         sweep = qkv_m_sweep(kb)
         others = kb.attention(args.batch, args.tokens)
         others["rmsnorm"] = kb.rmsnorm(m)
+        offsets = {name: rec.get("pair_offset_us") for name, rec in kernels.items()}
+        offsets["attention"] = others["attention"]["pair_offset_us"]
+        offsets["attention_with_kv_prep"] = others["attention"]["pair_offset_us"]
+        calibrate_in_forward(in_fwd, offsets)
 
         # The other prefix lengths and the batch-8 throughput point of the same workload,
         # and the 776-token forward with transformers' fp16 eager attention instead of the

@@ -251,6 +251,9 @@ int pi05w4a4_int4_gemm(const void* x_fp16, int64_t m, int32_t k, const int32_t* 
  * a call whose buffers would exceed the scratch size fails with PI05W4A4_EINVAL before
  * any launch.  Every call on one GPU shares that GPU's scratch: calls that overlap on one
  * device (other streams, other host threads) race and must be serialised by the caller.
+ * Footprint: the scratch is a static device array of the library, so every GPU that the
+ * library is loaded on reserves these 64 MiB of HBM until the process ends, whether or not
+ * this entry point is called.
  */
 #define PI05W4A4_NOALLOC_SCRATCH_BYTES (64u << 20)
 int pi05w4a4_int4_gemm_noalloc(const void* x_fp16, int64_t m, int32_t k, const int32_t* w_mfma,

@@ -513,10 +513,15 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       const int32_t* wcorr = ((GELU && ni >= NI / 2) ? W2 : W) + N * scale_off + N;
       wc[ni] = *reinterpret_cast<const v4i*>(wcorr + min(col, N - 16) + (lane >> 4) * 4);
     }
+    // The selection is applied to the MI + NI correction vectors, not to the MI x NI sums.
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi) qc[mi] = first_part ? qc[mi] : 0;
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) wc[ni] = first_part ? wc[ni] : v4i{0, 0, 0, 0};
 #pragma unroll
     for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = first_part ? (wc[ni] + qc[mi]) : v4i{0, 0, 0, 0};
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = wc[ni] + qc[mi];
   }
 
   // QKV attention prep, small tiles (2 x 2 fragments per wave): the K group's rotary

@@ -116,13 +116,13 @@ __device__ __forceinline__ uint32_t quant_pack8(const float (&v)[8], float sdiv)
 }
 
 // Same eight codes without a division per element.  qa = fl(v * rcp(sdiv) + 8) (one
-// fused rounding) differs from the exact q + 8, q = v / sdiv, by less than 1.2e-6: |q| <= 7,
-// the hardware reciprocal's relative error is at most 0.77 * 2^-23 (9.2e-8, measured on
-// gfx950 over every float in [1, 2) and a sample of the binades 2^-40 .. 2^40), so v * rcp
-// is within 6.4e-7 of q, and the fma rounds once at an ulp of at most 2^-20 (<= 4.8e-7).
+// fused rounding) differs from the exact q + 8, q = v / sdiv, by less than 1.31e-6:
+// |q| <= 7 and v_rcp_f32 is documented to 1 ulp, a relative error of at most 2^-23, so
+// v * rcp is within 7 * 2^-23 (8.3e-7) of q; the fma adds 8 exactly and rounds once, at an
+// ulp of at most 2^-20 for results below 16 (error <= 2^-21, 4.8e-7).
 // rint(q + 8) == rint(q) + 8 (8 is even, so ties still go to even), so rint(qa) - 8 ==
-// rint(q) unless q lies within 1.2e-6 of a half-integer.  Any lane that sees qa within
-// 3e-6 of one (2.5 times that bound) raises `near_tie` for this word; the caller then
+// rint(q) unless q lies within 1.31e-6 of a half-integer.  Any lane that sees qa within
+// 3e-6 of one (more than twice that bound) raises `near_tie` for this word; the caller then
 // redoes that word's codes with quant_pack8 (exact division).  Both paths therefore
 // produce the reference's round-half-even codes bit for bit.  One slow row sets a
 // launch's end, so the redo is kept small: a 3e-6 window (1e-5 before) and only the
