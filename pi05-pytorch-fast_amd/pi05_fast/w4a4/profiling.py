@@ -3,6 +3,7 @@
     python -m pi05_fast.w4a4.profiling trace <kernel_trace.csv> [--match REGEX] [--top N]
     python -m pi05_fast.w4a4.profiling counters <counter_collection.csv> ... [--match REGEX]
     python -m pi05_fast.w4a4.profiling forward <kernel_trace.csv> [--steps N]
+    python -m pi05_fast.w4a4.profiling traffic <FETCH_SIZE counters.csv> <WRITE_SIZE counters.csv>
 
 ``trace`` reads a ``rocprofv3 --kernel-trace --output-format csv`` file and lists, per
 kernel and grid, the launch count and the mean / median / min duration.  ``forward``
@@ -26,7 +27,10 @@ median of each counter over the dispatches and the figures derived from them on 
     fetch_kib / write_kib = FETCH_SIZE / WRITE_SIZE per dispatch
 
 The duration of a counter dispatch is its End - Start timestamp in that (serialised)
-run, so it can exceed the kernel's time in a plain trace.
+run, so it can exceed the kernel's time in a plain trace.  ``traffic`` takes the
+FETCH_SIZE run and the WRITE_SIZE run of ``bench.py --only-kernel ...,copy`` and prints
+each 776-token kernel class's HBM-side bytes per launch, scaled by what the same counter
+reads for the 64 MiB device copy, against its algorithmic bytes.
 """
 
 from __future__ import annotations
@@ -224,6 +228,75 @@ def counter_table(paths: list[str], match: str | None = None) -> str:
     return "\n".join(out)
 
 
+def _gemm_alg_bytes(m: int, k: int, n: int, out_bytes: float) -> float:
+    """Codes + scales/corrections of A and B, plus the output (as bench.py counts them)."""
+    return m * k / 2 + 4 * m + n * k / 2 + 4 * n + out_bytes
+
+
+# The kernel classes of the 776-token prefix-LM forward (one decoder layer's launches):
+# class -> (kernel name, workgroups, algorithmic bytes, what they are).
+_M = 776
+TRAFFIC_CLASSES = {
+    "gate_up_gelu": ("gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false>", 896,
+                     _gemm_alg_bytes(_M, 2048, 32768, 2.0 * _M * 16384),
+                     "codes A 0.79 MB + gate and up weights 33.55 MB + scales/corrections; fp16 h 25.43 MB"),
+    "gate_up": ("gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false>", 896,
+                _gemm_alg_bytes(_M, 2048, 32768, 2.0 * _M * 32768),
+                "codes A 0.79 MB + weights 33.55 MB + scales/corrections; fp16 gate and up 50.86 MB"),
+    "down_residual": ("gemm_w4a4_kernel<7, 4, 8, 8, false, 2, 2, false, false>", 224,
+                      _gemm_alg_bytes(_M, 16384, 2048, 2.0 * 2.0 * _M * 2048),
+                      "codes A 6.36 MB + down weights 16.78 MB + scales/corrections + fp16 residual 3.18 MB; "
+                      "fp16 out 3.18 MB"),
+    "qkv": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false>", 500,
+            _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560), "codes A 0.79 MB + weights 2.62 MB; fp16 q/k/v 3.97 MB"),
+    "qkv_rope": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, true, false>", 500,
+                 _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560) + 2 * _M * 256 * 2 * 2 + 2 * 832 * 256 * 2,
+                 "as qkv + rotary tables 0.79 MB read + key states 0.40 MB and K/V^T 0.85 MB written"),
+    "o_residual": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false>", 400,
+                   _gemm_alg_bytes(_M, 2048, 2048, 2.0 * 2.0 * _M * 2048),
+                   "codes A 0.79 MB + weights 2.10 MB + residual 3.18 MB; out 3.18 MB"),
+    "quant_k16384": ("fwht_quant_kernel<14, 8, 1, false>", 776, 2.0 * _M * 16384 + _M * 16384 / 2 + 4 * _M,
+                     "fp16 x 25.43 MB; codes 6.36 MB + scales"),
+    "rmsnorm_quant_k2048": ("fwht_quant_kernel<11, 6, 4, true>", 194, 2.0 * _M * 2048 + 2 * 2048 + _M * 2048 / 2 + 4 * _M,
+                            "fp16 x 3.18 MB + norm weight; codes 0.79 MB + scales"),
+}
+COPY_KIB = 65536.0  # the calibration copy (bench.py --only-kernel copy): 64 MiB read and written
+
+
+def _mean_counter(res: dict, counter: str, name: str, grid: int) -> tuple[float, int]:
+    for (kn, wgs, _), cs in res.items():
+        if name in kn and wgs == grid and counter in cs:
+            return statistics.fmean(cs[counter]), len(cs[counter])
+    raise KeyError(f"{counter} of {name} with {grid} workgroups not in the counter file")
+
+
+def traffic_table(fetch_csv: str, write_csv: str) -> str:
+    """FETCH_SIZE / WRITE_SIZE per launch of each class, scaled by what the same counters
+    read for the 64 MiB device copy of the same runs (``__amd_rocclr_copyBuffer`` with 256
+    workgroups), against the algorithmic bytes; ends with the ``traffic_bytes_per_launch``
+    lines that bench.py reads."""
+    rf, rw = read_counters([fetch_csv]), read_counters([write_csv])
+    cf, ncf = _mean_counter(rf, "FETCH_SIZE", "copyBuffer", 256)
+    cw, ncw = _mean_counter(rw, "WRITE_SIZE", "copyBuffer", 256)
+    sf, sw = COPY_KIB / cf, COPY_KIB / cw
+    out = [f"Calibration: the 64 MiB copy reads FETCH_SIZE {cf:.1f} KiB (n={ncf}) and WRITE_SIZE {cw:.1f} KiB "
+           f"(n={ncw}) per dispatch, so FETCH_SIZE is scaled by {sf:.4f} and WRITE_SIZE by {sw:.4f}.", "",
+           "| class | kernel | FETCH_SIZE KiB (mean) | WRITE_SIZE KiB (mean) | read MB (scaled) | write MB (scaled) "
+           "| total MB | algorithmic MB | ratio | algorithmic bytes |",
+           "|---|---|---:|---:|---:|---:|---:|---:|---:|---|"]
+    tb = {}
+    for cls, (kn, grid, alg, what) in TRAFFIC_CLASSES.items():
+        f, nf = _mean_counter(rf, "FETCH_SIZE", kn, grid)
+        w, nw = _mean_counter(rw, "WRITE_SIZE", kn, grid)
+        rb, wb = f * 1024 * sf, w * 1024 * sw
+        tb[cls] = rb + wb
+        out.append(f"| {cls} | `{kn}` {grid} WGs | {f:.1f} (n={nf}) | {w:.1f} (n={nw}) | {rb / 1e6:.2f} | "
+                   f"{wb / 1e6:.2f} | {(rb + wb) / 1e6:.2f} | {alg / 1e6:.2f} | {(rb + wb) / alg:.2f} | {what} |")
+    out.append("")
+    out.extend(f"traffic_bytes_per_launch[{k}]: {v:.0f}" for k, v in tb.items())
+    return "\n".join(out)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description="rocprofv3 summaries for the W4A4 kernels")
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -237,11 +310,16 @@ def main(argv=None) -> int:
     c = sub.add_parser("counters")
     c.add_argument("csv", nargs="+")
     c.add_argument("--match", default=None)
+    tr = sub.add_parser("traffic")
+    tr.add_argument("fetch_csv")
+    tr.add_argument("write_csv")
     a = ap.parse_args(argv)
     if a.cmd == "trace":
         print(trace_table(a.csv, a.match, a.top))
     elif a.cmd == "forward":
         print(forward_table(a.csv, a.steps))
+    elif a.cmd == "traffic":
+        print(traffic_table(a.fetch_csv, a.write_csv))
     else:
         print(counter_table(a.csv, a.match))
     return 0
