@@ -369,6 +369,46 @@ int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_m
                                    const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
                                    void* stream);
 
+/*
+ * E3M2 operand form of the gate/up GEMM.  The same INT4 codes, held on the device as OCP
+ * FP6 E3M2 values (every integer in [-8, 8] is one), feed gfx950's
+ * v_mfma_f32_16x16x128_f8f6f4: half the int8 MFMA's issue time for the same work and no
+ * nibble unpack; its fp32 sums of integer products stay below 2^24, so they equal the int32
+ * accumulators of pi05w4a4_gemm bit for bit and every output is the same fp16 value.  An
+ * alternative on-device form of the reference's int4_gemm2 / int4_gemm2_tiled for its
+ * gate/up weights (int4_gemm.cu:533-564, 618-642; apply.py:135-138); no other counterpart.
+ *   q6   activation codes, one 1536-byte fragment per 16 rows x 128 k: fragment (mb, kb) at
+ *        byte (mb*KB + kb)*1536 (KB = K/128); bytes [0, 1024) hold dwords 0-3 of lane L at
+ *        16 L, bytes [1024, 1536) dwords 4-5 of lane L at 1024 + 8 L, where lane L's six
+ *        dwords hold codes 128 kb + 32 (L/16) .. +31 of row 16 mb + L%16, code j in bits
+ *        6j .. 6j+5 (E3M2: sign bit 5, exponent bits 4-2 with bias 3, mantissa bits 1-0).
+ *        pi05w4a4_q_e3m2_bytes(M, K) bytes, 16-byte aligned; no row corrections.
+ *   w6   weights, int32 [N, 3K/16 + 16] (pi05w4a4_e3m2_words(N, K) words used): column
+ *        pair p (columns 32p .. 32p+31) and k block kb form 3072 bytes at (p*KB + kb)*3072,
+ *        three 1 KB chunks; chunk c holds bytes 16c .. 16c+15 of lane L's 48-byte record
+ *        [six dwords of column 32p + L%16 | six dwords of column 32p + 16 + L%16] (codes
+ *        as in q6) at 16 L.  The N fp32 column scales follow at word N*KB*24.
+ * Shapes: K = 2048 for the quantizers (the gate/up input); K % 128 == 0, K <= 2^18 for the
+ * GEMM; N % 32 == 0.
+ *
+ * pi05w4a4_repack_weight_e3m2: an MFMA-layout weight (pi05w4a4_repack_weight's output) ->
+ *   w6, not in place (load time).
+ * pi05w4a4_quantize_e3m2 / pi05w4a4_rmsnorm_quantize_e3m2: pi05w4a4_quantize /
+ *   pi05w4a4_rmsnorm_quantize with the codes written as q6 (the same codes and scales).
+ * pi05w4a4_gemm_e3m2: gelu_up = 0: pi05w4a4_gemm_multi of 1..3 w6 weights (n[g] columns
+ *   into y[g]); gelu_up = 1: pi05w4a4_gemm_gelu_up (ngroups = 2: gate, up with
+ *   n[0] == n[1]; y[0] = fp16(gelu_tanh(gate) * up)).  One launch, no workspace.
+ */
+size_t pi05w4a4_q_e3m2_bytes(int64_t m, int32_t k);
+size_t pi05w4a4_e3m2_words(int32_t n, int32_t k);
+int pi05w4a4_repack_weight_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int32_t* w6, void* stream);
+int pi05w4a4_quantize_e3m2(const void* x_fp16, int64_t m, int32_t k, void* q6, float* sa, void* stream);
+int pi05w4a4_rmsnorm_quantize_e3m2(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                   int64_t m, int32_t k, void* q6, float* sa, void* stream);
+int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, int32_t ngroups,
+                       const int32_t* const* w6, const int32_t* n, void* const* y_fp16, int32_t gelu_up,
+                       void* stream);
+
 #ifdef __cplusplus
 }
 #endif

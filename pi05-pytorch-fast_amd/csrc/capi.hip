@@ -278,7 +278,7 @@ namespace {
 
 // Validates the warm-buffer arguments of the cache-warming entry points and collects the
 // non-empty buffers.
-int collect_warm(const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
+static int collect_warm(const void* const* warm_ptrs, const size_t* warm_bytes, int32_t warm_n,
                  w4a4::CacheWarmParams* warm) {
   *warm = w4a4::CacheWarmParams{};
   if (warm_n < 0 || warm_n > w4a4::kMaxWarmBuffers)
@@ -296,7 +296,7 @@ int collect_warm(const void* const* warm_ptrs, const size_t* warm_bytes, int32_t
   return ok();
 }
 
-int quantize_call(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
+static int quantize_call(const void* x_fp16, int64_t m, int32_t k, int32_t* q, float* sa,
                   const w4a4::CacheWarmParams* warm, void* stream) {
   if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
   if (k <= 0 || k % 64 != 0) return fail(PI05W4A4_EINVAL, "K must be a multiple of 64, got %d", k);
@@ -482,6 +482,118 @@ int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
                     "rmsnorm quantize launch");
 }
 
+// ---- E3M2 operand form (the q6 / w6 layouts of w4a4_internal.h)
+
+size_t pi05w4a4_q_e3m2_bytes(int64_t m, int32_t k) {
+  if (m <= 0 || k <= 0) return 0;
+  return static_cast<size_t>(w4a4::q6_bytes(cdiv(m, 16), w4a4::kblocks128(k)));
+}
+
+size_t pi05w4a4_e3m2_words(int32_t n, int32_t k) {
+  if (n <= 0 || k <= 0) return 0;
+  return static_cast<size_t>(w4a4::w6_payload_words(n, w4a4::kblocks128(k))) + static_cast<size_t>(n);
+}
+
+namespace {
+// The fp32 sums of the E3M2 MFMA are exact while |acc| <= 64 K < 2^24.
+constexpr int32_t kMaxKE3m2 = 1 << 18;
+
+static int validate_e3m2_shape(int32_t n, int32_t k, const char* name) {
+  if (k <= 0 || k % 128 != 0 || k > kMaxKE3m2)
+    return fail(PI05W4A4_EINVAL, "%s: E3M2 operands need K %% 128 == 0 and K <= %d, got %d", name, kMaxKE3m2, k);
+  if (n <= 0 || n % 32 != 0 || n > kMaxN)
+    return fail(PI05W4A4_EINVAL, "%s: E3M2 weights need N %% 32 == 0 (column pairs) and N <= %d, got %d", name,
+                kMaxN, n);
+  return PI05W4A4_OK;
+}
+
+static int quantize_e3m2_call(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset, int64_t m,
+                              int32_t k, void* q6, float* sa, void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (k != 2048) return fail(PI05W4A4_EINVAL, "the E3M2 quantizer takes K = 2048, got %d", k);
+  if (m == 0) return ok();
+  if (!x_fp16 || !q6 || !sa) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (!aligned(x_fp16, 16) || (w_fp16 != nullptr && !aligned(w_fp16, 16)) || !aligned(q6, 16) || !aligned(sa, 4))
+    return fail(PI05W4A4_EINVAL, "x, w and q6 must be 16-byte aligned, sa 4-byte aligned");
+  if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
+  return hip_status(w4a4::launch_quantize_e3m2(x_fp16, w_fp16, eps, unit_offset != 0, m, k, q6, sa,
+                                               static_cast<float>(1.0 / std::sqrt(2048.0)),
+                                               static_cast<hipStream_t>(stream)),
+                    "E3M2 quantize launch");
+}
+}  // namespace
+
+int pi05w4a4_repack_weight_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int32_t* w6, void* stream) {
+  if (w_mfma == nullptr || w6 == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (w_mfma == w6) return fail(PI05W4A4_EINVAL, "the E3M2 repack is not in place");
+  const int rc = validate_e3m2_shape(n, k, "weight");
+  if (rc) return rc;
+  if (!aligned(w_mfma, 16) || !aligned(w6, 16)) return fail(PI05W4A4_EINVAL, "weights must be 16-byte aligned");
+  return hip_status(w4a4::launch_repack_e3m2(w_mfma, n, k, w6, static_cast<hipStream_t>(stream)),
+                    "E3M2 repack launch");
+}
+
+int pi05w4a4_quantize_e3m2(const void* x_fp16, int64_t m, int32_t k, void* q6, float* sa, void* stream) {
+  return quantize_e3m2_call(x_fp16, nullptr, 0.0f, 0, m, k, q6, sa, stream);
+}
+
+int pi05w4a4_rmsnorm_quantize_e3m2(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                   int64_t m, int32_t k, void* q6, float* sa, void* stream) {
+  if (m > 0 && w_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  return quantize_e3m2_call(x_fp16, w_fp16, eps, unit_offset, m, k, q6, sa, stream);
+}
+
+int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, int32_t ngroups,
+                       const int32_t* const* w6, const int32_t* n, void* const* y_fp16, int32_t gelu_up,
+                       void* stream) {
+  if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
+  if (w6 == nullptr || n == nullptr || y_fp16 == nullptr)
+    return fail(PI05W4A4_EINVAL, "null pointer argument");
+  if (gelu_up != 0 ? ngroups != 2 : (ngroups < 1 || ngroups > w4a4::kMaxGroups))
+    return fail(PI05W4A4_EINVAL, "ngroups must be 2 with gelu_up, else 1..3, got %d", ngroups);
+  if (gelu_up != 0 && n[0] != n[1])
+    return fail(PI05W4A4_EINVAL, "gate and up weights must have the same N (%d != %d)", n[0], n[1]);
+  for (int g = 0; g < ngroups; ++g) {
+    int rc = validate_e3m2_shape(n[g], k, "weight");
+    if (rc) return rc;
+    if (w6[g] == nullptr || !aligned(w6[g], 16)) return fail(PI05W4A4_EINVAL, "weights must be non-null and 16-byte aligned");
+    if (g < (gelu_up != 0 ? 1 : ngroups) && m > 0 && (y_fp16[g] == nullptr || !aligned(y_fp16[g], 16)))
+      return fail(PI05W4A4_EINVAL, "outputs must be non-null and 16-byte aligned");
+  }
+  if (m == 0) return ok();
+  if (q6 == nullptr || sa == nullptr) return fail(PI05W4A4_EINVAL, "null activation codes or scales");
+  if (!aligned(q6, 16) || !aligned(sa, 4))
+    return fail(PI05W4A4_EINVAL, "q6 must be 16-byte aligned, sa 4-byte aligned");
+  const int64_t mtiles = cdiv(m, 112);
+  if (mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
+  w4a4::GemmParams p{};
+  p.q = static_cast<const int32_t*>(q6);
+  p.sa = sa;
+  p.m = m;
+  p.k = k;
+  p.ngroups = ngroups;
+  const int tile_cols = gelu_up != 0 ? 128 : 256;  // 4 waves x 64 columns (GELU: 32 gate + 32 up)
+  int tile_begin = 0;
+  int64_t n_total = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    p.g[g].w = w6[g];
+    p.g[g].y = gelu_up != 0 ? y_fp16[0] : y_fp16[g];
+    p.g[g].n = n[g];
+    p.g[g].tile_begin = tile_begin;
+    tile_begin += static_cast<int>(cdiv(n[g], tile_cols));
+    n_total += n[g];
+  }
+  p.ntiles = gelu_up != 0 ? static_cast<int32_t>(cdiv(n[0], tile_cols)) : tile_begin;
+  p.mtiles = static_cast<int32_t>(mtiles);
+  p.ksplit = 1;
+  p.kblocks_per_split = w4a4::kblocks128(k);
+  p.mblocks = static_cast<int32_t>(cdiv(m, 16));
+  p.n_total = static_cast<int32_t>(n_total);
+  p.gelu_pair_n = gelu_up != 0 ? n[0] : 0;
+  p.mode = gelu_up != 0 ? w4a4::kEpiGeluUp : w4a4::kEpiFp16;
+  return hip_status(w4a4::launch_gemm_e3m2(p, static_cast<hipStream_t>(stream)), "E3M2 gemm launch");
+}
+
 int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t k,
                           const int32_t* w_gate_mfma, const int32_t* w_up_mfma, int32_t n,
                           void* h_fp16, void* workspace, size_t workspace_bytes, void* stream) {
@@ -514,7 +626,7 @@ std::mutex g_status_mu;
 uint32_t* g_status_host = nullptr;
 uint32_t* g_status_dev = nullptr;
 
-uint32_t* mlp_status_device_word() {
+static uint32_t* mlp_status_device_word() {
   std::lock_guard<std::mutex> lk(g_status_mu);
   if (g_status_dev != nullptr) return g_status_dev;
   void* hp = nullptr;

@@ -55,6 +55,8 @@
 // accumulators, and paired gate/up tiles finished exactly as the eager
 // `gelu(gate, approximate="tanh") * up` on the fp16 gate and up (apply.py:135-138).
 
+#include <type_traits>
+
 #include "cache_warm.h"
 #include "gelu_tanh.h"
 #include "quant_row.h"
@@ -64,6 +66,8 @@ namespace w4a4 {
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -132,6 +136,17 @@ __device__ __forceinline__ _Float16 dequant(int32_t acc, float sa, float sw) {
   asm volatile("" : "+v"(y));
   return static_cast<_Float16>(y);
 }
+
+// The same from an fp32 accumulator that already holds acc exactly (the E3M2 MFMA's
+// integer-valued fp32 sums): the identical two products and conversion.
+__device__ __forceinline__ _Float16 dequant(float acc, float sa, float sw) {
+  float y = __fmul_rn(__fmul_rn(acc, sa), sw);
+  asm volatile("" : "+v"(y));
+  return static_cast<_Float16>(y);
+}
+
+// E3M2 operand of one fragment from six consecutive dwords (the upper two are unused).
+__device__ __forceinline__ v8i e3m2_op(v4i lo, int d4, int d5) { return v8i{lo.x, lo.y, lo.z, lo.w, d4, d5, 0, 0}; }
 
 // RoPE of four dimension pairs (d, d + 128), each product and sum rounded to fp16 as
 // torch's (x * cos) + (rotate_half(x) * sin) on fp16 tensors (attention.hip's rope_pair).
@@ -252,9 +267,25 @@ __device__ __forceinline__ void down_quant_role(const GemmParams& p, char* lds) 
   }
 }
 
-template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false, bool QFUSE = false>
+// E3M2: both operands in the E3M2 layouts of w4a4_internal.h (q6 fragments, w6 column
+// pairs) and v_mfma_f32_16x16x128_f8f6f4: one MFMA per fragment pair and 128-deep k block
+// (half the int8 MFMA issue time for the same work) and no unpack.  Its operands take
+// 1.5x the bytes of INT4 codes, and a CU's vector-memory path delivers about one 64-lane
+// 16-byte load per ~28 clocks, so the A fragments, which the four waves of the workgroup
+// share, are staged once per workgroup in a double-buffered LDS tile by direct
+// global-to-LDS loads (11 1 KB chunks per k block, dealt over the waves), and only the B
+// column pairs stream per wave (three 16-byte loads per pair).  Step kb: wait for this
+// wave's loads, workgroup barrier (every wave's A(kb) chunks are in LDS; every wave has
+// read slot kb + 1 in step kb - 1), read A(kb) from LDS, issue A(kb + 1) and B(kb + 1),
+// then the 28 MFMAs.  All LDS reads of a step precede its LDS-bound loads, so the
+// compiler's conservative wait on those loads never lands before a read.  The fp32
+// accumulators start at zero and end at acc exactly (no 16x factor, no corrections).
+template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false, bool QFUSE = false,
+          bool E3M2 = false>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!(GELU && QKV_PREP), "the attention prep is a fp16 epilogue");
+  static_assert(!E3M2 || (MI == 7 && NI == 4 && NWAVES == 4 && KW == 1 && !QKV_PREP && !QFUSE),
+                "E3M2 operands: 112 x 256 tiles, four waves along N");
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
@@ -283,7 +314,9 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   constexpr int kLdsSw = kLdsSa + TROWS * 4;
   constexpr int kLdsRed = kLdsSw + NCOL * 4;
   constexpr int kLdsStage = kLdsRed + (kSpread ? KW * PM * NI * 64 * 16 : 0);
-  constexpr int kLdsGemm = kLdsStage + (kSpread ? KW : NW) * 16 * LSR * 2;
+  constexpr int kLdsA6 = (kLdsStage + (kSpread ? KW : NW) * 16 * LSR * 2 + 15) / 16 * 16;
+  constexpr int kA6Stage = 7 * 1024 + 4 * 1024;  // 7 d0-3 chunks, 4 chunks of d4-5 parts (3.5 KB used)
+  constexpr int kLdsGemm = kLdsA6 + (E3M2 ? 2 * kA6Stage : 0);
   constexpr int kLdsPool = (QFUSE && kQuantLdsBytes > kLdsGemm) ? kQuantLdsBytes : kLdsGemm;
   __shared__ __align__(16) char lds_pool[kLdsPool];
   int8_t* const fix_lds = reinterpret_cast<int8_t*>(lds_pool + kLdsFix);
@@ -399,7 +432,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 
   const int K = p.k;
   const int KB128 = kblocks128(K);
-  const int64_t scale_off = static_cast<int64_t>(KB128) * 16;  // words per weight column
+  // Words per weight column before the scales: 16 per k block (INT4), 24 (E3M2).
+  const int64_t scale_off = static_cast<int64_t>(KB128) * (E3M2 ? 24 : 16);
   const int64_t M = p.m;
   const int64_t m0 = static_cast<int64_t>(mt) * (16 * MI);
   // First output column of this wave (within the group).  In GELU mode a wave covers
@@ -445,7 +479,8 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   }
   const int nkb = kb_end - kb_begin;
 
-  v4i acc[MI][NI];
+  using AccV = std::conditional_t<E3M2, v4f, v4i>;
+  AccV acc[MI][NI];
 
   // ---- main loop: A and B straight from global memory into a 2-deep register ring.
   // Each load is a scalar fragment base plus one shared unsigned 32-bit lane offset
@@ -493,14 +528,19 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   };
   // The first ring load is unconditional: with nkb == 0 it reads the clamped block
   // kb_end - 1 >= 0 and is never used.
-  load(kb_begin, ra[0], rb[0]);
+  if constexpr (!E3M2) load(kb_begin, ra[0], rb[0]);
 
   // Accumulators start at the correction terms, qcorr[row] + wcorr[col], so that they end
   // at 16 * acc exactly (S + qcorr + wcorr).  Only the first k part of the first K slice
   // carries them: the other parts' sums are added to it.  Lane L owns rows 16*mi + L%16
   // and columns 16*ni + 4*(L/16) + 0..3 of its wave tile (see the epilogue).  Rows and
   // columns past the matrix read clamped, in-bounds words and are never stored.
-  {
+  if constexpr (E3M2) {
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = AccV{0, 0, 0, 0};
+  } else {
     const bool first_part = (ks == 0) && (wk == 0);
     const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
     int32_t qc[MI];
@@ -576,6 +616,93 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // iterations of RING steps; steps past nkb only load (clamped, in bounds) and skip
   // their multiply, so no memory instruction is conditional and the compiler's vmcnt
   // bookkeeping stays exact.
+  if constexpr (E3M2) {
+    // A: chunk c of a stage (c < 7: the d0-3 part of row block c of the tile; c >= 7:
+    // bytes 1024 (c - 7) .. of the concatenated d4-5 parts, the last chunk half used and
+    // its upper lanes clamped to re-read in-bounds bytes into an unread LDS area).  Wave
+    // w issues chunks w, w + 4, w + 8 below 11.  Row blocks past M are clamped.
+    char* const a6 = lds_pool + kLdsA6;
+    const char* agp[3];
+    int aoff[3];
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int c = wave + 4 * j;
+      int blk, off;
+      if (c < 7) {
+        blk = c;
+        off = lane * 16;
+      } else {
+        const int t = (c - 7) * 1024 + lane * 16;
+        blk = min(t >> 9, 6);
+        off = 1024 + (t & 511);
+      }
+      const int mb = min(mt * MI + blk, p.mblocks - 1);
+      agp[j] = reinterpret_cast<const char*>(p.q) + static_cast<int64_t>(mb) * KB128 * kE3m2FragBytes + off;
+      aoff[j] = c * 1024;
+    }
+    const int nachunks = wave < 3 ? 3 : 2;  // 11 chunks over 4 waves
+    auto load_a6 = [&](int kb, int slot) {
+      const int64_t o = static_cast<int64_t>(min(kb, kb_end - 1)) * kE3m2FragBytes;
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        if (j >= nachunks) break;
+        __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(agp[j] + o),
+                                         (__attribute__((address_space(3))) void*)(a6 + slot * kA6Stage + aoff[j]),
+                                         16, 0, 0);
+      }
+    };
+    // B: the wave's two column pairs (GELU: its gate pair and its up pair; else two
+    // consecutive pairs), pairs past N clamped.
+    const char* bp6[2];
+#pragma unroll
+    for (int qd = 0; qd < 2; ++qd) {
+      const int pair = min((GELU ? wcol : wcol + 32 * qd) >> 5, (N >> 5) - 1);
+      const int32_t* base = (GELU && qd == 1) ? W2 : W;
+      bp6[qd] = reinterpret_cast<const char*>(base) + static_cast<int64_t>(pair) * KB128 * kE3m2PairBytes + lane * 16;
+    }
+    v4i b6[2][2][3];
+    auto load_b6 = [&](int kb, v4i (&b)[2][3]) {
+      const int64_t o = static_cast<int64_t>(min(kb, kb_end - 1)) * kE3m2PairBytes;
+#pragma unroll
+      for (int qd = 0; qd < 2; ++qd)
+#pragma unroll
+        for (int c = 0; c < 3; ++c) b[qd][c] = *reinterpret_cast<const v4i*>(bp6[qd] + o + c * 1024);
+    };
+    load_a6(kb_begin, 0);
+    load_b6(kb_begin, b6[0]);
+    for (int i = 0; i < nkb; i += 2) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        if (i + j >= nkb) break;  // uniform over the workgroup: every wave has the same k range
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        const char* st = a6 + j * kA6Stage;
+        v8i aop[MI];
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+          const v4i lo = *reinterpret_cast<const v4i*>(st + mi * 1024 + lane * 16);
+          const int2 hi = *reinterpret_cast<const int2*>(st + 7 * 1024 + mi * 512 + lane * 8);
+          aop[mi] = e3m2_op(lo, hi.x, hi.y);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        load_a6(kb_begin + i + j + 1, j ^ 1);
+        load_b6(kb_begin + i + j + 1, b6[j ^ 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+#pragma unroll
+          for (int ni = 0; ni < NI; ++ni) {
+            // fragment ni: pair ni / 2, column half ni % 2 (dwords 0-5 or 6-11 of the record)
+            const v4i* r = b6[j][ni >> 1];
+            const v8i bop = (ni & 1) ? e3m2_op(v4i{r[1].z, r[1].w, r[2].x, r[2].y}, r[2].z, r[2].w)
+                                     : e3m2_op(r[0], r[1].x, r[1].y);
+            acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bop, aop[mi], acc[mi][ni], 3, 3, 0, 0, 0, 0);
+          }
+        }
+      }
+    }
+    // The clamped prefetches of the last step land before the LDS is reused or the wave ends.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
 #pragma unroll
   for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
   unpack_first(ra[0], rb[0]);
@@ -596,6 +723,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       if (j == 0 || i + j < nkb) compute(ra[j], rb[j], ra[(j + 1) % RING], rb[(j + 1) % RING]);
     }
   }
+  }
 
   // A wave without k blocks never waited for its correction-table loads (see the first
   // step above): it waits now, before the barrier below (or the k reduction's) publishes
@@ -604,7 +732,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     if (nkb == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  if (tid < TROWS) epi_sa[tid] = e_sa * 0.0625f;
+  if (tid < TROWS) epi_sa[tid] = E3M2 ? e_sa : e_sa * 0.0625f;  // INT4: the accumulators hold 16 acc
   if (tid < NCOL) epi_sw[tid] = e_colvalid ? e_sw : 0.0f;
   if constexpr (KW == 1) __syncthreads();  // KW > 1: the k reduction below synchronises
 
@@ -702,11 +830,11 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       half4 ob[GELU ? 1 : NI];
 #pragma unroll
       for (int ni = 0; ni < (GELU ? NI / 2 : NI); ++ni) {
-        const v4i s = acc[mi][ni];
+        const AccV s = acc[mi][ni];
         const float swv[4] = {sw[ni].x, sw[ni].y, sw[ni].z, sw[ni].w};
         half4 o;
         if (GELU) {
-          const v4i su = acc[mi][ni + NI / 2];
+          const AccV su = acc[mi][ni + NI / 2];
           const float swu[4] = {sw[ni + NI / 2].x, sw[ni + NI / 2].y, sw[ni + NI / 2].z, sw[ni + NI / 2].w};
           // The four table lookups are issued ahead of the GELU arithmetic, which hides
           // their LDS latency.  The product with up is a packed fp16 multiply: the product
@@ -861,7 +989,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
                                __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-  } else {
+  } else if constexpr (!E3M2) {
     // kEpiPartial: partial sums of 16 * acc, int32 [ksplit, M, n_total] at column
     // col_off + col (slice 0 carries the corrections);
     // kEpiAcc:     int32 [M, N] accumulators of the group, (16 * acc) / 16.
@@ -1015,6 +1143,17 @@ hipError_t launch_gemm_gelu_quant(const GemmParams& p, int nquant, hipStream_t s
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles) + static_cast<unsigned>(nquant));
   gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, true><<<grid, 256, 0, stream>>>(p);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_e3m2(const GemmParams& p, hipStream_t stream) {
+  if (p.ksplit != 1 || (p.mode != kEpiFp16 && p.mode != kEpiGeluUp) || p.rope_group != 0 || p.res != nullptr)
+    return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles));
+  if (p.mode == kEpiGeluUp)
+    gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, true><<<grid, 256, 0, stream>>>(p);
+  else
+    gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, true><<<grid, 256, 0, stream>>>(p);
   return hipGetLastError();
 }
 

@@ -172,7 +172,8 @@ __global__ __launch_bounds__(T) void quant_rot_kernel(const _Float16* __restrict
 // with ss summed per lane over its R consecutive elements in order, then over the 64
 // lanes by the xor butterfly 32, 16, .., 1 (the oracle restates this order exactly), and
 // the fp16 h is what gets rotated and quantized, as if the norm's output had been stored.
-template <int LOGK, int LOGT, int ROWS, bool NORM = false>
+// E3M2 (K = 2048): the codes are written as E3M2 fragments (q points at the q6 buffer).
+template <int LOGK, int LOGT, int ROWS, bool NORM = false, bool E3M2 = false>
 __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     const _Float16* __restrict__ x, int64_t m, int32_t* __restrict__ q, float* __restrict__ sa,
     int32_t* __restrict__ qcorr, float inv_sqrt_k, const _Float16* __restrict__ nw = nullptr,
@@ -240,8 +241,9 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
 
   if constexpr (T == 64) {
     (void)L;
-    fwht_quant_row_wave<LOGK>(v, t, row, q, sa, qcorr, inv_sqrt_k);
+    fwht_quant_row_wave<LOGK, E3M2>(v, t, row, q, sa, qcorr, inv_sqrt_k);
   } else {
+    static_assert(!E3M2, "E3M2 codes come from the one-wave rows");
     fwht_quant_row<LOGK, LOGT>(v, L, red, ired, t, row, q, sa, qcorr, inv_sqrt_k);
   }
 }
@@ -324,6 +326,21 @@ hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int 
   fwht_quant_kernel<11, 6, 4, true><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
       static_cast<const _Float16*>(x), m, q, sa, qcorr, inv_sqrt_k, static_cast<const _Float16*>(w),
       eps, unit_offset);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_e3m2(const void* x, const void* nw, float eps, int unit_offset, int64_t m,
+                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream) {
+  if (m <= 0) return hipSuccess;
+  if (k != 2048) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((m + 3) / 4));
+  const _Float16* xh = static_cast<const _Float16*>(x);
+  int32_t* q = static_cast<int32_t*>(q6);
+  if (nw != nullptr)
+    fwht_quant_kernel<11, 6, 4, true, true><<<grid, 256, 0, stream>>>(
+        xh, m, q, sa, nullptr, inv_sqrt_k, static_cast<const _Float16*>(nw), eps, unit_offset);
+  else
+    fwht_quant_kernel<11, 6, 4, false, true><<<grid, 256, 0, stream>>>(xh, m, q, sa, nullptr, inv_sqrt_k);
   return hipGetLastError();
 }
 

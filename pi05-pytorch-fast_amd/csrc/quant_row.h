@@ -141,6 +141,46 @@ __device__ __forceinline__ uint32_t quant_pack8_rcp(const float (&v)[8], float r
   return word ^ kObFlipHi;
 }
 
+// The codes of quant_pack8 / quant_pack8_rcp as floats c + 8 in [1, 15] (same arithmetic,
+// so the same codes), for the E3M2 operand form.
+__device__ __forceinline__ void quant_codes8(const float (&v)[8], float sdiv, float* c) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float r = __builtin_rintf(__fdiv_rn(v[e], sdiv));
+    c[e] = fminf(fmaxf(r, -7.0f), 7.0f) + 8.0f;
+  }
+}
+__device__ __forceinline__ void quant_codes8_rcp(const float (&v)[8], float rcp, bool& near_tie, float* c) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float qa = __builtin_fmaf(v[e], rcp, 8.0f);
+    const float r = __builtin_rintf(qa);
+    near_tie |= fabsf(qa - r) > 0.499997f;
+    c[e] = fminf(fmaxf(r, 1.0f), 15.0f);
+  }
+}
+
+// One lane's 32 consecutive codes of row `row` (elements 32 t .. 32 t + 31, t the lane) as
+// an E3M2 fragment slot (the q6 layout of w4a4_internal.h): c holds code + 8.
+// v_cvt_scalef32_2xpk16_bf6_f32 converts two 16-value vectors, interleaving them (output
+// value 2i from the first, 2i + 1 from the second), so the even and the odd codes go in
+// separately; integers in [-7, 7] convert exactly.
+__device__ __forceinline__ void store_e3m2_slot(const float (&c)[32], int t, int64_t row, int32_t kb128,
+                                                uint8_t* __restrict__ q6) {
+  typedef float v16f __attribute__((ext_vector_type(16)));
+  v16f ev, od;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    ev[i] = c[2 * i] - 8.0f;
+    od[i] = c[2 * i + 1] - 8.0f;
+  }
+  const auto d = __builtin_amdgcn_cvt_scalef32_2xpk16_bf6_f32(ev, od, 1.0f);
+  uint8_t* const frag = q6 + ((row >> 4) * kb128 + (t >> 2)) * static_cast<int64_t>(kE3m2FragBytes);
+  const int slot = static_cast<int>(row & 15) + 16 * (t & 3);
+  *reinterpret_cast<uint4*>(frag + 16 * slot) = make_uint4(d[0], d[1], d[2], d[3]);
+  *reinterpret_cast<uint2*>(frag + 1024 + 8 * slot) = make_uint2(d[4], d[5]);
+}
+
 // Rotation, quantization and stores of one row of K = 2^LOGK values held by T = 2^LOGT
 // threads, R = K/T consecutive values per thread (thread t: elements t*R .. t*R + R - 1).
 // The log2(K) butterfly stages run in passes of r = log2(R) consecutive stride bits, each
@@ -333,7 +373,9 @@ __device__ __forceinline__ void lane_stage(float (&v)[R], int lane) {
   }
 }
 
-template <int LOGK>
+// E3M2: the codes go out as E3M2 fragment slots (q then points at the q6 buffer; no row
+// corrections), else as INT4 words and qcorr.
+template <int LOGK, bool E3M2 = false>
 __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)], int t, int64_t row,
                                                     int32_t* __restrict__ q, float* __restrict__ sa,
                                                     int32_t* __restrict__ qcorr, float inv_sqrt_k) {
@@ -369,6 +411,37 @@ __device__ __forceinline__ void fwht_quant_row_wave(float (&v)[1 << (LOGK - 6)],
   amax = wave_max_dpp(amax);
   const float sdiv = __fadd_rn(__fdiv_rn(amax, 7.0f), 1e-12f);
   if (t == 0) sa[row] = __fmul_rn(sdiv, inv_sqrt_k);
+  if constexpr (E3M2) {
+    static_assert(R == 32, "one E3M2 fragment slot (32 codes) per lane");
+    float c[R];
+    bool tie[R / 8];
+    bool near_tie = false;
+    const float rcp = __builtin_amdgcn_rcpf(sdiv);
+#pragma unroll
+    for (int u = 0; u < R / 8; ++u) {
+      float c8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+      tie[u] = false;
+      quant_codes8_rcp(c8, rcp, tie[u], c + 8 * u);
+      near_tie |= tie[u];
+    }
+    if (__builtin_amdgcn_ballot_w64(near_tie) != 0) {  // rare: redo the flagged groups exactly
+#pragma unroll
+      for (int u = 0; u < R / 8; ++u) {
+        if (__builtin_amdgcn_ballot_w64(tie[u]) != 0) {
+          float c8[8], x8[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) c8[e] = v[8 * u + e];
+          quant_codes8(c8, sdiv, x8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) c[8 * u + e] = tie[u] ? x8[e] : c[8 * u + e];
+        }
+      }
+    }
+    store_e3m2_slot(c, t, row, kblocks128(K), reinterpret_cast<uint8_t*>(q));
+    return;
+  }
   // Codes of the lane's R consecutive elements: R / 8 words, word u = codes 8u .. 8u + 7.
   uint32_t words[R / 8];
   bool tie[R / 8];

@@ -81,7 +81,70 @@ __global__ __launch_bounds__(256) void weight_corr_kernel(const int32_t* __restr
   if (lane == 0) dst[static_cast<int64_t>(n) * kblocks128(k) * 16 + n + col] = -8 * s16;
 }
 
+// E3M2 bits of an integer code in [-8, 8]: magnitudes 0, 1, 2, 3, 4, 5, 6, 7, 8 are
+// 0, 2^0, 2^1, 1.5 * 2^1, 2^2, 1.25 * 2^2, 1.5 * 2^2, 1.75 * 2^2, 2^3 (exponent field
+// e + 3, two mantissa bits), the sign in bit 5.
+__device__ __forceinline__ uint32_t e3m2_bits(int c) {
+  constexpr uint32_t kMag[9] = {0x00, 0x0c, 0x10, 0x12, 0x14, 0x15, 0x16, 0x17, 0x18};
+  return c < 0 ? (0x20u | kMag[-c]) : kMag[c];
+}
+
+// INT4 MFMA layout -> E3M2 pair layout (w4a4_internal.h).  One thread per (column, k
+// block, 32-code group): it reads the column's 16-byte slot of the INT4 fragment, decodes
+// the weight nibbles (even k: high nibble, two's complement; odd k: low nibble, offset
+// binary), re-encodes the 32 codes as E3M2 (code j in bits 6j .. 6j+5 of six dwords) and
+// writes the dwords into the column pair's 48-byte lane record.  The last N threads copy
+// the column scales.  Load time only.
+__global__ __launch_bounds__(256) void repack_e3m2_kernel(const int32_t* __restrict__ src, int32_t n, int32_t k,
+                                                          int32_t* __restrict__ dst) {
+  const int32_t kb128 = kblocks128(k);
+  const int64_t slots = static_cast<int64_t>(n) * kb128 * 4;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx < slots) {
+    const int g = static_cast<int>(idx & 3);
+    const int64_t kb = (idx >> 2) % kb128;
+    const int64_t col = (idx >> 2) / kb128;
+    uint32_t d[6] = {0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t w = static_cast<uint32_t>(src[frag_word_index(col, static_cast<int32_t>(kb * 16 + 4 * g + i), kb128)]);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t byte = (w >> (8 * b)) & 0xffu;
+        const int even = static_cast<int>((byte >> 4) ^ 8u) - 8;  // two's complement nibble
+        const int odd = static_cast<int>(byte & 15u) - 8;          // offset binary nibble
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int j = 8 * i + 2 * b + h;  // code index in the slot's 32
+          const uint32_t f = e3m2_bits(h ? odd : even);
+          const int bit = 6 * j;
+          d[bit >> 5] |= f << (bit & 31);
+          if ((bit & 31) > 26) d[(bit >> 5) + 1] |= f >> (32 - (bit & 31));
+        }
+      }
+    }
+    const int64_t pair = col >> 5;
+    const int h = static_cast<int>((col >> 4) & 1);
+    const int lane = static_cast<int>(col & 15) + 16 * g;
+    uint8_t* const base = reinterpret_cast<uint8_t*>(dst) + (pair * kb128 + kb) * kE3m2PairBytes;
+#pragma unroll
+    for (int i = 0; i < 6; ++i) {
+      const int byte_in_record = 4 * (6 * h + i);
+      *reinterpret_cast<uint32_t*>(base + (byte_in_record >> 4) * 1024 + 16 * lane + (byte_in_record & 15)) = d[i];
+    }
+  } else if (idx < slots + n) {
+    const int64_t col = idx - slots;
+    dst[w6_payload_words(n, kb128) + col] = src[static_cast<int64_t>(n) * kb128 * 16 + col];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_repack_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int32_t* dst, hipStream_t stream) {
+  const int64_t total = static_cast<int64_t>(n) * kblocks128(k) * 4 + n;
+  repack_e3m2_kernel<<<dim3(static_cast<unsigned>((total + 255) / 256)), 256, 0, stream>>>(w_mfma, n, k, dst);
+  return hipGetLastError();
+}
 
 hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t k,
                          int64_t src_stride, int32_t* dst, hipStream_t stream) {

@@ -138,6 +138,31 @@ __host__ __device__ inline int64_t q_total_words(int64_t mblocks, int32_t kb128)
 
 __host__ __device__ inline int32_t kblocks128(int32_t k) { return (k + 127) >> 7; }
 
+// E3M2 (bf6) operand layouts, for gfx950's v_mfma_f32_16x16x128_f8f6f4 with both operands
+// in the OCP FP6 E3M2 format (sign, 3 exponent bits with bias 3, 2 mantissa bits, no
+// inf/NaN).  Every integer in [-8, 8] is an E3M2 value, so INT4 codes travel exactly;
+// the MFMA's products are integers of magnitude <= 64 and its fp32 sums stay integers
+// below 2^24 for K <= 2^18, so the fp32 accumulator equals the int32 dot product bit for
+// bit, in any summation order.  One MFMA covers 16 x 16 x 128 at twice the int8 MFMA's
+// rate and needs no unpack: lane L supplies codes 32*(L/16) .. +31 of line L%16 of its
+// 128-deep block, code j in bits 6j .. 6j+5 of six dwords d0 .. d5.
+//  * Activations (q6): one 1536-byte fragment per 16 rows x 128 k, fragment (mb, kb) at
+//    byte (mb * kb128 + kb) * 1536: bytes [0, 1024) hold d0-d3 of lane L at 16 L, bytes
+//    [1024, 1536) hold d4-d5 of lane L at 1024 + 8 L.  No row corrections (the codes are
+//    signed values); sa as for the INT4 codes.
+//  * Weights (w6): columns in pairs; pair p (columns 32p .. 32p+31) and k block kb form
+//    3072 bytes at (p * kb128 + kb) * 3072, three 1 KB chunks: chunk c holds bytes
+//    16c .. 16c+15 of each lane's 48-byte record [d0..d5 of column 32p + L%16 | d0..d5 of
+//    column 32p + 16 + L%16] at 16 L.  Three 16-byte loads per lane fetch both fragments
+//    with each fragment's six dwords in consecutive registers.  The fp32 column scales
+//    follow the payload (N * kb128 * 24 words); the tensor is int32 [N, 3K/16 + 16].
+constexpr int kE3m2FragBytes = 1536;
+constexpr int kE3m2PairBytes = 3072;
+__host__ __device__ inline int64_t q6_bytes(int64_t mblocks, int32_t kb128) {
+  return mblocks * kb128 * kE3m2FragBytes;
+}
+__host__ __device__ inline int64_t w6_payload_words(int64_t n, int32_t kb128) { return n * kb128 * 24; }
+
 // GEMM tile configurations: wave tile (16*MI) x (16*NI); K4 / K8 = the 4 / 8 waves of
 // a workgroup split K (one column block per workgroup) instead of N.
 enum TileCfg : int {
@@ -196,6 +221,15 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
                            float inv_sqrt_k, hipStream_t stream, const CacheWarmParams* warm = nullptr);
 hipError_t launch_repack(const int32_t* src, int32_t layout, int32_t n, int32_t k,
                          int64_t src_stride, int32_t* dst, hipStream_t stream);
+// INT4 MFMA-layout weight (N % 32 == 0, K % 128 == 0) -> the E3M2 pair layout w6.
+hipError_t launch_repack_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int32_t* dst, hipStream_t stream);
+// K = 2048 activation quant (optionally with the fused RMSNorm, nw != null) writing E3M2
+// fragments (q6) instead of INT4 codes.
+hipError_t launch_quantize_e3m2(const void* x, const void* nw, float eps, int unit_offset, int64_t m,
+                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream);
+// GEMM on E3M2 operands: 112 x 256 workgroup tiles (4 waves along N), modes kEpiFp16
+// (1..3 groups) and kEpiGeluUp; p.q points at q6, the groups' w at w6.
+hipError_t launch_gemm_e3m2(const GemmParams& p, hipStream_t stream);
 // Chooses the tile configuration; returns the K split used (>= 1) through *ksplit_out.
 hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
 // The paired gate/up GELU GEMM (7x4 tiles, no K split) with the down-projection quant of

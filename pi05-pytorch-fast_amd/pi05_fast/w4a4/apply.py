@@ -76,8 +76,13 @@ def load_time_weight(
     use_mfma = os.environ.get("PI05_W4A4_MFMA", "1") != "0"
     on_gpu = device is not None and torch.device(device).type == "cuda"
     if use_mfma and on_gpu and out_features % 16 == 0:
-        from pi05_fast.w4a4.extension import repack_weight
+        from pi05_fast.w4a4.extension import repack_weight, repack_weight_e3m2
 
+        # The MLP's gate/up weights (K = 2048) take the E3M2 form of the same codes, which
+        # the FP6-MFMA GEMM reads (PI05_W4A4_E3M2=0: the INT4 MFMA layout for all).
+        if (os.environ.get("PI05_W4A4_E3M2", "1") != "0" and name.endswith((".mlp.gate_proj", ".mlp.up_proj"))
+                and in_features == 2048 and out_features % 32 == 0):
+            return repack_weight_e3m2(w.to(device), k=in_features, tiled=False), False
         return repack_weight(w.to(device), k=in_features, tiled=False), False
     gate_preshuffle = os.environ.get("PI05_W4A4_GATE_PRESHUFFLE", "1") != "0"
     row_pad_words = _row_pad_words()
@@ -392,7 +397,8 @@ def _fused_decoder_layer_forward(
     if past_key_values is not None:
         value_states = v.view(*v.shape[:-1], -1, hd).transpose(1, 2)
         past_key_values.update(key_states, value_states, attn.layer_idx)
-    if os.environ.get("PI05_W4A4_FUSE_DOWN_QUANT", "0") == "1":
+    if os.environ.get("PI05_W4A4_FUSE_DOWN_QUANT", "0") == "1" and ext.is_mfma_layout(mlp.gate_proj.packed,
+                                                                                   mlp.gate_proj.in_features):
         # The down projection's activation quant in the gate/up launch (one launch fewer).
         y, _ = ext.rms_norm_int4_mlp(x2, w2, eps2, mlp.gate_proj.packed, mlp.up_proj.packed, mlp.down_proj.packed,
                                      x2, warm=[mlp.down_proj.packed] if warming else None, unit_offset=off2)

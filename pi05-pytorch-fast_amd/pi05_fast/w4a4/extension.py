@@ -16,7 +16,10 @@ Weight layouts accepted (the reference's marker-stride convention):
     for drop-in use; the copy doubles the weight's device memory);
   * WMMA-tiled ``[N, K/8+9]`` (L3) -- ``*_tiled`` ops, repacked once likewise;
   * MFMA-fragment-major ``[N, K/8+16]`` -- produced once by ``repack_weight`` (and by
-    ``apply.replace_linears_from_packed`` at load), consumed directly (fast path).
+    ``apply.replace_linears_from_packed`` at load), consumed directly (fast path);
+  * E3M2 column pairs ``[N, 3K/16+16]`` -- the same codes as FP6 E3M2 values for the
+    FP6 MFMA (``repack_weight_e3m2``; the gate/up weights at load): the ops quantize the
+    activations into the matching E3M2 fragments.  All weights of one call must share it.
 
 There is no CPU fallback: without the library (or without a GPU) the ops raise.
 """
@@ -33,6 +36,7 @@ import torch
 
 MFMA_MARKER_WORDS = 16
 WMMA_MARKER_WORDS = 9
+E3M2_MARKER_WORDS = 16  # [N, 3K/16 + 16]: E3M2 codes are 3K/16 words per column
 
 _LAYOUT_ROW_MAJOR = 0
 _LAYOUT_WMMA_TILED = 1
@@ -125,6 +129,12 @@ def load_int4_gemm():
                            i32, i32, i32, vp]),
         "pi05w4a4_mlp_ctl_words": (sz, [i64]),
         "pi05w4a4_mlp_status": (i64, [i32]),
+        "pi05w4a4_q_e3m2_bytes": (sz, [i64, i32]),
+        "pi05w4a4_e3m2_words": (sz, [i32, i32]),
+        "pi05w4a4_repack_weight_e3m2": (ctypes.c_int, [vp, i32, i32, vp, vp]),
+        "pi05w4a4_quantize_e3m2": (ctypes.c_int, [vp, i64, i32, vp, vp, vp]),
+        "pi05w4a4_rmsnorm_quantize_e3m2": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
+        "pi05w4a4_gemm_e3m2": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -260,6 +270,19 @@ def is_mfma_layout(w: torch.Tensor, k: int) -> bool:
     return w.dim() == 2 and w.size(1) == k // 8 + MFMA_MARKER_WORDS and w.size(0) % 16 == 0
 
 
+def is_e3m2_layout(w: torch.Tensor, k: int) -> bool:
+    """An E3M2 column-pair weight [N, 3K/16 + 16] (K % 128 == 0, N % 32 == 0)."""
+    return (w.dim() == 2 and k % 128 == 0 and w.size(1) == 3 * k // 16 + E3M2_MARKER_WORDS
+            and w.size(0) % 32 == 0)
+
+
+def _q6_bytes(m: int, k: int) -> int:
+    """pi05w4a4_q_e3m2_bytes: 1536 bytes per 16-row block and 128-deep k block."""
+    if m <= 0 or k <= 0:
+        return 0
+    return (m + 15) // 16 * ((k + 127) // 128) * 1536
+
+
 # ----------------------------------------------------------------------------- pieces
 def _warm_args(warm, who: str):
     """(pointer array, byte-size array, count) of the non-empty warm tensors, or None."""
@@ -332,6 +355,77 @@ def repack_weight(w: torch.Tensor, k: int | None = None, tiled: bool | None = No
         _check(lib.pi05w4a4_repack_weight(_ptr(src), layout, n, k, int(src.size(1)), _ptr(out),
                                           _stream(w.device)), "pi05w4a4_repack_weight")
     return out
+
+
+def repack_weight_e3m2(w: torch.Tensor, k: int | None = None, tiled: bool | None = None) -> torch.Tensor:
+    """The E3M2 column-pair form ``[N, 3K/16 + 16]`` of a packed weight (any layout
+    ``repack_weight`` reads, or the MFMA layout): the same INT4 codes as FP6 E3M2 values,
+    for the FP6-MFMA GEMM.  N % 32 == 0 and K % 128 == 0."""
+    if not w.is_cuda:
+        raise RuntimeError("packed W must be on CUDA/HIP")
+    if w.dtype != torch.int32 or w.dim() != 2:
+        raise RuntimeError("packed W must be int32 [N, K/8+1]")
+    n = int(w.size(0))
+    if k is None:
+        if tiled is None:
+            tiled = False
+        k = (int(w.size(1)) - (WMMA_MARKER_WORDS if tiled else 1)) * 8
+    if k % 128 != 0 or n % 32 != 0:
+        raise RuntimeError(f"the E3M2 layout needs K % 128 == 0 and N % 32 == 0, got N={n} K={k}")
+    if is_e3m2_layout(w, k):
+        return w
+    src = w if is_mfma_layout(w, k) else repack_weight(w, k, tiled=tiled)
+    out = torch.zeros((n, 3 * k // 16 + E3M2_MARKER_WORDS), dtype=torch.int32, device=w.device)
+    lib = load_int4_gemm()
+    with torch.cuda.device(w.device):
+        _check(lib.pi05w4a4_repack_weight_e3m2(_ptr(src.contiguous()), n, k, _ptr(out), _stream(w.device)),
+               "pi05w4a4_repack_weight_e3m2")
+    return out
+
+
+def quantize_e3m2(x: torch.Tensor, norm=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """``quantize`` (or, with ``norm`` = (weight, eps, unit_offset), ``rms_norm_quantize``)
+    with the codes written as E3M2 fragments (uint8 [pi05w4a4_q_e3m2_bytes(M, K)]): the
+    activation form of the FP6-MFMA GEMM.  K = 2048."""
+    k = _check_x(x)
+    if k != 2048:
+        raise RuntimeError(f"the E3M2 quantizer takes K = 2048, got {k}")
+    x2 = x if x.is_contiguous() else x.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    m = x2.numel() // k
+    lib = _lib if _lib is not None else load_int4_gemm()
+    dev = x2.device
+    q6 = torch.empty((_q6_bytes(m, k),), dtype=torch.uint8, device=dev)
+    sa = torch.empty((m,), dtype=torch.float32, device=dev)
+    with _on_device(dev):
+        if norm is None:
+            _check(lib.pi05w4a4_quantize_e3m2(x2.data_ptr(), m, k, q6.data_ptr(), sa.data_ptr(), _stream(dev)),
+                   "pi05w4a4_quantize_e3m2")
+        else:
+            weight, eps, unit_offset = norm
+            if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 1 or weight.numel() != k:
+                raise RuntimeError(f"RMSNorm weight must be a float16 CUDA/HIP tensor [{k}]")
+            wn = weight if weight.is_contiguous() else weight.contiguous()
+            _check(lib.pi05w4a4_rmsnorm_quantize_e3m2(x2.data_ptr(), wn.data_ptr(), float(eps),
+                                                      1 if unit_offset else 0, m, k, q6.data_ptr(), sa.data_ptr(),
+                                                      _stream(dev)), "pi05w4a4_rmsnorm_quantize_e3m2")
+    return q6, sa
+
+
+def _gemm_e3m2_from_q(q6, sa, k, weights, out_shape_prefix, device, gelu=False):
+    """GEMMs of 1..3 E3M2-layout weights (or the GELU pair) from E3M2 activation codes."""
+    lib = _lib if _lib is not None else load_int4_gemm()
+    m = int(sa.size(0))
+    ns = tuple(int(w.size(0)) for w in weights)
+    outs = [torch.empty((m, ns[0]), dtype=torch.float16, device=device)] if gelu else \
+        [torch.empty((m, nn), dtype=torch.float16, device=device) for nn in ns]
+    g = len(ns)
+    w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for w in weights])
+    y_arr = (ctypes.c_void_p * g)(*([outs[0].data_ptr(), None] if gelu else [o.data_ptr() for o in outs]))
+    _check(lib.pi05w4a4_gemm_e3m2(q6.data_ptr(), sa.data_ptr(), m, k, g, w_arr, _n_array(ns), y_arr,
+                                  1 if gelu else 0, _stream(device)), "pi05w4a4_gemm_e3m2")
+    return [o.view(*out_shape_prefix, o.size(1)) for o in outs]
 
 
 # Repacked copies of weights that arrive in a reference layout (L1/L2/L3), one per source
@@ -551,6 +645,9 @@ def _rms_norm_mlp_impl(x, norm_weight, eps, unit_offset, w_gate, w_up, w_down, r
 def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: bool = False,
          norm=None, residual=None, warm=None):
     k = _check_x(x)
+    n_e3m2 = sum(1 for w in ws if is_e3m2_layout(w, k))
+    if n_e3m2:
+        return _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual)
     if residual is not None:  # before any launch: the kernel reads it through a raw pointer
         _check_residual(residual, x.device, (*x.shape[:-1], int(ws[0].size(0))))
     # the reference quantizes before checking the weights
@@ -564,6 +661,20 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
     dev = x.device
     with _on_device(dev):
         return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), dev, kind, gelu=gelu, residual=residual)
+
+
+def _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual):
+    """_run for E3M2-layout weights: E3M2 activation quant, then the FP6-MFMA GEMM."""
+    if n_e3m2 != len(ws):
+        raise RuntimeError(f"{kind}: the weights of one call must all be E3M2-layout ([N, 3K/16+16]) or none")
+    if residual is not None:
+        raise RuntimeError(f"{kind}: the residual epilogue takes INT4-layout weights, not E3M2")
+    for w in ws:
+        _check_packed(w, k)
+    q6, sa = quantize_e3m2(x, norm)
+    dev = x.device
+    with _on_device(dev):
+        return _gemm_e3m2_from_q(q6, sa, k, ws, tuple(x.shape[:-1]), dev, gelu=gelu)
 
 
 def _rms_norm_impl(x: torch.Tensor, weight: torch.Tensor, eps: float, unit_offset: bool) -> torch.Tensor:

@@ -8,6 +8,7 @@ import torch.nn as nn
 
 from pi05_fast.w4a4.extension import int4_gemm, int4_gemm_tiled
 from pi05_fast.w4a4.pack import (
+    E3M2_MARKER_WORDS,
     MFMA_MARKER_WORDS,
     WMMA_PRESHUFFLE_PAD_WORDS,
     pack_linear_weight,
@@ -56,11 +57,21 @@ class W4A4Linear(nn.Module):
 
     @property
     def mfma(self) -> bool:
-        """True when ``packed`` is in the gfx950 MFMA-fragment-major layout."""
+        """True when ``packed`` is in a gfx950 MFMA operand layout: the INT4
+        fragment-major layout or the E3M2 column pairs of the FP6-MFMA GEMM."""
+        return not self.preshuffled and (
+            (self.packed.shape[1] == self.in_features // 8 + MFMA_MARKER_WORDS and self.out_features % 16 == 0)
+            or self.e3m2
+        )
+
+    @property
+    def e3m2(self) -> bool:
+        """True when ``packed`` holds the codes as E3M2 column pairs ``[N, 3K/16 + 16]``."""
         return (
             not self.preshuffled
-            and self.packed.shape[1] == self.in_features // 8 + MFMA_MARKER_WORDS
-            and self.out_features % 16 == 0
+            and self.in_features % 128 == 0
+            and self.packed.shape[1] == 3 * self.in_features // 16 + E3M2_MARKER_WORDS
+            and self.out_features % 32 == 0
         )
 
     @classmethod
@@ -81,7 +92,7 @@ class W4A4Linear(nn.Module):
         return y
 
     def extra_repr(self) -> str:
-        layout = "wmma" if self.preshuffled else ("mfma" if self.mfma else "row")
+        layout = "wmma" if self.preshuffled else ("e3m2" if self.e3m2 else ("mfma" if self.mfma else "row"))
         return (
             f"in={self.in_features}, out={self.out_features}, "
             f"rotate={self.rotate}, layout={layout}"

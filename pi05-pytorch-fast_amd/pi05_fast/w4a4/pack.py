@@ -235,6 +235,60 @@ def qcorr_from_fragment_major(q: torch.Tensor, m: int, k: int) -> torch.Tensor:
     return q.reshape(-1)[pw : pw + m]
 
 
+# ---- E3M2 (OCP FP6: sign bit 5, exponent bits 4-2 with bias 3, mantissa bits 1-0) forms
+# of the INT4 codes, read by the gfx950 FP6-MFMA gate/up GEMM.  A lane slot is six
+# little-endian dwords holding 32 codes, code j in bits 6j .. 6j+5.
+E3M2_MARKER_WORDS = 16
+
+
+def e3m2_to_float(bits: torch.Tensor) -> torch.Tensor:
+    """Values of 6-bit E3M2 patterns: (-1)^s 2^(e-3) (1 + m/4), subnormal (e = 0) m/16."""
+    b = bits.to(torch.int64)
+    e = (b >> 2) & 7
+    man = (b & 3).to(torch.float64)
+    mag = torch.where(e == 0, man / 16.0, torch.exp2((e - 3).to(torch.float64)) * (1.0 + man / 4.0))
+    return torch.where((b >> 5) & 1 == 1, -mag, mag)
+
+
+def _slot_values(slot_bytes: torch.Tensor) -> torch.Tensor:
+    """[..., 24] uint8 lane slots -> [..., 32] float64 E3M2 values."""
+    bits = torch.stack([(slot_bytes.to(torch.int64) >> i) & 1 for i in range(8)], dim=-1)  # little-endian bits
+    bits = bits.reshape(*slot_bytes.shape[:-1], 32, 6)
+    return e3m2_to_float((bits << torch.arange(6)).sum(dim=-1))
+
+
+def _as_codes(vals: torch.Tensor) -> torch.Tensor:
+    codes = torch.round(vals)
+    if not torch.equal(codes, vals):
+        raise ValueError("E3M2 codes hold a non-integer value")
+    return codes.to(torch.int8)
+
+
+def codes_from_e3m2_fragments(q6: torch.Tensor, m: int, k: int) -> torch.Tensor:
+    """E3M2 activation fragments (``quantize_e3m2``'s q6, 1536 bytes per 16 rows x 128 k)
+    -> int8 codes [M, K]."""
+    mb, kb = (m + 15) // 16, (k + 127) // 128
+    f = q6.reshape(-1)[: mb * kb * 1536].to(torch.uint8).reshape(mb, kb, 1536)
+    slots = torch.cat((f[:, :, :1024].reshape(mb, kb, 64, 16), f[:, :, 1024:].reshape(mb, kb, 64, 8)), dim=-1)
+    vals = _slot_values(slots)  # [mb, kb, lane, 32]: row 16 mb + lane % 16, k 128 kb + 32 (lane / 16) + j
+    vals = vals.reshape(mb, kb, 4, 16, 32).permute(0, 3, 1, 2, 4).reshape(mb * 16, kb * 128)
+    return _as_codes(vals[:m, :k])  # the pad rows of the last block are never written
+
+
+def codes_from_e3m2_weight(w6: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """E3M2 column-pair weight int32 [N, 3K/16+16] -> (int8 codes [N, K], fp32 scales [N])."""
+    n = int(w6.size(0))
+    kb = (k + 127) // 128
+    flat = w6.reshape(-1).contiguous()
+    payload = flat[: n * kb * 24].view(torch.uint8).reshape(n // 32, kb, 3, 64, 16)
+    rec = payload.permute(0, 1, 3, 2, 4).reshape(n // 32, kb, 64, 48)  # lane records
+    slots = torch.stack((rec[..., :24], rec[..., 24:]), dim=2)  # [pair, kb, half, lane, 24]
+    vals = _slot_values(slots)  # column 32 p + 16 half + lane % 16, k 128 kb + 32 (lane / 16) + j
+    vals = vals.reshape(n // 32, kb, 2, 4, 16, 32).permute(0, 2, 4, 1, 3, 5).reshape(n, kb * 128)
+    scales = flat[n * kb * 24 : n * kb * 24 + n].view(torch.float32)
+    return _as_codes(vals[:, :k]), scales
+
+
 def quant_activation_cpu(x: torch.Tensor, rotate: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """CPU statement of the activation quant (pack.py:113-131): x [M, K] -> (codes [M, K], scale [M]).
 

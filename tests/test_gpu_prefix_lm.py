@@ -79,9 +79,14 @@ class _Recorder:
 
 def _row_major(w: torch.Tensor, k: int) -> np.ndarray:
     """The L1 row-major [N, K/8+1] form of a weight in any layout the ops take: MFMA
-    (K/8+16), WMMA-tiled (K/8+9) or row-major / row-padded (scale at word K/8)."""
+    (K/8+16), E3M2 column pairs (3K/16+16), WMMA-tiled (K/8+9) or row-major / row-padded
+    (scale at word K/8)."""
     from pi05_fast.w4a4 import pack
 
+    if k % 128 == 0 and w.shape[1] == 3 * k // 16 + pack.E3M2_MARKER_WORDS:
+        codes, scales = pack.codes_from_e3m2_weight(w.cpu(), k)
+        return np.concatenate([orc.pack_nibbles(codes.numpy()).astype(np.int32),
+                               scales.numpy().view(np.int32)[:, None]], axis=1)
     if w.shape[1] == k // 8 + pack.MFMA_MARKER_WORDS:
         return pack.unpack_mfma_weight(w.cpu(), k).numpy()
     if w.shape[1] == k // 8 + pack.WMMA_PRESHUFFLE_PAD_WORDS:
@@ -272,6 +277,7 @@ def test_prefix_lm_fused_down_quant_ops_match_oracle(cuda, monkeypatch, layers, 
 
     print(f"prefix LM forward, fused down quant: {layers} layers x {tokens} tokens x batch {batch}", flush=True)
     monkeypatch.setenv("PI05_W4A4_FUSE_DOWN_QUANT", "1")
+    monkeypatch.setenv("PI05_W4A4_E3M2", "0")  # the down quant rides on the INT4 gate/up launch
     model, _ = _build(cuda, layers, fuse_gelu=True, fuse_layer=True)
     rec = _Recorder(monkeypatch)
     x = prefix_inputs(batch, tokens, cuda)
