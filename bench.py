@@ -62,9 +62,12 @@ for _p in (ROOT / "pi05-pytorch-fast_amd", ROOT):
 METRIC = "W4A4 prefix-LM ms @776 tok; int8 TOPS & % MFMA peak per GEMM (1 MI355X)"
 INT8_PEAK_TOPS = 5000.0   # MI355X dense int8 MFMA, published
 FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA, published
+FP6_PEAK_TOPS = 10100.0    # MI355X dense fp6 / fp4 MFMA, published
 HBM_PEAK_GBS = 8000.0     # MI355X HBM3E, published
 # HBM-side traffic per launch of the W4A4 kernels (rocprofv3 FETCH_SIZE / WRITE_SIZE summary).
 TRAFFIC_FILE = ROOT / "profiles" / "w4a4_kernels_776tok_traffic.md"
+# The forward's gate/up weights take the E3M2 operand form at load unless PI05_W4A4_E3M2=0.
+E3M2_GATE_UP = os.environ.get("PI05_W4A4_E3M2", "1") != "0"
 
 
 def parse_args():
@@ -195,24 +198,38 @@ class KernelBench:
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "pair_offset_us": self.last_pair_offset_us}
 
-    def gemm(self, m, k, ns, gelu=False, residual=False, copies=1):
+    def gemm(self, m, k, ns, gelu=False, residual=False, copies=1, e3m2=False):
         """One W4A4 GEMM launch shape.  With `copies` > 1 (plain grouped GEMM only), that
         many weight sets are packed and the timed graph cycles through them, one set per
-        launch, so that weights come from HBM rather than from the L2 / Infinity Cache."""
+        launch, so that weights come from HBM rather than from the L2 / Infinity Cache.
+        `e3m2`: the same codes in the E3M2 operand form (pi05w4a4_gemm_e3m2, FP6 MFMA)."""
         torch, lib, P = self.torch, self.lib, self.ext._ptr
         gen = torch.Generator(device=self.dev).manual_seed(20260923 + k + sum(ns))
         x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
-        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        if e3m2:
+            q = torch.empty(int(lib.pi05w4a4_q_e3m2_bytes(m, k)), dtype=torch.uint8, device=self.dev)
+        else:
+            q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
         sa = torch.empty(m, dtype=torch.float32, device=self.dev)
-        self._check(lib.pi05w4a4_quantize(P(x), m, k, P(q), P(sa), self._stream()))
-        if copies > 1 and (gelu or residual):
-            raise ValueError("weight copies are for the plain grouped GEMM")
+        quant = lib.pi05w4a4_quantize_e3m2 if e3m2 else lib.pi05w4a4_quantize
+        self._check(quant(P(x), m, k, P(q), P(sa), self._stream()))
+        if copies > 1 and (gelu or residual or e3m2):
+            raise ValueError("weight copies are for the plain grouped INT4 GEMM")
         ws = [self._packed(n, k, gen) for n in ns]
+        if e3m2:
+            ws = [self.ext.repack_weight_e3m2(w, k=k) for w in ws]
         g = len(ns)
         n_arr = (ctypes.c_int32 * g)(*ns)
-        wsb = int(lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0))
+        wsb = 0 if e3m2 else int(lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 1 if gelu else 0))
         work = torch.empty(max(wsb, 16), dtype=torch.uint8, device=self.dev)
-        if gelu:
+        if e3m2:
+            w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for w in ws])
+            outs = [torch.empty(m, n, dtype=torch.float16, device=self.dev) for n in (ns[:1] if gelu else ns)]
+            y_arr = (ctypes.c_void_p * g)(*([outs[0].data_ptr(), None] if gelu else [o.data_ptr() for o in outs]))
+            fn = lambda: self._check(lib.pi05w4a4_gemm_e3m2(  # noqa: E731
+                P(q), P(sa), m, k, g, w_arr, n_arr, y_arr, 1 if gelu else 0, self._stream()))
+            out_bytes = 2.0 * m * sum(o.size(1) for o in outs)
+        elif gelu:
             out = torch.empty(m, ns[0], dtype=torch.float16, device=self.dev)
             fn = lambda: self._check(lib.pi05w4a4_gemm_gelu_up(  # noqa: E731
                 P(q), P(sa), m, k, P(ws[0]), P(ws[1]), ns[0], P(out), P(work), wsb, self._stream()))
@@ -237,10 +254,17 @@ class KernelBench:
         ops = 2.0 * m * n * k
         nbytes = m * k / 2 + 4 * m + n * k / 2 + 4 * n + out_bytes
         tops = ops / (us * 1e-6) / 1e12
-        return {"m": m, "k": k, "n": n, "avg_us": round(us, 3), "ops": ops, "tops": round(tops, 1),
-                "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "bytes": nbytes,
-                "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb,
-                "pair_offset_us": self.last_pair_offset_us}
+        rec = {"m": m, "k": k, "n": n, "avg_us": round(us, 3), "ops": ops, "tops": round(tops, 1),
+               "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4), "bytes": nbytes,
+               "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "workspace_bytes": wsb,
+               "pair_offset_us": self.last_pair_offset_us}
+        if e3m2:
+            # The same int products on the FP6 MFMA, whose dense peak is twice the int8 one;
+            # its operands take 1.5x the INT4 bytes.
+            rec.update({"operands": "e3m2 (v_mfma_f32_16x16x128_f8f6f4)",
+                        "frac_fp6_peak": round(tops / FP6_PEAK_TOPS, 4),
+                        "operand_bytes": m * k * 0.75 + 4 * m + n * k * 0.75 + 4 * n + out_bytes})
+        return rec
 
 
     def gelu_quant(self, m, k=2048, n=16384, fused=True):
@@ -380,6 +404,10 @@ def forward_point(torch, model, prefix_inputs, dev, tokens: int, batch: int, ste
 
 def _in_forward_label(fn_name: str, args: tuple, kwargs: dict) -> str:
     """Kernel class of one library call made by the forward."""
+    if fn_name == "_gemm_e3m2_from_q":
+        return "gate_up_gelu" if kwargs.get("gelu") else ("gate_up" if len(args[3]) == 2 else "gemm")
+    if fn_name == "quantize_e3m2":
+        return "rmsnorm_quant_k2048" if len(args) > 1 and args[1] is not None else "quant_k2048"
     if fn_name == "_gemm_from_q":
         k, weights = args[2], args[3]
         if kwargs.get("gelu"):
@@ -408,7 +436,7 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
     alone.  `raw_avg_us` is the mean pair interval; `calibrate_in_forward` takes off it
     the event-pair cost that the same kernel shows when launched alone (`avg_us`)."""
     names = ("_gemm_from_q", "quantize", "rms_norm_quantize", "_prefix_attention_impl", "_gemm_qkv_rope",
-             "_gemm_gelu_quant_from_q")
+             "_gemm_gelu_quant_from_q", "_gemm_e3m2_from_q", "quantize_e3m2")
     orig = {n: getattr(ext, n) for n in names}
     records = []
 
@@ -481,21 +509,48 @@ def in_forward_times(torch, ext, model, x, mask, reps: int = 5) -> dict:
 _KERNEL_CLASS_RULES = (
     # (regex on the kernel name as the profiler reports it, demangled or mangled) -> class
     (r"fwht_quant_kernel(?:<14,|ILi14E)", "quant_k16384"),
-    (r"fwht_quant_kernel(?:<11, 6, 4, true>|ILi11ELi6ELi4ELb1E)", "rmsnorm_quant_k2048"),
+    (r"fwht_quant_kernel(?:<11, 6, 4, true[,>]|ILi11ELi6ELi4ELb1E)", "rmsnorm_quant_k2048"),
     (r"fwht_quant_kernel(?:<11,|ILi11E)", "quant_k2048"),
     (r"prefix_attention_kernel", "attention"),
     (r"kv_prep_kernel", "attn_kv_prep"),
     (r"rmsnorm_kernel", "rmsnorm"),
-    # gemm_w4a4_kernel<MI, NI, NWAVES, KW, GELU, RING, WPE, QKV_PREP, QFUSE>: the 776-token
-    # forward's GEMMs by their tile configuration
-    (r"gemm_w4a4_kernel(?:<[^>]*, true, \d+, \d+, false, true>|I(?:Li\d+E){4}Lb1E(?:Li\d+E){2}Lb0ELb1E)",
-     "gate_up_gelu_quant"),
-    (r"gemm_w4a4_kernel(?:<\d+, \d+, \d+, \d+, true,|I(?:Li\d+E){4}Lb1E)", "gate_up_gelu"),
-    (r"gemm_w4a4_kernel(?:<[^>]*, true, false>|I(?:Li\d+E){4}Lb0E(?:Li\d+E){2}Lb1E)", "qkv_rope"),
-    (r"gemm_w4a4_kernel(?:<7, 4, 8, 8,|ILi7ELi4ELi8ELi8E)", "down_residual"),
-    (r"gemm_w4a4_kernel(?:<7, 4, 4, 1, false,|ILi7ELi4ELi4ELi1ELb0E)", "gate_up"),
-    (r"gemm_w4a4_kernel(?:<2, 2, 4, 1,|ILi2ELi2ELi4ELi1E)", "o_residual"),
 )
+
+
+def _gemm_template_args(name: str) -> list[int] | None:
+    """The template arguments of a gemm_w4a4_kernel instance, from its demangled
+    (``<7, 4, 4, 1, true, ...>``) or mangled (``ILi7ELi4E...Lb1E...``) name: ints, with
+    booleans as 0 / 1.  None for other kernels."""
+    m = re.search(r"gemm_w4a4_kernel<([^>]*)>", name)
+    if m:
+        return [1 if a.strip() == "true" else 0 if a.strip() == "false" else int(a) for a in m.group(1).split(",")]
+    m = re.search(r"gemm_w4a4_kernelI((?:L[ib]\d+E)+)E", name)
+    if m:
+        return [int(v) for v in re.findall(r"L[ib](\d+)E", m.group(1))]
+    return None
+
+
+def kernel_class(name: str) -> str:
+    """Kernel class of a profiled kernel name.  gemm_w4a4_kernel<MI, NI, NWAVES, KW, GELU,
+    RING, WPE, QKV_PREP, QFUSE, E3M2>: the 776-token forward's GEMMs by their tile
+    configuration and epilogue."""
+    a = _gemm_template_args(name)
+    if a is not None:
+        mi, ni, nwaves, kw, gelu = a[:5]
+        qkv_prep = len(a) > 7 and a[7] == 1
+        qfuse = len(a) > 8 and a[8] == 1
+        if gelu:
+            return "gate_up_gelu_quant" if qfuse else "gate_up_gelu"
+        if qkv_prep:
+            return "qkv_rope"
+        if kw == 8:
+            return "down_residual"
+        if (mi, ni, nwaves, kw) == (7, 4, 4, 1):
+            return "gate_up"
+        if (mi, ni, nwaves, kw) == (2, 2, 4, 1):
+            return "o_residual"
+        return "gemm"
+    return next((c for rx, c in _KERNEL_CLASS_RULES if re.search(rx, name)), "other")
 
 
 def profiled_in_forward(torch, replay, reps: int = 10, warm_s: float = 0.5) -> dict | None:
@@ -523,7 +578,7 @@ def profiled_in_forward(torch, replay, reps: int = 10, warm_s: float = 0.5) -> d
         dur = getattr(e, "device_time_total", None)
         if dur is None:
             dur = e.cuda_time_total
-        label = next((c for rx, c in _KERNEL_CLASS_RULES if re.search(rx, e.name)), "other")
+        label = kernel_class(e.name)
         per[label].append(float(dur))
     if not per:
         return None
@@ -565,8 +620,12 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "quant_k16384": lambda: kb.quant(m, inter),
         "qkv": lambda: kb.gemm(m, h, [2048, 256, 256]),
         "o": lambda: kb.gemm(m, h, [2048]),
-        "gate_up": lambda: kb.gemm(m, h, [inter, inter]),
-        "gate_up_gelu": lambda: kb.gemm(m, h, [inter, inter], gelu=True),
+        # gate/up as the forward runs it: E3M2 operands (the load-time default) unless
+        # PI05_W4A4_E3M2=0; the INT4 kernels beside them
+        "gate_up": lambda: kb.gemm(m, h, [inter, inter], e3m2=E3M2_GATE_UP),
+        "gate_up_gelu": lambda: kb.gemm(m, h, [inter, inter], gelu=True, e3m2=E3M2_GATE_UP),
+        "gate_up_int4": lambda: kb.gemm(m, h, [inter, inter]),
+        "gate_up_gelu_int4": lambda: kb.gemm(m, h, [inter, inter], gelu=True),
         "down": lambda: kb.gemm(m, inter, [h]),
         "o_residual": lambda: kb.gemm(m, h, [2048], residual=True),
         "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
@@ -890,8 +949,9 @@ def main() -> int:
         "unit": "TFLOP/s",
         "frac": round(dk["tops"] / INT8_PEAK_TOPS, 4),
         "traffic": traffic,
-        "kernel": "gemm_w4a4_kernel (gate/up, int4_gemm2)" if args.unfused_gelu
-                  else "gemm_w4a4_kernel (gate/up + GELU-tanh*up epilogue, int4_gemm2_gelu)",
+        "kernel": ("gemm_w4a4_kernel (gate/up, int4_gemm2)" if args.unfused_gelu
+                   else "gemm_w4a4_kernel (gate/up + GELU-tanh*up epilogue, int4_gemm2_gelu)")
+                  + (", E3M2 operands on the FP6 MFMA (v_mfma_f32_16x16x128_f8f6f4)" if E3M2_GATE_UP else ""),
         "ops_per_launch": dk["ops"],
         "avg_launch_us": dk["avg_us"],
         "ops_unit": "int8 MAC x 2 per second (dense int8 MFMA)",
