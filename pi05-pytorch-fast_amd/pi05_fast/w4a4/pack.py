@@ -250,18 +250,26 @@ def e3m2_to_float(bits: torch.Tensor) -> torch.Tensor:
     return torch.where((b >> 5) & 1 == 1, -mag, mag)
 
 
-def _slot_values(slot_bytes: torch.Tensor) -> torch.Tensor:
-    """[..., 24] uint8 lane slots -> [..., 32] float64 E3M2 values."""
-    bits = torch.stack([(slot_bytes.to(torch.int64) >> i) & 1 for i in range(8)], dim=-1)  # little-endian bits
-    bits = bits.reshape(*slot_bytes.shape[:-1], 32, 6)
-    return e3m2_to_float((bits << torch.arange(6)).sum(dim=-1))
+def _slot_codes(slot_bytes: torch.Tensor) -> torch.Tensor:
+    """[..., 24] uint8 lane slots -> [..., 32] int8 codes.  Each slot is read as three
+    little-endian 64-bit words; field j (bits 6j .. 6j+5) is decoded through the 64-entry
+    value table of ``e3m2_to_float``.  Every field must be an integer value."""
+    import numpy as np
 
-
-def _as_codes(vals: torch.Tensor) -> torch.Tensor:
-    codes = torch.round(vals)
-    if not torch.equal(codes, vals):
+    u = np.ascontiguousarray(slot_bytes.numpy()).view("<u8")  # [..., 3]
+    words = [np.ascontiguousarray(u[..., i]) for i in range(3)]
+    fields = []
+    for j in range(32):
+        w, off = divmod(6 * j, 64)
+        f = words[w] >> np.uint64(off)
+        if off > 58:
+            f = f | (words[w + 1] << np.uint64(64 - off))
+        fields.append((f & np.uint64(63)).astype(np.uint8))
+    fields = np.stack(fields, axis=-1)
+    vals = e3m2_to_float(torch.arange(64)).numpy()
+    if not np.take((np.rint(vals) == vals).astype(np.uint8), fields).all():
         raise ValueError("E3M2 codes hold a non-integer value")
-    return codes.to(torch.int8)
+    return torch.from_numpy(np.take(np.rint(vals).astype(np.int8), fields))
 
 
 def codes_from_e3m2_fragments(q6: torch.Tensor, m: int, k: int) -> torch.Tensor:
@@ -270,9 +278,10 @@ def codes_from_e3m2_fragments(q6: torch.Tensor, m: int, k: int) -> torch.Tensor:
     mb, kb = (m + 15) // 16, (k + 127) // 128
     f = q6.reshape(-1)[: mb * kb * 1536].to(torch.uint8).reshape(mb, kb, 1536)
     slots = torch.cat((f[:, :, :1024].reshape(mb, kb, 64, 16), f[:, :, 1024:].reshape(mb, kb, 64, 8)), dim=-1)
-    vals = _slot_values(slots)  # [mb, kb, lane, 32]: row 16 mb + lane % 16, k 128 kb + 32 (lane / 16) + j
-    vals = vals.reshape(mb, kb, 4, 16, 32).permute(0, 3, 1, 2, 4).reshape(mb * 16, kb * 128)
-    return _as_codes(vals[:m, :k])  # the pad rows of the last block are never written
+    # [mb, kb, lane, 24] slots of row 16 mb + lane % 16, codes 128 kb + 32 (lane / 16) + j; only
+    # the rows below M are decoded (the pad rows of the last block are never written)
+    slots = slots.reshape(mb, kb, 4, 16, 24).permute(0, 3, 1, 2, 4).reshape(mb * 16, kb * 4, 24)[:m]
+    return _slot_codes(slots).reshape(m, kb * 128)[:, :k]
 
 
 def codes_from_e3m2_weight(w6: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -283,10 +292,10 @@ def codes_from_e3m2_weight(w6: torch.Tensor, k: int) -> tuple[torch.Tensor, torc
     payload = flat[: n * kb * 24].view(torch.uint8).reshape(n // 32, kb, 3, 64, 16)
     rec = payload.permute(0, 1, 3, 2, 4).reshape(n // 32, kb, 64, 48)  # lane records
     slots = torch.stack((rec[..., :24], rec[..., 24:]), dim=2)  # [pair, kb, half, lane, 24]
-    vals = _slot_values(slots)  # column 32 p + 16 half + lane % 16, k 128 kb + 32 (lane / 16) + j
-    vals = vals.reshape(n // 32, kb, 2, 4, 16, 32).permute(0, 2, 4, 1, 3, 5).reshape(n, kb * 128)
+    codes = _slot_codes(slots)  # column 32 p + 16 half + lane % 16, k 128 kb + 32 (lane / 16) + j
+    codes = codes.reshape(n // 32, kb, 2, 4, 16, 32).permute(0, 2, 4, 1, 3, 5).reshape(n, kb * 128)
     scales = flat[n * kb * 24 : n * kb * 24 + n].view(torch.float32)
-    return _as_codes(vals[:, :k]), scales
+    return codes[:, :k], scales
 
 
 def quant_activation_cpu(x: torch.Tensor, rotate: bool | None = None) -> tuple[torch.Tensor, torch.Tensor]:
