@@ -730,3 +730,116 @@ def test_gelu_op_rejects_wmma_tiled_weights():
         ext._check_gelu_weights(x, tiled, tiled[:16])
     row = torch.empty(16384, 2048 // 8 + 1, dtype=torch.int32, device="meta")
     ext._check_gelu_weights(x, row, row)
+
+
+# ----------------------------------------------------------------------------- E3M2 form
+def _e3m2_encode_closed_form(c: int) -> int:
+    """The 6-bit E3M2 pattern of integer c from the format's definition alone (search over
+    the 64 patterns: (-1)^s 2^(e-3) (1 + m/4), subnormal m/16), independent of pack.py."""
+    for b in range(64):
+        s, e, m = b >> 5, (b >> 2) & 7, b & 3
+        v = (m / 16.0) if e == 0 else 2.0 ** (e - 3) * (1 + m / 4.0)
+        if (-v if s else v) == c and not (c == 0 and b != 0):
+            return b
+    raise AssertionError(f"{c} is not an E3M2 value")
+
+
+def test_e3m2_value_table():
+    """OCP FP6 E3M2 known values, and every INT4 code (including -8 and 8) is one."""
+    from pi05_fast.w4a4 import pack
+
+    vals = pack.e3m2_to_float(torch.arange(64)).tolist()
+    assert vals[0x1F] == 28.0 and vals[0x01] == 0.0625 and vals[0x0C] == 1.0 and vals[0x04] == 0.25
+    assert vals[0x18] == 8.0 and vals[0x38] == -8.0 and vals[0x17] == 7.0 and vals[0x15] == 5.0
+    assert vals[0x20] == 0.0  # negative zero
+    assert {_e3m2_encode_closed_form(c) for c in range(-8, 9)} == {
+        0x00, 0x0C, 0x10, 0x12, 0x14, 0x15, 0x16, 0x17, 0x18, 0x2C, 0x30, 0x32, 0x34, 0x35, 0x36, 0x37, 0x38}
+
+
+def _pack_slot(codes32) -> bytes:
+    bits = 0
+    for j, c in enumerate(codes32):
+        bits |= _e3m2_encode_closed_form(int(c)) << (6 * j)
+    return bits.to_bytes(24, "little")
+
+
+def test_e3m2_decoders_against_an_independent_packer():
+    """pack.codes_from_e3m2_weight / codes_from_e3m2_fragments read back what a packer
+    written from the layout's definition (include/pi05_w4a4.h) lays down."""
+    from pi05_fast.w4a4 import pack
+
+    rng = np.random.default_rng(5)
+    n, k = 64, 256
+    kb = k // 128
+    codes = rng.integers(-8, 9, size=(n, k))
+    scales = rng.random(n).astype(np.float32)
+    payload = np.zeros((n // 32, kb, 3, 64, 16), np.uint8)
+    for p_ in range(n // 32):
+        for b in range(kb):
+            for lane in range(64):
+                rec = b"".join(_pack_slot(codes[32 * p_ + 16 * h + lane % 16, 128 * b + 32 * (lane // 16):][:32])
+                               for h in range(2))
+                for c in range(3):
+                    payload[p_, b, c, lane] = np.frombuffer(rec[16 * c:16 * c + 16], np.uint8)
+    w6 = np.zeros(n * (3 * k // 16 + 16), np.int32)
+    w6[: n * kb * 24] = payload.reshape(-1).view(np.int32)
+    w6[n * kb * 24: n * kb * 24 + n] = scales.view(np.int32)
+    got, sc = pack.codes_from_e3m2_weight(torch.from_numpy(w6.reshape(n, -1)), k)
+    assert np.array_equal(got.numpy(), codes) and np.array_equal(sc.numpy(), scales)
+
+    m = 20  # two row blocks, the second partly padding
+    acts = rng.integers(-7, 8, size=(m, k))
+    frags = np.zeros((2, kb, 1536), np.uint8)
+    for mb in range(2):
+        for b in range(kb):
+            for lane in range(64):
+                row = 16 * mb + lane % 16
+                slot = _pack_slot(acts[row, 128 * b + 32 * (lane // 16):][:32]) if row < m else bytes(24)
+                frags[mb, b, 16 * lane:16 * lane + 16] = np.frombuffer(slot[:16], np.uint8)
+                frags[mb, b, 1024 + 8 * lane:1024 + 8 * lane + 8] = np.frombuffer(slot[16:], np.uint8)
+    got = pack.codes_from_e3m2_fragments(torch.from_numpy(frags.reshape(-1)), m, k)
+    assert np.array_equal(got.numpy(), acts)
+
+
+def test_e3m2_sizes_and_layout_marker(lib):
+    from pi05_fast.w4a4 import extension as ext
+    from pi05_fast.w4a4.linear import W4A4Linear
+
+    for m, k in ((1, 2048), (776, 2048), (17, 4096)):
+        assert ext._q6_bytes(m, k) == lib.pi05w4a4_q_e3m2_bytes(m, k) == (m + 15) // 16 * (k // 128) * 1536
+    for n, k in ((16384, 2048), (64, 4096)):
+        assert lib.pi05w4a4_e3m2_words(n, k) == n * (k // 128) * 24 + n <= n * (3 * k // 16 + 16)
+
+    def meta(n, w):
+        return torch.empty((n, w), dtype=torch.int32, device="meta")
+
+    assert ext.is_e3m2_layout(meta(16384, 3 * 2048 // 16 + 16), 2048)
+    assert not ext.is_e3m2_layout(meta(16384, 2048 // 8 + 16), 2048)
+    assert not ext.is_e3m2_layout(meta(48, 3 * 2048 // 16 + 16), 2048)  # N % 32
+    assert not ext.is_mfma_layout(meta(16384, 3 * 2048 // 16 + 16), 2048)
+    lin = W4A4Linear(torch.zeros(64, 3 * 2048 // 16 + 16, dtype=torch.int32), in_features=2048)
+    assert lin.e3m2 and lin.mfma and "layout=e3m2" in lin.extra_repr()
+    lin4 = W4A4Linear(torch.zeros(64, 2048 // 8 + 16, dtype=torch.int32), in_features=2048)
+    assert lin4.mfma and not lin4.e3m2
+
+
+def test_e3m2_abi_validation_without_gpu(lib):
+    """Argument errors come back before any launch (no GPU needed)."""
+    import ctypes
+
+    vp = ctypes.c_void_p
+    w = (vp * 2)(16, 16)
+    n = (ctypes.c_int32 * 2)(64, 32)
+    y = (vp * 2)(16, 16)
+    assert lib.pi05w4a4_gemm_e3m2(16, 16, 8, 2048, 2, w, n, y, 1, None) != 0  # gate/up N differ
+    assert b"same N" in lib.pi05w4a4_last_error()
+    n2 = (ctypes.c_int32 * 2)(48, 48)
+    assert lib.pi05w4a4_gemm_e3m2(16, 16, 8, 2048, 2, w, n2, y, 0, None) != 0
+    assert b"N % 32" in lib.pi05w4a4_last_error()
+    n3 = (ctypes.c_int32 * 2)(64, 64)
+    assert lib.pi05w4a4_gemm_e3m2(16, 16, 8, 2000, 2, w, n3, y, 0, None) != 0
+    assert b"K % 128" in lib.pi05w4a4_last_error()
+    assert lib.pi05w4a4_quantize_e3m2(16, 8, 1024, 16, 16, None) != 0
+    assert b"K = 2048" in lib.pi05w4a4_last_error()
+    assert lib.pi05w4a4_repack_weight_e3m2(16, 64, 2048, 16, None) != 0  # in place
+    assert lib.pi05w4a4_gemm_e3m2(16, 16, 0, 2048, 2, w, n3, y, 0, None) == 0  # M = 0: nothing to do
