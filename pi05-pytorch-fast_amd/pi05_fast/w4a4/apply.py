@@ -96,6 +96,9 @@ def load_time_weight(
     if preshuffled:
         w = preshuffle_wmma_weight(w, in_features)
     elif row_pad_words > 1 and w.shape[1] == logical_words + 1:
+        if in_features % 128 == 0 and row_pad_words == in_features // 16 + 16:
+            raise ValueError(f"PI05_W4A4_ROW_PAD_WORDS={row_pad_words} collides with the E3M2 layout marker "
+                             f"stride 3K/16+16 at K={in_features}")
         w = torch.nn.functional.pad(w, (0, row_pad_words - 1))
     if device is not None:
         w = w.to(device)
