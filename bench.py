@@ -185,15 +185,20 @@ class KernelBench:
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "pair_offset_us": self.last_pair_offset_us}
 
-    def rmsnorm_quant(self, m, k=2048):
+    def rmsnorm_quant(self, m, k=2048, e3m2=False):
+        """The RMSNorm + K = 2048 activation quant kernel; `e3m2`: its E3M2-fragment form
+        (the gate/up input)."""
         torch, lib, P = self.torch, self.lib, self.ext._ptr
         x = torch.randn(m, k, device=self.dev, dtype=torch.float16)
         w = torch.randn(k, device=self.dev, dtype=torch.float16) * 0.1
-        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        if e3m2:
+            q = torch.empty(int(lib.pi05w4a4_q_e3m2_bytes(m, k)), dtype=torch.uint8, device=self.dev)
+        else:
+            q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
         sa = torch.empty(m, dtype=torch.float32, device=self.dev)
-        us = self._time(lambda: self._check(lib.pi05w4a4_rmsnorm_quantize(
-            P(x), P(w), 1e-6, 1, m, k, P(q), P(sa), self._stream())))
-        nbytes = 2.0 * m * k + 2 * k + m * k / 2 + 4 * m
+        fn = lib.pi05w4a4_rmsnorm_quantize_e3m2 if e3m2 else lib.pi05w4a4_rmsnorm_quantize
+        us = self._time(lambda: self._check(fn(P(x), P(w), 1e-6, 1, m, k, P(q), P(sa), self._stream())))
+        nbytes = 2.0 * m * k + 2 * k + m * k * (0.75 if e3m2 else 0.5) + 4 * m
         gbs = nbytes / (us * 1e-6) / 1e9
         return {"m": m, "k": k, "avg_us": round(us, 3), "bytes": nbytes, "gbs": round(gbs, 1),
                 "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "pair_offset_us": self.last_pair_offset_us}
@@ -630,6 +635,7 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
         "o_residual": lambda: kb.gemm(m, h, [2048], residual=True),
         "down_residual": lambda: kb.gemm(m, inter, [h], residual=True),
         "rmsnorm_quant_k2048": lambda: kb.rmsnorm_quant(m),
+        "rmsnorm_quant_e3m2": lambda: kb.rmsnorm_quant(m, e3m2=True),
         "qkv_rope": lambda: kb.qkv_rope(1, m),
         "gate_up_gelu_quant": lambda: kb.gelu_quant(m),
         "gate_up_gelu_then_quant": lambda: kb.gelu_quant(m, fused=False),
@@ -921,11 +927,13 @@ def main() -> int:
     # gate/up quants, the o-proj quant inside the attention kernel, residual adds in the o
     # and down epilogues).
     fused_kv = os.environ.get("PI05_W4A4_FUSE_KV", "1") != "0" and args.tokens % 8 == 0
-    calls = {"rmsnorm_quant_k2048": 2, "quant_k2048": 0, "quant_k16384": 1, "qkv": 0 if fused_kv else 1,
+    calls = {"rmsnorm_quant_k2048": 1 if E3M2_GATE_UP else 2, "rmsnorm_quant_e3m2": 1 if E3M2_GATE_UP else 0,
+             "quant_k2048": 0, "quant_k16384": 1, "qkv": 0 if fused_kv else 1,
              "qkv_rope": 1 if fused_kv else 0, "o_residual": 1, "down_residual": 1, "gate_up_gelu": 1, "gate_up": 0,
              "o": 0, "down": 0}
     if args.unfused_gelu:
-        calls.update({"rmsnorm_quant_k2048": 0, "quant_k2048": 3, "qkv": 1, "qkv_rope": 0, "o_residual": 0,
+        calls.update({"rmsnorm_quant_k2048": 0, "rmsnorm_quant_e3m2": 0, "quant_k2048": 3, "qkv": 1, "qkv_rope": 0,
+                      "o_residual": 0,
                       "down_residual": 0, "gate_up_gelu": 0, "gate_up": 1, "o": 1, "down": 1})
     for name, c in calls.items():
         kernels[name]["calls_per_layer"] = c
@@ -956,7 +964,8 @@ def main() -> int:
         "avg_launch_us": dk["avg_us"],
         "ops_unit": "int8 MAC x 2 per second (dense int8 MFMA)",
         "traffic_source": traffic_src,
-        "algorithmic_bytes_per_launch": dk["bytes"],
+        # E3M2: the operand bytes of the form the kernel reads (6 bits per code)
+        "algorithmic_bytes_per_launch": dk.get("operand_bytes", dk["bytes"]),
         # the same kernel timed inside the eager forward (in_forward below)
         "in_forward": in_forward_roof,
     }

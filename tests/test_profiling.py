@@ -85,8 +85,11 @@ def test_traffic_table_calibrates_with_the_copy(tmp_path):
 def test_traffic_classes_algorithmic_bytes():
     """The 776-token byte counts stated in the table's descriptions."""
     c = prof.TRAFFIC_CLASSES
-    assert c["gate_up_gelu"][2] / 1e6 == pytest.approx(59.91, abs=0.01)
-    assert c["gate_up"][2] / 1e6 == pytest.approx(85.34, abs=0.01)
+    assert c["gate_up_gelu_int4"][2] / 1e6 == pytest.approx(59.91, abs=0.01)
+    assert c["gate_up_int4"][2] / 1e6 == pytest.approx(85.34, abs=0.01)
+    assert c["gate_up_gelu"][2] / 1e6 == pytest.approx(77.09, abs=0.01)  # E3M2 operands: 6 bits per code
+    assert c["gate_up"][2] / 1e6 == pytest.approx(102.51, abs=0.01)
+    assert c["rmsnorm_quant_e3m2"][2] / 1e6 == pytest.approx(4.38, abs=0.01)
     assert c["down_residual"][2] / 1e6 == pytest.approx(29.50, abs=0.01)
     assert c["o_residual"][2] / 1e6 == pytest.approx(9.26, abs=0.01)
     assert c["quant_k16384"][2] / 1e6 == pytest.approx(31.79, abs=0.01)
