@@ -564,7 +564,19 @@ int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, in
   if (q6 == nullptr || sa == nullptr) return fail(PI05W4A4_EINVAL, "null activation codes or scales");
   if (!aligned(q6, 16) || !aligned(sa, 4))
     return fail(PI05W4A4_EINVAL, "q6 must be 16-byte aligned, sa 4-byte aligned");
-  const int64_t mtiles = cdiv(m, 112);
+  // Tiles: 112 x 256 (GELU: 112 x 128 gate + up) when they give at least 1.5 workgroups per
+  // CU, else 32 x 128 (the narrow GEMMs: QKV, o).
+  const int64_t cus = w4a4::device_cu_count();
+  const int64_t m7 = cdiv(m, 112);
+  int64_t n7 = 0, n2 = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    n7 += cdiv(n[g], gelu_up != 0 ? 128 : 256);
+    n2 += cdiv(n[g], 128);
+  }
+  if (gelu_up != 0) n7 = cdiv(n[0], 128);
+  const bool narrow = gelu_up == 0 && 2 * m7 * n7 < 3 * cus;
+  const int tile_cfg = narrow ? w4a4::kCfg2x2 : w4a4::kCfg7x4;
+  const int64_t mtiles = narrow ? cdiv(m, 32) : m7;
   if (mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
   w4a4::GemmParams p{};
   p.q = static_cast<const int32_t*>(q6);
@@ -572,7 +584,7 @@ int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, in
   p.m = m;
   p.k = k;
   p.ngroups = ngroups;
-  const int tile_cols = gelu_up != 0 ? 128 : 256;  // 4 waves x 64 columns (GELU: 32 gate + 32 up)
+  const int tile_cols = gelu_up != 0 ? 128 : (narrow ? 128 : 256);  // 4 waves x 64 (GELU: 32 + 32) or 32 columns
   int tile_begin = 0;
   int64_t n_total = 0;
   for (int g = 0; g < ngroups; ++g) {
@@ -591,7 +603,7 @@ int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, in
   p.n_total = static_cast<int32_t>(n_total);
   p.gelu_pair_n = gelu_up != 0 ? n[0] : 0;
   p.mode = gelu_up != 0 ? w4a4::kEpiGeluUp : w4a4::kEpiFp16;
-  return hip_status(w4a4::launch_gemm_e3m2(p, static_cast<hipStream_t>(stream)), "E3M2 gemm launch");
+  return hip_status(w4a4::launch_gemm_e3m2(p, tile_cfg, static_cast<hipStream_t>(stream)), "E3M2 gemm launch");
 }
 
 int pi05w4a4_gemm_gelu_up(const int32_t* q, const float* sa, int64_t m, int32_t k,

@@ -284,8 +284,8 @@ template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool
           bool E3M2 = false>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!(GELU && QKV_PREP), "the attention prep is a fp16 epilogue");
-  static_assert(!E3M2 || (MI == 7 && NI == 4 && NWAVES == 4 && KW == 1 && !QKV_PREP && !QFUSE),
-                "E3M2 operands: 112 x 256 tiles, four waves along N");
+  static_assert(!E3M2 || (NI % 2 == 0 && NWAVES == 4 && KW == 1 && !QFUSE && (!GELU || NI == 4)),
+                "E3M2 operands: four waves along N, whole column pairs per wave");
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
   static_assert(NWAVES % KW == 0 && (KW & (KW - 1)) == 0, "waves split as NW x KW");
   constexpr int NW = NWAVES / KW;
@@ -315,7 +315,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   constexpr int kLdsRed = kLdsSw + NCOL * 4;
   constexpr int kLdsStage = kLdsRed + (kSpread ? KW * PM * NI * 64 * 16 : 0);
   constexpr int kLdsA6 = (kLdsStage + (kSpread ? KW : NW) * 16 * LSR * 2 + 15) / 16 * 16;
-  constexpr int kA6Stage = 7 * 1024 + 4 * 1024;  // 7 d0-3 chunks, 4 chunks of d4-5 parts (3.5 KB used)
+  // E3M2 A stage: MI 1 KB chunks of d0-3 parts, then ceil(MI / 2) 1 KB chunks of the
+  // concatenated 512-byte d4-5 parts (the last one half used when MI is odd).
+  constexpr int kA6Chunks = MI + (MI + 1) / 2;
+  constexpr int kA6Stage = kA6Chunks * 1024;
   constexpr int kLdsGemm = kLdsA6 + (E3M2 ? 2 * kA6Stage : 0);
   constexpr int kLdsPool = (QFUSE && kQuantLdsBytes > kLdsGemm) ? kQuantLdsBytes : kLdsGemm;
   __shared__ __align__(16) char lds_pool[kLdsPool];
@@ -617,54 +620,56 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // their multiply, so no memory instruction is conditional and the compiler's vmcnt
   // bookkeeping stays exact.
   if constexpr (E3M2) {
-    // A: chunk c of a stage (c < 7: the d0-3 part of row block c of the tile; c >= 7:
-    // bytes 1024 (c - 7) .. of the concatenated d4-5 parts, the last chunk half used and
-    // its upper lanes clamped to re-read in-bounds bytes into an unread LDS area).  Wave
-    // w issues chunks w, w + 4, w + 8 below 11.  Row blocks past M are clamped.
+    // A: chunk c of a stage (c < MI: the d0-3 part of row block c of the tile; c >= MI:
+    // bytes 1024 (c - MI) .. of the concatenated d4-5 parts; for odd MI the last chunk is
+    // half used and its upper lanes re-read in-bounds bytes into an unread LDS area).  Wave
+    // w issues chunks w, w + 4, ... below kA6Chunks.  Row blocks past M are clamped.
+    constexpr int kAPerWave = (kA6Chunks + NWAVES - 1) / NWAVES;
     char* const a6 = lds_pool + kLdsA6;
-    const char* agp[3];
-    int aoff[3];
+    const char* agp[kAPerWave];
+    int aoff[kAPerWave];
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
-      const int c = wave + 4 * j;
+    for (int j = 0; j < kAPerWave; ++j) {
+      const int c = min(wave + NWAVES * j, kA6Chunks - 1);
       int blk, off;
-      if (c < 7) {
+      if (c < MI) {
         blk = c;
         off = lane * 16;
       } else {
-        const int t = (c - 7) * 1024 + lane * 16;
-        blk = min(t >> 9, 6);
+        const int t = (c - MI) * 1024 + lane * 16;
+        blk = min(t >> 9, MI - 1);
         off = 1024 + (t & 511);
       }
       const int mb = min(mt * MI + blk, p.mblocks - 1);
       agp[j] = reinterpret_cast<const char*>(p.q) + static_cast<int64_t>(mb) * KB128 * kE3m2FragBytes + off;
       aoff[j] = c * 1024;
     }
-    const int nachunks = wave < 3 ? 3 : 2;  // 11 chunks over 4 waves
+    const int nachunks = (kA6Chunks - wave + NWAVES - 1) / NWAVES;
     auto load_a6 = [&](int kb, int slot) {
       const int64_t o = static_cast<int64_t>(min(kb, kb_end - 1)) * kE3m2FragBytes;
 #pragma unroll
-      for (int j = 0; j < 3; ++j) {
+      for (int j = 0; j < kAPerWave; ++j) {
         if (j >= nachunks) break;
         __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void*)(agp[j] + o),
                                          (__attribute__((address_space(3))) void*)(a6 + slot * kA6Stage + aoff[j]),
                                          16, 0, 0);
       }
     };
-    // B: the wave's two column pairs (GELU: its gate pair and its up pair; else two
+    // B: the wave's NI / 2 column pairs (GELU: its gate pair and its up pair; else
     // consecutive pairs), pairs past N clamped.
-    const char* bp6[2];
+    constexpr int NP = NI / 2;
+    const char* bp6[NP];
 #pragma unroll
-    for (int qd = 0; qd < 2; ++qd) {
+    for (int qd = 0; qd < NP; ++qd) {
       const int pair = min((GELU ? wcol : wcol + 32 * qd) >> 5, (N >> 5) - 1);
       const int32_t* base = (GELU && qd == 1) ? W2 : W;
       bp6[qd] = reinterpret_cast<const char*>(base) + static_cast<int64_t>(pair) * KB128 * kE3m2PairBytes + lane * 16;
     }
-    v4i b6[2][2][3];
-    auto load_b6 = [&](int kb, v4i (&b)[2][3]) {
+    v4i b6[2][NP][3];
+    auto load_b6 = [&](int kb, v4i (&b)[NP][3]) {
       const int64_t o = static_cast<int64_t>(min(kb, kb_end - 1)) * kE3m2PairBytes;
 #pragma unroll
-      for (int qd = 0; qd < 2; ++qd)
+      for (int qd = 0; qd < NP; ++qd)
 #pragma unroll
         for (int c = 0; c < 3; ++c) b[qd][c] = *reinterpret_cast<const v4i*>(bp6[qd] + o + c * 1024);
     };
@@ -680,7 +685,7 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi) {
           const v4i lo = *reinterpret_cast<const v4i*>(st + mi * 1024 + lane * 16);
-          const int2 hi = *reinterpret_cast<const int2*>(st + 7 * 1024 + mi * 512 + lane * 8);
+          const int2 hi = *reinterpret_cast<const int2*>(st + MI * 1024 + mi * 512 + lane * 8);
           aop[mi] = e3m2_op(lo, hi.x, hi.y);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -1146,14 +1151,23 @@ hipError_t launch_gemm_gelu_quant(const GemmParams& p, int nquant, hipStream_t s
   return hipGetLastError();
 }
 
-hipError_t launch_gemm_e3m2(const GemmParams& p, hipStream_t stream) {
-  if (p.ksplit != 1 || (p.mode != kEpiFp16 && p.mode != kEpiGeluUp) || p.rope_group != 0 || p.res != nullptr)
+hipError_t launch_gemm_e3m2(const GemmParams& p, int tile_cfg, hipStream_t stream) {
+  if (p.ksplit != 1 || (p.mode != kEpiFp16 && p.mode != kEpiGeluUp)) return hipErrorInvalidValue;
+  const bool gelu = p.mode == kEpiGeluUp;
+  const bool prep = p.rope_group > 0;
+  if ((gelu && (prep || p.res != nullptr || tile_cfg != kCfg7x4)) || (tile_cfg != kCfg7x4 && tile_cfg != kCfg2x2))
     return hipErrorInvalidValue;
   const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles));
-  if (p.mode == kEpiGeluUp)
+  if (gelu)
     gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, true><<<grid, 256, 0, stream>>>(p);
-  else
+  else if (tile_cfg == kCfg7x4 && !prep)
     gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, true><<<grid, 256, 0, stream>>>(p);
+  else if (tile_cfg == kCfg7x4)
+    gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, true, false, true><<<grid, 256, 0, stream>>>(p);
+  else if (!prep)
+    gemm_w4a4_kernel<2, 2, 4, 1, false, 2, 2, false, false, true><<<grid, 256, 0, stream>>>(p);
+  else
+    gemm_w4a4_kernel<2, 2, 4, 1, false, 2, 2, true, false, true><<<grid, 256, 0, stream>>>(p);
   return hipGetLastError();
 }
 
