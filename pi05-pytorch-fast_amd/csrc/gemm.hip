@@ -67,6 +67,7 @@ namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v12i __attribute__((ext_vector_type(12)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -665,13 +666,20 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       const int32_t* base = (GELU && qd == 1) ? W2 : W;
       bp6[qd] = reinterpret_cast<const char*>(base) + static_cast<int64_t>(pair) * KB128 * kE3m2PairBytes + lane * 16;
     }
-    v4i b6[2][NP][3];
-    auto load_b6 = [&](int kb, v4i (&b)[NP][3]) {
+    // A pair's three loads land in one 12-dword value, so that both fragments are
+    // consecutive register runs of it (no copies to assemble the MFMA operands).
+    v12i b6[2][NP];
+    auto load_b6 = [&](int kb, v12i (&b)[NP]) {
       const int64_t o = static_cast<int64_t>(min(kb, kb_end - 1)) * kE3m2PairBytes;
 #pragma unroll
-      for (int qd = 0; qd < NP; ++qd)
-#pragma unroll
-        for (int c = 0; c < 3; ++c) b[qd][c] = *reinterpret_cast<const v4i*>(bp6[qd] + o + c * 1024);
+      for (int qd = 0; qd < NP; ++qd) {
+        const v4i c0 = *reinterpret_cast<const v4i*>(bp6[qd] + o);
+        const v4i c1 = *reinterpret_cast<const v4i*>(bp6[qd] + o + 1024);
+        const v4i c2 = *reinterpret_cast<const v4i*>(bp6[qd] + o + 2048);
+        const v8i c01 = __builtin_shufflevector(c0, c1, 0, 1, 2, 3, 4, 5, 6, 7);
+        const v8i c2x = __builtin_shufflevector(c2, c2, 0, 1, 2, 3, 4, 5, 6, 7);
+        b[qd] = __builtin_shufflevector(c01, c2x, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11);
+      }
     };
     load_a6(kb_begin, 0);
     load_b6(kb_begin, b6[0]);
@@ -697,9 +705,9 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
 #pragma unroll
           for (int ni = 0; ni < NI; ++ni) {
             // fragment ni: pair ni / 2, column half ni % 2 (dwords 0-5 or 6-11 of the record)
-            const v4i* r = b6[j][ni >> 1];
-            const v8i bop = (ni & 1) ? e3m2_op(v4i{r[1].z, r[1].w, r[2].x, r[2].y}, r[2].z, r[2].w)
-                                     : e3m2_op(r[0], r[1].x, r[1].y);
+            const v12i r = b6[j][ni >> 1];
+            const v8i bop = (ni & 1) ? __builtin_shufflevector(r, r, 6, 7, 8, 9, 10, 11, 6, 7)
+                                     : __builtin_shufflevector(r, r, 0, 1, 2, 3, 4, 5, 0, 1);
             acc[mi][ni] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bop, aop[mi], acc[mi][ni], 3, 3, 0, 0, 0, 0);
           }
         }
