@@ -272,6 +272,40 @@ class KernelBench:
         return rec
 
 
+    def qkv_block(self, m, warm, copies=200, ns=(2048, 256, 256), k=2048):
+        """The QKV block of a decoder layer as launched: RMSNorm + quant, then the QKV GEMM,
+        the timed graph cycling `copies` weight sets (from HBM, as in `gemm(copies=...)`).
+        `warm`: the norm + quant launch reads the set its GEMM is about to use into the
+        Infinity Cache (pi05w4a4_rmsnorm_quantize_warm)."""
+        torch, lib, P = self.torch, self.lib, self.ext._ptr
+        gen = torch.Generator(device=self.dev).manual_seed(20261202 + m)
+        x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
+        nw = torch.randn(k, device=self.dev, dtype=torch.float16, generator=gen) * 0.1
+        q = torch.empty(int(lib.pi05w4a4_q_words(m, k)), dtype=torch.int32, device=self.dev)
+        sa = torch.empty(m, dtype=torch.float32, device=self.dev)
+        g = len(ns)
+        n_arr = (ctypes.c_int32 * g)(*ns)
+        wsb = int(lib.pi05w4a4_gemm_workspace_bytes(m, k, g, n_arr, 0))
+        work = torch.empty(max(wsb, 16), dtype=torch.uint8, device=self.dev)
+        outs = [torch.empty(m, n, dtype=torch.float16, device=self.dev) for n in ns]
+        y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in outs])
+        sets = [[self._packed(n, k, gen) for n in ns] for _ in range(copies)]
+        w_arrs = [(ctypes.c_void_p * g)(*[w.data_ptr() for w in s]) for s in sets]
+        warm_bytes = (ctypes.c_size_t * g)(*[w.numel() * w.element_size() for w in sets[0]])
+        turn = itertools.cycle(range(copies))
+
+        def fn():
+            i = next(turn)
+            if warm:
+                self._check(lib.pi05w4a4_rmsnorm_quantize_warm(P(x), P(nw), 1e-6, 1, m, k, P(q), P(sa), w_arrs[i],
+                                                               warm_bytes, g, self._stream()))
+            else:
+                self._check(lib.pi05w4a4_rmsnorm_quantize(P(x), P(nw), 1e-6, 1, m, k, P(q), P(sa), self._stream()))
+            self._check(lib.pi05w4a4_gemm_multi(P(q), P(sa), m, k, g, w_arrs[i], n_arr, y_arr, P(work), wsb,
+                                                self._stream()))
+
+        return round(self._time(fn, iters=copies), 3)
+
     def gelu_quant(self, m, k=2048, n=16384, fused=True):
         """Gate/up with the GELU-tanh*up epilogue and the down projection's activation quant
         of its output: one launch (pi05w4a4_gemm_gelu_up_quant) or, with fused=False, the
@@ -674,6 +708,10 @@ def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
             "gemm_cold_gbs": cold["gbs"], "frac_hbm_cold": round(cold["gbs"] / HBM_PEAK_GBS, 4),
             "rmsnorm_quant_us": nq["avg_us"],
             "block_cold_us": round(cold["avg_us"] + nq["avg_us"], 3),
+            # the two launches back to back in one graph, without and with the norm + quant
+            # launch warming the weights of its GEMM
+            "block_cold_pair_us": kb.qkv_block(m, warm=False),
+            "block_cold_warm_us": kb.qkv_block(m, warm=True),
         }
     return out
 

@@ -225,6 +225,18 @@ int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
                               void* stream);
 
 /*
+ * pi05w4a4_rmsnorm_quantize plus cache warming: when the row workgroups (4 rows each) leave
+ * CUs without one, a workgroup per such CU reads warm_n <= 4 further device buffers
+ * (16-byte aligned, sizes multiples of 16 bytes) and discards the data, so that the GEMM
+ * after it finds them in the Infinity Cache.  No counterpart in the reference: the QKV
+ * entry ops pass their own weights with the quantization of their input.  Results are
+ * those of pi05w4a4_rmsnorm_quantize.
+ */
+int pi05w4a4_rmsnorm_quantize_warm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                   int64_t m, int32_t k, int32_t* q, float* sa, const void* const* warm_ptrs,
+                                   const size_t* warm_bytes, int32_t warm_n, void* stream);
+
+/*
  * Raw int32 accumulators acc[m, n] (row-major [M, N]) for bit-exact checks; no dequant.
  * Debug counterpart of the int32 accumulation inside gemm_iu4 (int4_gemm.cu:114-178).
  */

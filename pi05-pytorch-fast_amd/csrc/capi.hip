@@ -467,9 +467,12 @@ int pi05w4a4_permute_rope_pairs(const int32_t* src_mfma, int32_t k, int32_t* dst
   return ok();
 }
 
-int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
-                              int32_t unit_offset, int64_t m, int32_t k, int32_t* q, float* sa,
-                              void* stream) {
+}  // extern "C"
+
+namespace {
+static int rmsnorm_quantize_call(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                 int64_t m, int32_t k, int32_t* q, float* sa,
+                                 const w4a4::CacheWarmParams* warm, void* stream) {
   if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
   if (k != 2048) return fail(PI05W4A4_EINVAL, "the fused RMSNorm quantizer takes K = 2048, got %d", k);
   if (m == 0) return ok();
@@ -478,8 +481,27 @@ int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
     return fail(PI05W4A4_EINVAL, "x, w and q must be 16-byte aligned, sa 4-byte aligned");
   if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
   return hip_status(w4a4::launch_rmsnorm_quantize(x_fp16, w_fp16, eps, unit_offset != 0, m, k, q, sa,
-                                                  static_cast<float>(1.0 / std::sqrt(2048.0)), static_cast<hipStream_t>(stream)),
+                                                  static_cast<float>(1.0 / std::sqrt(2048.0)),
+                                                  static_cast<hipStream_t>(stream), warm),
                     "rmsnorm quantize launch");
+}
+}  // namespace
+
+extern "C" {
+
+int pi05w4a4_rmsnorm_quantize(const void* x_fp16, const void* w_fp16, float eps,
+                              int32_t unit_offset, int64_t m, int32_t k, int32_t* q, float* sa,
+                              void* stream) {
+  return rmsnorm_quantize_call(x_fp16, w_fp16, eps, unit_offset, m, k, q, sa, nullptr, stream);
+}
+
+int pi05w4a4_rmsnorm_quantize_warm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                   int64_t m, int32_t k, int32_t* q, float* sa, const void* const* warm_ptrs,
+                                   const size_t* warm_bytes, int32_t warm_n, void* stream) {
+  w4a4::CacheWarmParams warm;
+  const int rc = collect_warm(warm_ptrs, warm_bytes, warm_n, &warm);
+  if (rc) return rc;
+  return rmsnorm_quantize_call(x_fp16, w_fp16, eps, unit_offset, m, k, q, sa, &warm, stream);
 }
 
 // ---- E3M2 operand form (the q6 / w6 layouts of w4a4_internal.h)

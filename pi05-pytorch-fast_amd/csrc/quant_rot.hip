@@ -319,13 +319,18 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
 
 hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int unit_offset,
                                   int64_t m, int32_t k, int32_t* q, float* sa, float inv_sqrt_k,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, const CacheWarmParams* warm) {
   if (m <= 0) return hipSuccess;
   if (k != 2048) return hipErrorInvalidValue;
   int32_t* qcorr = q + q_payload_words((m + 15) / 16, kblocks128(k));
-  fwht_quant_kernel<11, 6, 4, true><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
+  // Cache warming: one workgroup for each CU that the row workgroups (4 rows each) leave
+  // without one; none once the rows cover every CU.
+  const int64_t row_blocks = (m + 3) / 4;
+  const int64_t cus = device_cu_count();
+  const int64_t extra = (warm != nullptr && warm->nbuf > 0 && row_blocks < cus) ? cus - row_blocks : 0;
+  fwht_quant_kernel<11, 6, 4, true><<<dim3(static_cast<unsigned>(row_blocks + extra)), 256, 0, stream>>>(
       static_cast<const _Float16*>(x), m, q, sa, qcorr, inv_sqrt_k, static_cast<const _Float16*>(w),
-      eps, unit_offset);
+      eps, unit_offset, extra > 0 ? *warm : CacheWarmParams{});
   return hipGetLastError();
 }
 

@@ -243,9 +243,10 @@ hipError_t launch_gelu_up(const void* g, const void* u, int64_t n, void* y, hipS
 hipError_t launch_rmsnorm(const void* x, const void* w, float eps, int unit_offset, int64_t m,
                           int32_t k, void* y, hipStream_t stream);
 // RMSNorm fused into the K = 2048 activation quant (hipErrorInvalidValue for other K).
+// With warm buffers, workgroups appended for the CUs that the rows leave idle read them.
 hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int unit_offset,
                                   int64_t m, int32_t k, int32_t* q, float* sa, float inv_sqrt_k,
-                                  hipStream_t stream);
+                                  hipStream_t stream, const CacheWarmParams* warm = nullptr);
 hipError_t launch_attn_kv_prep(const AttnParams& p, hipStream_t stream);
 hipError_t launch_prefix_attention(const AttnParams& p, hipStream_t stream);
 

@@ -110,6 +110,9 @@ def load_int4_gemm():
         "pi05w4a4_gelu_tanh_mul": (ctypes.c_int, [vp, vp, i64, vp, vp]),
         "pi05w4a4_gemm_residual": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, sz, vp]),
         "pi05w4a4_rmsnorm_quantize": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
+        "pi05w4a4_rmsnorm_quantize_warm": (
+            ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(sz), i32,
+                           vp]),
         "pi05w4a4_attn_kv_mfma_elems": (sz, [i64, i32, i32, i32]),
         "pi05w4a4_attn_kv_prep": (ctypes.c_int, [vp, vp, i64, vp, vp, i64, i32, i32, i32, vp, vp, vp]),
         "pi05w4a4_prefix_attention": (
@@ -550,9 +553,12 @@ def _gemm_from_q(q, sa, k, weights, out_shape_prefix, device, kind, gelu=False, 
 
 
 def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
-                      unit_offset: bool = True) -> tuple[torch.Tensor, torch.Tensor]:
+                      unit_offset: bool = True, warm: list[torch.Tensor] | None = None
+                      ) -> tuple[torch.Tensor, torch.Tensor]:
     """``quantize`` of ``rms_norm(x, weight, eps, unit_offset)`` in one kernel (K = 2048):
-    the norm's fp16 output is rotated and quantized without being stored."""
+    the norm's fp16 output is rotated and quantized without being stored.  ``warm``: up to 4
+    device tensors that the CUs left idle by the rows read into the Infinity Cache (the
+    GEMM's weights); the results are the same."""
     k = _check_x(x)
     if k != 2048:
         raise RuntimeError(f"the fused RMSNorm quantizer takes K = 2048, got {k}")
@@ -568,9 +574,41 @@ def rms_norm_quantize(x: torch.Tensor, weight: torch.Tensor, eps: float,
     q = torch.empty((_q_words(m, k),), dtype=torch.int32, device=dev)
     sa = torch.empty((m,), dtype=torch.float32, device=dev)
     with _on_device(dev):
-        _check(lib.pi05w4a4_rmsnorm_quantize(x2.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0, m, k,
-                                             q.data_ptr(), sa.data_ptr(), _stream(dev)), "pi05w4a4_rmsnorm_quantize")
+        wa = _warm_args(warm, "rms_norm_quantize") if warm else None
+        if wa is None:
+            _check(lib.pi05w4a4_rmsnorm_quantize(x2.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0, m,
+                                                 k, q.data_ptr(), sa.data_ptr(), _stream(dev)),
+                   "pi05w4a4_rmsnorm_quantize")
+        else:
+            _check(lib.pi05w4a4_rmsnorm_quantize_warm(x2.data_ptr(), w.data_ptr(), float(eps), 1 if unit_offset else 0,
+                                                      m, k, q.data_ptr(), sa.data_ptr(), *wa, _stream(dev)),
+                   "pi05w4a4_rmsnorm_quantize_warm")
     return q, sa
+
+
+# Weights up to this many bytes per call are read into the Infinity Cache by the norm +
+# quant launch ahead of their GEMM (the QKV projections: 2.6 MB at PaliGemma-2B sizes),
+# from this many rows on.  With fewer rows the launch is too short to hide the reads: at
+# M = 1 the norm + quant + QKV pair took 8.76 us with warming against 8.41 without, at
+# M = 640 13.58 against 14.14 (weights from HBM).
+_NORM_WARM_MAX_BYTES = 16 << 20
+_NORM_WARM_MIN_ROWS = 256
+
+
+def _norm_warm(ws: list[torch.Tensor], x: torch.Tensor) -> list[torch.Tensor] | None:
+    """The weights for the norm + quant launch of x to warm (PI05_W4A4_CACHE_WARM=0: none):
+    MFMA-layout weights only (what the GEMM reads), at most _NORM_WARM_MAX_BYTES in total,
+    for at least _NORM_WARM_MIN_ROWS rows."""
+    if os.environ.get("PI05_W4A4_CACHE_WARM", "1") == "0":
+        return None
+    k = int(x.size(-1))
+    if x.numel() // k < _NORM_WARM_MIN_ROWS:
+        return None
+    if not all(w.is_cuda and w.is_contiguous() and is_mfma_layout(w, k) for w in ws):
+        return None
+    if sum(w.numel() * w.element_size() for w in ws) > _NORM_WARM_MAX_BYTES:
+        return None
+    return list(ws)
 
 
 # Control blocks of pi05w4a4_gemm_gelu_up_quant, one per (device, stream): zeroed when
@@ -651,7 +689,7 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
     if residual is not None:  # before any launch: the kernel reads it through a raw pointer
         _check_residual(residual, x.device, (*x.shape[:-1], int(ws[0].size(0))))
     # the reference quantizes before checking the weights
-    q, sa = quantize(x, warm) if norm is None else rms_norm_quantize(x, *norm)
+    q, sa = quantize(x, warm) if norm is None else rms_norm_quantize(x, *norm, warm=warm)
     conv = []
     for w in ws:
         _check_packed(w, k)
@@ -859,7 +897,7 @@ def _rms_norm_qkv_rope_impl(x, norm_weight, eps, unit_offset, w_q, w_k_rope, w_v
     for name, t in (("cos", cos), ("sin", sin)):
         if not t.is_cuda or t.dtype != torch.float16 or t.device != x.device:
             raise RuntimeError(f"rms_norm_int4_gemm3_rope: {name} must be float16 on {x.device}")
-    q, sa = rms_norm_quantize(x, norm_weight, eps, unit_offset)
+    q, sa = rms_norm_quantize(x, norm_weight, eps, unit_offset, warm=_norm_warm([w_q, w_k_rope, w_v], x))
     return _gemm_qkv_rope(q, sa, k, w_q, w_k_rope, w_v, _rope_tables(cos, sin, b, s), b, s, x.device)
 
 
@@ -994,7 +1032,8 @@ def _register_custom_op() -> None:
         x: torch.Tensor, norm_weight: torch.Tensor, eps: float, unit_offset: bool,
         w0: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor,
     ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        a, b, c = _run(x, [w0, w1, w2], tiled=False, kind="int4_gemm3", norm=(norm_weight, eps, unit_offset))
+        a, b, c = _run(x, [w0, w1, w2], tiled=False, kind="int4_gemm3", norm=(norm_weight, eps, unit_offset),
+                       warm=_norm_warm([w0, w1, w2], x))
         return a, b, c
 
     @_rms_norm_int4_gemm3.register_fake
@@ -1203,7 +1242,8 @@ def rms_norm_int4_gemm3(x, norm_weight, eps, w0, w1, w2, unit_offset=True):
     quant (K = 2048)."""
     if _direct(x, norm_weight, w0, w1, w2):
         return tuple(_run(x, [w0, w1, w2], tiled=False, kind="int4_gemm3",
-                          norm=(norm_weight, float(eps), bool(unit_offset))))
+                          norm=(norm_weight, float(eps), bool(unit_offset)),
+                          warm=_norm_warm([w0, w1, w2], x)))
     return torch.ops.pi05_w4a4.rms_norm_int4_gemm3(x, norm_weight, float(eps), bool(unit_offset), w0, w1, w2)
 
 

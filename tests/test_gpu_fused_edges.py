@@ -3,7 +3,8 @@ against the oracle:
 
 - ``pi05w4a4_rmsnorm_quantize``: codes, scales and row corrections equal the oracle's
   ``quant_activation`` of ``rms_norm_lanes(x)`` (GemmaRMSNorm restated in the kernel's fp32
-  summation order; the fp16 norm output is what gets quantized);
+  summation order; the fp16 norm output is what gets quantized), also in its cache-warming
+  form ``pi05w4a4_rmsnorm_quantize_warm``;
 - ``pi05w4a4_gemm_residual``: y equals fp16(int4_gemm_ref(x, W) + residual), the rounding
   of the decoder's eager fp16 residual add, also through the split-K path (small M).
 """
@@ -52,6 +53,58 @@ def test_rmsnorm_quantize_matches_oracle(ext, cuda, m, scale, offset):
 
     qc = inp.to_np(qcorr_from_fragment_major(q.cpu(), m, k))
     assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
+
+
+@pytest.mark.parametrize("m", [1, 5, 776, 1100])
+def test_rmsnorm_quantize_cache_warm_changes_nothing(ext, cuda, m):
+    """The norm + quant with cache warming (a workgroup for each CU the row workgroups leave
+    idle reads further buffers, here 12 MB; at M = 1100 the rows cover every CU and nothing
+    is read) writes the oracle's codes, scales and row corrections, the same as the plain
+    call, and leaves the buffers it read unchanged."""
+    k = 2048
+    gen = inp.generator(900 + m)
+    x = inp.activations(gen, m, k)
+    w = (torch.randn(k, generator=gen) * 0.1).half()
+    big = [torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=cuda) for n in (1 << 20,) * 3]
+    keep = [t.clone() for t in big]
+    xd, wd = x.to(cuda), w.to(cuda)
+    q0, s0 = ext.rms_norm_quantize(xd, wd, 1e-6)
+    q1, s1 = ext.rms_norm_quantize(xd, wd, 1e-6, warm=big)
+    torch.cuda.synchronize()
+    c1 = _codes(q1, m, k)
+    assert np.array_equal(_codes(q0, m, k), c1) and torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+    q_ref, s_ref = orc.quant_activation(orc.rms_norm_lanes(x.numpy(), w.numpy(), 1e-6))
+    assert np.array_equal(c1, q_ref)
+    assert np.array_equal(inp.to_np(s1).view(np.int32), s_ref.view(np.int32))
+    from pi05_fast.w4a4.pack import qcorr_from_fragment_major
+
+    qc = inp.to_np(qcorr_from_fragment_major(q1.cpu(), m, k))
+    assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
+    for t, t0 in zip(big, keep):
+        assert torch.equal(t, t0)
+
+
+@pytest.mark.parametrize("m", [1, 776])
+def test_rms_norm_qkv_warms_its_weights_same_outputs(ext, cuda, monkeypatch, m):
+    """rms_norm_int4_gemm3 (whose norm + quant launch warms the QKV weights from 256 rows
+    on: at M = 776, not at M = 1) gives the same q, k, v with warming on and off
+    (PI05_W4A4_CACHE_WARM=0), equal to the oracle's GEMMs of the oracle's codes."""
+    k = 2048
+    gen = inp.generator(950 + m)
+    x = inp.activations(gen, m, k)
+    nw = (torch.randn(k, generator=gen) * 0.1).half()
+    packed = [inp.packed_weight(gen, n, k) for n in (2048, 256, 256)]
+    ws = [ext.repack_weight(p.to(cuda), k=k) for p in packed]
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("PI05_W4A4_CACHE_WARM", flag)
+        outs.append(ext.rms_norm_int4_gemm3(x.to(cuda), nw.to(cuda), 1e-6, *ws))
+    torch.cuda.synchronize()
+    h = orc.rms_norm_lanes(x.numpy(), nw.numpy(), 1e-6)
+    for a, b, p in zip(outs[0], outs[1], packed):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+        want = orc.int4_gemm_ref(h, p.numpy())
+        assert np.array_equal(inp.to_np(a).view(np.int16), want.view(np.int16))
 
 
 def test_rmsnorm_quantize_equals_norm_then_quantize(ext, cuda):
