@@ -407,6 +407,8 @@ int pi05w4a4_prefix_attention_warm(const void* q, int64_t ld_q, const void* kv_m
  *   w6, not in place (load time).
  * pi05w4a4_quantize_e3m2 / pi05w4a4_rmsnorm_quantize_e3m2: pi05w4a4_quantize /
  *   pi05w4a4_rmsnorm_quantize with the codes written as q6 (the same codes and scales).
+ * pi05w4a4_rmsnorm_quantize_e3m2_warm: pi05w4a4_rmsnorm_quantize_e3m2 with the cache
+ *   warming of pi05w4a4_rmsnorm_quantize_warm (the gate/up op passes part of its up weight).
  * pi05w4a4_gemm_e3m2: gelu_up = 0: pi05w4a4_gemm_multi of 1..3 w6 weights (n[g] columns
  *   into y[g]); gelu_up = 1: pi05w4a4_gemm_gelu_up (ngroups = 2: gate, up with
  *   n[0] == n[1]; y[0] = fp16(gelu_tanh(gate) * up)).  One launch, no workspace.
@@ -417,6 +419,9 @@ int pi05w4a4_repack_weight_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int
 int pi05w4a4_quantize_e3m2(const void* x_fp16, int64_t m, int32_t k, void* q6, float* sa, void* stream);
 int pi05w4a4_rmsnorm_quantize_e3m2(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
                                    int64_t m, int32_t k, void* q6, float* sa, void* stream);
+int pi05w4a4_rmsnorm_quantize_e3m2_warm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                        int64_t m, int32_t k, void* q6, float* sa, const void* const* warm_ptrs,
+                                        const size_t* warm_bytes, int32_t warm_n, void* stream);
 int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, int32_t ngroups,
                        const int32_t* const* w6, const int32_t* n, void* const* y_fp16, int32_t gelu_up,
                        void* stream);

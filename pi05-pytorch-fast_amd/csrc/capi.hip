@@ -530,7 +530,8 @@ static int validate_e3m2_shape(int32_t n, int32_t k, const char* name) {
 }
 
 static int quantize_e3m2_call(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset, int64_t m,
-                              int32_t k, void* q6, float* sa, void* stream) {
+                              int32_t k, void* q6, float* sa, void* stream,
+                              const w4a4::CacheWarmParams* warm = nullptr) {
   if (m < 0) return fail(PI05W4A4_EINVAL, "M must be >= 0, got %lld", (long long)m);
   if (k != 2048) return fail(PI05W4A4_EINVAL, "the E3M2 quantizer takes K = 2048, got %d", k);
   if (m == 0) return ok();
@@ -540,7 +541,7 @@ static int quantize_e3m2_call(const void* x_fp16, const void* w_fp16, float eps,
   if (m > 0x7fffffffLL) return fail(PI05W4A4_EINVAL, "M too large");
   return hip_status(w4a4::launch_quantize_e3m2(x_fp16, w_fp16, eps, unit_offset != 0, m, k, q6, sa,
                                                static_cast<float>(1.0 / std::sqrt(2048.0)),
-                                               static_cast<hipStream_t>(stream)),
+                                               static_cast<hipStream_t>(stream), warm),
                     "E3M2 quantize launch");
 }
 }  // namespace
@@ -563,6 +564,16 @@ int pi05w4a4_rmsnorm_quantize_e3m2(const void* x_fp16, const void* w_fp16, float
                                    int64_t m, int32_t k, void* q6, float* sa, void* stream) {
   if (m > 0 && w_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
   return quantize_e3m2_call(x_fp16, w_fp16, eps, unit_offset, m, k, q6, sa, stream);
+}
+
+int pi05w4a4_rmsnorm_quantize_e3m2_warm(const void* x_fp16, const void* w_fp16, float eps, int32_t unit_offset,
+                                        int64_t m, int32_t k, void* q6, float* sa, const void* const* warm_ptrs,
+                                        const size_t* warm_bytes, int32_t warm_n, void* stream) {
+  if (m > 0 && w_fp16 == nullptr) return fail(PI05W4A4_EINVAL, "null pointer argument");
+  w4a4::CacheWarmParams warm;
+  const int rc = collect_warm(warm_ptrs, warm_bytes, warm_n, &warm);
+  if (rc) return rc;
+  return quantize_e3m2_call(x_fp16, w_fp16, eps, unit_offset, m, k, q6, sa, stream, &warm);
 }
 
 int pi05w4a4_gemm_e3m2(const void* q6, const float* sa, int64_t m, int32_t k, int32_t ngroups,

@@ -335,17 +335,24 @@ hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int 
 }
 
 hipError_t launch_quantize_e3m2(const void* x, const void* nw, float eps, int unit_offset, int64_t m,
-                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream) {
+                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream,
+                                const CacheWarmParams* warm) {
   if (m <= 0) return hipSuccess;
   if (k != 2048) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((m + 3) / 4));
+  // Cache warming as in launch_rmsnorm_quantize: one workgroup per CU the rows leave idle.
+  const int64_t row_blocks = (m + 3) / 4;
+  const int64_t cus = device_cu_count();
+  const int64_t extra = (warm != nullptr && warm->nbuf > 0 && row_blocks < cus) ? cus - row_blocks : 0;
+  const CacheWarmParams wp = extra > 0 ? *warm : CacheWarmParams{};
+  const dim3 grid(static_cast<unsigned>(row_blocks + extra));
   const _Float16* xh = static_cast<const _Float16*>(x);
   int32_t* q = static_cast<int32_t*>(q6);
   if (nw != nullptr)
     fwht_quant_kernel<11, 6, 4, true, true><<<grid, 256, 0, stream>>>(
-        xh, m, q, sa, nullptr, inv_sqrt_k, static_cast<const _Float16*>(nw), eps, unit_offset);
+        xh, m, q, sa, nullptr, inv_sqrt_k, static_cast<const _Float16*>(nw), eps, unit_offset, wp);
   else
-    fwht_quant_kernel<11, 6, 4, false, true><<<grid, 256, 0, stream>>>(xh, m, q, sa, nullptr, inv_sqrt_k);
+    fwht_quant_kernel<11, 6, 4, false, true><<<grid, 256, 0, stream>>>(xh, m, q, sa, nullptr, inv_sqrt_k, nullptr,
+                                                                       0.0f, 0, wp);
   return hipGetLastError();
 }
 

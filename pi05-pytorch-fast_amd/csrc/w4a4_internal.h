@@ -226,7 +226,8 @@ hipError_t launch_repack_e3m2(const int32_t* w_mfma, int32_t n, int32_t k, int32
 // K = 2048 activation quant (optionally with the fused RMSNorm, nw != null) writing E3M2
 // fragments (q6) instead of INT4 codes.
 hipError_t launch_quantize_e3m2(const void* x, const void* nw, float eps, int unit_offset, int64_t m,
-                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream);
+                                int32_t k, void* q6, float* sa, float inv_sqrt_k, hipStream_t stream,
+                                const CacheWarmParams* warm = nullptr);
 // GEMM on E3M2 operands, tile_cfg kCfg7x4 (112 x 256 workgroup tiles, GELU pairs or
 // plain) or kCfg2x2 (32 x 128), four waves along N, no K split; modes kEpiFp16 (1..3
 // groups, optional residual or QKV attention prep) and kEpiGeluUp; p.q points at q6, the

@@ -383,7 +383,10 @@ def _fused_decoder_layer_forward(
     # idle workgroup slots the down-proj weights.  The next layer's QKV weights were tried
     # as well: no gain, and the longer warming outlasts the attention.
     warming = os.environ.get("PI05_W4A4_CACHE_WARM", "1") != "0"
-    warm = [attn.o_proj.packed, mlp.gate_proj.packed, mlp.up_proj.packed] if warming else None
+    # (the tail of the up weight is warmed by the gate/up op's own norm + quant launch)
+    warm = None
+    if warming:
+        warm = [attn.o_proj.packed, mlp.gate_proj.packed, ext.gate_up_warm_split(mlp.up_proj.packed)[0]]
     wk_rope = _k_rope_weight(attn, x)
     if wk_rope is not None:
         # One KV head: RoPE and the attention's K/V layout in the QKV GEMM epilogue.

@@ -137,6 +137,9 @@ def load_int4_gemm():
         "pi05w4a4_repack_weight_e3m2": (ctypes.c_int, [vp, i32, i32, vp, vp]),
         "pi05w4a4_quantize_e3m2": (ctypes.c_int, [vp, i64, i32, vp, vp, vp]),
         "pi05w4a4_rmsnorm_quantize_e3m2": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
+        "pi05w4a4_rmsnorm_quantize_e3m2_warm": (
+            ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(sz), i32,
+                           vp]),
         "pi05w4a4_gemm_e3m2": (ctypes.c_int, [vp, vp, i64, i32, i32, vp, vp, vp, i32, vp]),
     }
     for name, (res, args) in sig.items():
@@ -386,10 +389,12 @@ def repack_weight_e3m2(w: torch.Tensor, k: int | None = None, tiled: bool | None
     return out
 
 
-def quantize_e3m2(x: torch.Tensor, norm=None) -> tuple[torch.Tensor, torch.Tensor]:
+def quantize_e3m2(x: torch.Tensor, norm=None, warm: list[torch.Tensor] | None = None
+                  ) -> tuple[torch.Tensor, torch.Tensor]:
     """``quantize`` (or, with ``norm`` = (weight, eps, unit_offset), ``rms_norm_quantize``)
     with the codes written as E3M2 fragments (uint8 [pi05w4a4_q_e3m2_bytes(M, K)]): the
-    activation form of the FP6-MFMA GEMM.  K = 2048."""
+    activation form of the FP6-MFMA GEMM.  K = 2048.  ``warm`` (with ``norm``): buffers the
+    launch's idle CUs read into the Infinity Cache, as in ``rms_norm_quantize``."""
     k = _check_x(x)
     if k != 2048:
         raise RuntimeError(f"the E3M2 quantizer takes K = 2048, got {k}")
@@ -410,9 +415,17 @@ def quantize_e3m2(x: torch.Tensor, norm=None) -> tuple[torch.Tensor, torch.Tenso
             if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 1 or weight.numel() != k:
                 raise RuntimeError(f"RMSNorm weight must be a float16 CUDA/HIP tensor [{k}]")
             wn = weight if weight.is_contiguous() else weight.contiguous()
-            _check(lib.pi05w4a4_rmsnorm_quantize_e3m2(x2.data_ptr(), wn.data_ptr(), float(eps),
-                                                      1 if unit_offset else 0, m, k, q6.data_ptr(), sa.data_ptr(),
-                                                      _stream(dev)), "pi05w4a4_rmsnorm_quantize_e3m2")
+            wa = _warm_args(warm, "quantize_e3m2") if warm else None
+            if wa is None:
+                _check(lib.pi05w4a4_rmsnorm_quantize_e3m2(x2.data_ptr(), wn.data_ptr(), float(eps),
+                                                          1 if unit_offset else 0, m, k, q6.data_ptr(),
+                                                          sa.data_ptr(), _stream(dev)),
+                       "pi05w4a4_rmsnorm_quantize_e3m2")
+            else:
+                _check(lib.pi05w4a4_rmsnorm_quantize_e3m2_warm(x2.data_ptr(), wn.data_ptr(), float(eps),
+                                                               1 if unit_offset else 0, m, k, q6.data_ptr(),
+                                                               sa.data_ptr(), *wa, _stream(dev)),
+                       "pi05w4a4_rmsnorm_quantize_e3m2_warm")
     return q6, sa
 
 
@@ -595,6 +608,34 @@ _NORM_WARM_MAX_BYTES = 16 << 20
 _NORM_WARM_MIN_ROWS = 256
 
 
+# The tail of the up weight that the gate/up op's own norm + quant launch warms (from
+# _NORM_WARM_MIN_ROWS rows on); the fused decoder layer's attention launch warms the rest
+# (gate_up_warm_split).  At 776 tokens, E3M2 weights (forward A/B in one process, three
+# rounds): 3-6 MB 15-25 us faster than none, 8 MB less, 12 MB and all 26 MB slower.
+_GATE_UP_SELF_WARM_BYTES = 4 << 20
+
+
+def gate_up_warm_split(w_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
+    """(head, tail) byte ranges of the up weight as flat views: the gate/up op's norm +
+    quant launch warms the tail (at most _GATE_UP_SELF_WARM_BYTES, a multiple of 16 bytes),
+    the caller may warm the head earlier."""
+    flat = w_up.reshape(-1)
+    per16 = max(1, 16 // flat.element_size())
+    tail = min(flat.numel(), _GATE_UP_SELF_WARM_BYTES // flat.element_size()) // per16 * per16
+    if tail <= 0:
+        return flat, None
+    return flat[: flat.numel() - tail], flat[flat.numel() - tail:]
+
+
+def _gate_up_warm(w_up: torch.Tensor, x: torch.Tensor) -> list[torch.Tensor] | None:
+    """The up weight's tail for the gate/up op's norm + quant launch to warm."""
+    if os.environ.get("PI05_W4A4_CACHE_WARM", "1") == "0" or not (w_up.is_cuda and w_up.is_contiguous()):
+        return None
+    if x.numel() // int(x.size(-1)) < _NORM_WARM_MIN_ROWS:
+        return None
+    return [t for t in gate_up_warm_split(w_up)[1:] if t is not None and t.numel() > 0] or None
+
+
 def _norm_warm(ws: list[torch.Tensor], x: torch.Tensor) -> list[torch.Tensor] | None:
     """The weights for the norm + quant launch of x to warm (PI05_W4A4_CACHE_WARM=0: none):
     MFMA-layout weights only (what the GEMM reads), at most _NORM_WARM_MAX_BYTES in total,
@@ -685,7 +726,7 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
     k = _check_x(x)
     n_e3m2 = sum(1 for w in ws if is_e3m2_layout(w, k))
     if n_e3m2:
-        return _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual)
+        return _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual, warm=warm)
     if residual is not None:  # before any launch: the kernel reads it through a raw pointer
         _check_residual(residual, x.device, (*x.shape[:-1], int(ws[0].size(0))))
     # the reference quantizes before checking the weights
@@ -701,7 +742,7 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
         return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), dev, kind, gelu=gelu, residual=residual)
 
 
-def _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual):
+def _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual, warm=None):
     """_run for E3M2-layout weights: E3M2 activation quant, then the FP6-MFMA GEMM."""
     if n_e3m2 != len(ws):
         raise RuntimeError(f"{kind}: the weights of one call must all be E3M2-layout ([N, 3K/16+16]) or none")
@@ -709,7 +750,7 @@ def _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual):
         raise RuntimeError(f"{kind}: the residual epilogue takes INT4-layout weights, not E3M2")
     for w in ws:
         _check_packed(w, k)
-    q6, sa = quantize_e3m2(x, norm)
+    q6, sa = quantize_e3m2(x, norm, warm=warm if norm is not None else None)
     dev = x.device
     with _on_device(dev):
         return _gemm_e3m2_from_q(q6, sa, k, ws, tuple(x.shape[:-1]), dev, gelu=gelu)
@@ -1047,7 +1088,7 @@ def _register_custom_op() -> None:
     ) -> torch.Tensor:
         _check_gelu_weights(x, w_gate, w_up)
         return _run(x, [w_gate, w_up], tiled=False, kind="int4_gemm2_gelu", gelu=True,
-                    norm=(norm_weight, eps, unit_offset))[0]
+                    norm=(norm_weight, eps, unit_offset), warm=_gate_up_warm(w_up, x))[0]
 
     @_rms_norm_int4_gemm2_gelu.register_fake
     def _rms_norm_int4_gemm2_gelu_fake(x, norm_weight, eps, unit_offset, w_gate, w_up):
@@ -1253,7 +1294,7 @@ def rms_norm_int4_gemm2_gelu(x, norm_weight, eps, w_gate, w_up, unit_offset=True
     if _direct(x, norm_weight, w_gate, w_up):
         _check_gelu_weights(x, w_gate, w_up)
         return _run(x, [w_gate, w_up], tiled=False, kind="int4_gemm2_gelu", gelu=True,
-                    norm=(norm_weight, float(eps), bool(unit_offset)))[0]
+                    norm=(norm_weight, float(eps), bool(unit_offset)), warm=_gate_up_warm(w_up, x))[0]
     return torch.ops.pi05_w4a4.rms_norm_int4_gemm2_gelu(x, norm_weight, float(eps), bool(unit_offset),
                                                         w_gate, w_up)
 

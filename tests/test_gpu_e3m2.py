@@ -95,6 +95,44 @@ def test_rms_norm_quantize_e3m2_matches_int4(ext, cuda, m):
     assert torch.equal(sa.view(torch.int32), sa6.view(torch.int32))
 
 
+@pytest.mark.parametrize("m", [3, 776])
+def test_rms_norm_quantize_e3m2_cache_warm_changes_nothing(ext, cuda, m):
+    """The E3M2 norm + quant with cache warming (a workgroup for each CU the rows leave idle
+    reads further buffers) writes the same codes and scales as without, and leaves the
+    buffers unchanged."""
+    k = 2048
+    gen = inp.generator(650 + m)
+    x = inp.activations(gen, m, k).to(cuda)
+    w = (torch.randn(k, generator=gen) * 0.1).to(torch.float16).to(cuda)
+    big = [torch.randint(-2**31, 2**31 - 1, (n,), dtype=torch.int32, device=cuda) for n in (1 << 20,) * 2]
+    keep = [t.clone() for t in big]
+    q0, s0 = ext.quantize_e3m2(x, (w, 1e-6, True))
+    q1, s1 = ext.quantize_e3m2(x, (w, 1e-6, True), warm=big)
+    torch.cuda.synchronize()
+    assert np.array_equal(_e3m2_codes(q1, m, k), _e3m2_codes(q0, m, k))
+    assert torch.equal(s0.view(torch.int32), s1.view(torch.int32))
+    for t, t0 in zip(big, keep):
+        assert torch.equal(t, t0)
+
+
+def test_gate_up_op_warming_changes_nothing(ext, cuda, monkeypatch):
+    """rms_norm_int4_gemm2_gelu on E3M2 weights at 776 rows, whose norm + quant launch warms
+    the up weight's tail, equals the call without warming (PI05_W4A4_CACHE_WARM=0)."""
+    m, k, n = 776, 2048, 16384
+    gen = inp.generator(660)
+    x = inp.activations(gen, m, k).to(cuda)
+    nw = (torch.randn(k, generator=gen) * 0.1).to(torch.float16).to(cuda)
+    g6, u6 = (ext.repack_weight_e3m2(inp.random_packed(gen, n, k).to(cuda), k=k) for _ in range(2))
+    head, tail = ext.gate_up_warm_split(u6)
+    assert tail is not None and head.numel() + tail.numel() == u6.numel()
+    outs = []
+    for flag in ("1", "0"):
+        monkeypatch.setenv("PI05_W4A4_CACHE_WARM", flag)
+        outs.append(ext.rms_norm_int4_gemm2_gelu(x, nw, 1e-6, g6, u6))
+    torch.cuda.synchronize()
+    assert _same_f16(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("n,k", [(64, 2048), (16384, 2048), (96, 4096)])
 def test_repack_e3m2_keeps_codes_and_scales(ext, cuda, n, k):
     from pi05_fast.w4a4.pack import codes_from_e3m2_weight
