@@ -272,11 +272,12 @@ class KernelBench:
         return rec
 
 
-    def qkv_block(self, m, warm, copies=200, ns=(2048, 256, 256), k=2048):
+    def qkv_block(self, m, warm, copies=200, ns=(2048, 256, 256), k=2048, fused=False):
         """The QKV block of a decoder layer as launched: RMSNorm + quant, then the QKV GEMM,
         the timed graph cycling `copies` weight sets (from HBM, as in `gemm(copies=...)`).
         `warm`: the norm + quant launch reads the set its GEMM is about to use into the
-        Infinity Cache (pi05w4a4_rmsnorm_quantize_warm)."""
+        Infinity Cache (pi05w4a4_rmsnorm_quantize_warm).  `fused` (M <= 4): the one launch of
+        pi05w4a4_quant_gemm_small instead, which quantizes inside the GEMM launch."""
         torch, lib, P = self.torch, self.lib, self.ext._ptr
         gen = torch.Generator(device=self.dev).manual_seed(20261202 + m)
         x = torch.randn(m, k, device=self.dev, dtype=torch.float16, generator=gen)
@@ -296,6 +297,10 @@ class KernelBench:
 
         def fn():
             i = next(turn)
+            if fused:
+                self._check(lib.pi05w4a4_quant_gemm_small(P(x), P(nw), 1e-6, 1, m, k, g, w_arrs[i], n_arr, y_arr,
+                                                          None, self._stream()))
+                return
             if warm:
                 self._check(lib.pi05w4a4_rmsnorm_quantize_warm(P(x), P(nw), 1e-6, 1, m, k, P(q), P(sa), w_arrs[i],
                                                                warm_bytes, g, self._stream()))
@@ -687,7 +692,7 @@ def kernel_table(kb: KernelBench, m: int, only: str = "") -> dict:
     return {name: fn() for name, fn in jobs.items()}
 
 
-def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
+def qkv_m_sweep(kb: KernelBench, ms=(1, 4, 64, 640, 776)) -> dict:
     """The fused QKV projection (int4_gemm3: one activation quant, N = 2048 + 256 + 256,
     K = 2048) and its RMSNorm + quant over a range of token counts, down to the
     weight-streaming regime of M = 1 and 64.  `hot`: the same weights every launch (they
@@ -713,6 +718,9 @@ def qkv_m_sweep(kb: KernelBench, ms=(1, 64, 640, 776)) -> dict:
             "block_cold_pair_us": kb.qkv_block(m, warm=False),
             "block_cold_warm_us": kb.qkv_block(m, warm=True),
         }
+        if m <= 4:
+            # the one-launch form the ops take at these sizes (norm + quant inside the GEMM)
+            out[str(m)]["block_cold_fused_us"] = kb.qkv_block(m, warm=False, fused=True)
     return out
 
 

@@ -210,6 +210,22 @@ int pi05w4a4_gemm_residual(const int32_t* q, const float* sa, int64_t m, int32_t
                            void* y_fp16, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Small-M quant + GEMM in one launch (1 <= M <= 4, K = 2048): the y[g] of
+ * pi05w4a4_gemm_multi (or, with a residual and one weight, of pi05w4a4_gemm_residual)
+ * applied to the codes and scales of pi05w4a4_quantize(x), or of
+ * pi05w4a4_rmsnorm_quantize(x, nw, eps, unit_offset) when nw is not null, bit for bit.
+ * Every workgroup (16 x 32 tiles whose four waves split K) quantizes the rows itself into
+ * LDS while its first weight fragments load, so no activation codes are stored and the
+ * separate quant launch of decode-sized calls is gone.  Replaces the reference's quantize_x
+ * followed by gemm_from_q (int4_gemm.cu:496-531, 566-616) at those sizes, with the norm of
+ * the following entry point when nw is given.  x, nw, the weights, y and the residual are
+ * 16-byte aligned; the weights are MFMA-layout with N % 16 == 0.
+ */
+int pi05w4a4_quant_gemm_small(const void* x_fp16, const void* nw_fp16, float eps, int32_t unit_offset, int64_t m,
+                              int32_t k, int32_t ngroups, const int32_t* const* w_mfma, const int32_t* n,
+                              void* const* y_fp16, const void* residual_fp16, void* stream);
+
+/*
  * RMSNorm fused into the K = 2048 activation quant: the codes and scales of
  * pi05w4a4_quantize applied to h = fp16((x * r) * (unit_offset + w)),
  * r = 1 / sqrt(sum(x^2) / K + eps), the input norm of every attention and MLP block of

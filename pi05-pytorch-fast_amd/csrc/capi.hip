@@ -397,6 +397,54 @@ int pi05w4a4_gemm_multi(const int32_t* q, const float* sa, int64_t m, int32_t k,
                   workspace_bytes, static_cast<hipStream_t>(stream));
 }
 
+int pi05w4a4_quant_gemm_small(const void* x_fp16, const void* nw_fp16, float eps, int32_t unit_offset, int64_t m,
+                              int32_t k, int32_t ngroups, const int32_t* const* w_mfma, const int32_t* n,
+                              void* const* y_fp16, const void* residual_fp16, void* stream) {
+  if (m < 1 || m > w4a4::kQproMaxRows)
+    return fail(PI05W4A4_EINVAL, "the small-M quant + GEMM takes 1..%d rows, got %lld", w4a4::kQproMaxRows,
+                (long long)m);
+  if (k != 2048) return fail(PI05W4A4_EINVAL, "the small-M quant + GEMM takes K = 2048, got %d", k);
+  if (x_fp16 == nullptr || !aligned(x_fp16, 16)) return fail(PI05W4A4_EINVAL, "x must be non-null and 16-byte aligned");
+  if (nw_fp16 != nullptr && !aligned(nw_fp16, 16)) return fail(PI05W4A4_EINVAL, "the norm weight must be 16-byte aligned");
+  if (ngroups < 1 || ngroups > w4a4::kMaxGroups || w_mfma == nullptr || n == nullptr || y_fp16 == nullptr)
+    return fail(PI05W4A4_EINVAL, "ngroups must be 1..3 with non-null arrays");
+  if (residual_fp16 != nullptr && (ngroups != 1 || !aligned(residual_fp16, 16)))
+    return fail(PI05W4A4_EINVAL, "a residual takes one weight and 16-byte alignment");
+  w4a4::GemmParams p{};
+  int tile_begin = 0;
+  int64_t n_total = 0;
+  for (int g = 0; g < ngroups; ++g) {
+    const int rc = validate_weight(w_mfma[g], n[g], "weight");
+    if (rc) return rc;
+    if (y_fp16[g] == nullptr || !aligned(y_fp16[g], 16)) return fail(PI05W4A4_EINVAL, "outputs must be non-null and 16-byte aligned");
+    p.g[g].w = w_mfma[g];
+    p.g[g].y = y_fp16[g];
+    p.g[g].n = n[g];
+    p.g[g].tile_begin = tile_begin;
+    tile_begin += static_cast<int>(cdiv(n[g], kCfg1x2K4.cols(false)));
+    n_total += n[g];
+  }
+  p.q = static_cast<const int32_t*>(x_fp16);  // not read: the prologue's codes stay in LDS
+  p.sa = nullptr;
+  p.m = m;
+  p.k = k;
+  p.ngroups = ngroups;
+  p.ntiles = tile_begin;
+  p.mtiles = 1;
+  p.ksplit = 1;
+  p.kblocks_per_split = w4a4::kblocks128(k);
+  p.mblocks = 1;
+  p.n_total = static_cast<int32_t>(n_total);
+  p.mode = w4a4::kEpiFp16;
+  p.res = static_cast<const _Float16*>(residual_fp16);
+  p.xpro = static_cast<const _Float16*>(x_fp16);
+  p.nwpro = static_cast<const _Float16*>(nw_fp16);
+  p.eps_pro = eps;
+  p.unit_offset_pro = unit_offset != 0;
+  p.inv_sqrt_k_pro = static_cast<float>(1.0 / std::sqrt(static_cast<double>(k)));
+  return hip_status(w4a4::launch_gemm_qpro(p, static_cast<hipStream_t>(stream)), "small-M quant + gemm launch");
+}
+
 int pi05w4a4_gemm_residual(const int32_t* q, const float* sa, int64_t m, int32_t k,
                            const int32_t* w_mfma, int32_t n, const void* residual_fp16,
                            void* y_fp16, void* workspace, size_t workspace_bytes, void* stream) {

@@ -282,9 +282,11 @@ __device__ __forceinline__ void down_quant_role(const GemmParams& p, char* lds) 
 // compiler's conservative wait on those loads never lands before a read.  The fp32
 // accumulators start at zero and end at acc exactly (no 16x factor, no corrections).
 template <int MI, int NI, int NWAVES, int KW, bool GELU, int RING, int WPE, bool QKV_PREP = false, bool QFUSE = false,
-          bool E3M2 = false>
+          bool E3M2 = false, bool QPRO = false>
 __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_w4a4_kernel(const GemmParams p) {
   static_assert(!(GELU && QKV_PREP), "the attention prep is a fp16 epilogue");
+  static_assert(!QPRO || (MI == 1 && NWAVES == 4 && KW == 4 && RING >= 3 && !GELU && !QFUSE && !E3M2),
+                "the quant prologue runs in the four K-split waves of one 16-row block");
   static_assert(!E3M2 || (NI % 2 == 0 && NWAVES == 4 && KW == 1 && !QFUSE && (!GELU || NI == 4)),
                 "E3M2 operands: four waves along N, whole column pairs per wave");
   static_assert(!GELU || (NI % 2 == 0), "GELU pairing needs an even NI");
@@ -320,7 +322,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // concatenated 512-byte d4-5 parts (the last one half used when MI is odd).
   constexpr int kA6Chunks = MI + (MI + 1) / 2;
   constexpr int kA6Stage = kA6Chunks * 1024;
-  constexpr int kLdsGemm = kLdsA6 + (E3M2 ? 2 * kA6Stage : 0);
+  // QPRO: the block's 16 rows of codes (K = 2048: 16 fragments of 1 KB), then 16 row scales
+  // and 16 row corrections.
+  constexpr int kLdsPro = kLdsA6 + (E3M2 ? 2 * kA6Stage : 0);
+  constexpr int kLdsGemm = kLdsPro + (QPRO ? 16 * 1024 + 2 * 16 * 4 : 0);
   constexpr int kLdsPool = (QFUSE && kQuantLdsBytes > kLdsGemm) ? kQuantLdsBytes : kLdsGemm;
   __shared__ __align__(16) char lds_pool[kLdsPool];
   int8_t* const fix_lds = reinterpret_cast<int8_t*>(lds_pool + kLdsFix);
@@ -341,6 +346,22 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // Wave-uniform values are kept in scalar registers: fragment base addresses are scalar
   // and every load of a k block shares one 32-bit lane offset.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+  // QPRO: the M <= 4 rows are quantized here, by every workgroup for itself: wave w takes row
+  // min(w, M - 1) (32 consecutive elements per lane).  Its loads (and the norm weights') are
+  // issued first, so that the weight prefetches below queue behind them and their wait
+  // covers these loads only.  Without a norm the weight loads read the row again.
+  half8 pro_x[QPRO ? 4 : 1], pro_w[QPRO ? 4 : 1];
+  if constexpr (QPRO) {
+    const int64_t prow = min(static_cast<int64_t>(wave), p.m - 1);
+    const _Float16* xr = p.xpro + prow * 2048 + lane * 32;
+    const _Float16* wr = (p.nwpro != nullptr ? p.nwpro : xr - lane * 32) + lane * 32;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      pro_x[c] = *reinterpret_cast<const half8*>(xr + 8 * c);
+      pro_w[c] = *reinterpret_cast<const half8*>(wr + 8 * c);
+    }
+  }
   const int wn = wave % NW;  // column block of the wave
   const int wk = wave / NW;  // k part of the wave
 
@@ -493,10 +514,18 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   uint4 rb[RING][NI];
   auto load = [&](int kb, uint4 (&a)[MI], uint4 (&b)[NI]) {
     const uint32_t off = static_cast<uint32_t>(min(kb, kb_end - 1)) * 1024u + static_cast<uint32_t>(lane) * 16u;
+    if constexpr (!QPRO) {
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) a[mi] = *reinterpret_cast<const uint4*>(abase[mi] + off);
+      for (int mi = 0; mi < MI; ++mi) a[mi] = *reinterpret_cast<const uint4*>(abase[mi] + off);
+    }
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) b[ni] = *reinterpret_cast<const uint4*>(bbase[ni] + off);
+  };
+  // QPRO: the activation fragment of block kb from the workgroup's LDS codes.
+  const char* const pro_q = lds_pool + kLdsPro;
+  auto load_a_lds = [&](int kb, uint4 (&a)[MI]) {
+    const int kc = max(min(kb, kb_end - 1), 0);
+    a[0] = *reinterpret_cast<const uint4*>(pro_q + static_cast<uint32_t>(kc) * 1024u + static_cast<uint32_t>(lane) * 16u);
   };
   // The two MFMAs of a 128-deep block (codes 0-15 and 16-31 of each lane's 32).  The
   // weights are operand A of the MFMA and the activations operand B, so accumulator
@@ -533,6 +562,25 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // The first ring load is unconditional: with nkb == 0 it reads the clamped block
   // kb_end - 1 >= 0 and is never used.
   if constexpr (!E3M2) load(kb_begin, ra[0], rb[0]);
+  if constexpr (QPRO) {
+    // The rest of the weight prefetch goes out before the prologue's arithmetic.
+#pragma unroll
+    for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(pro_x[c][e]);
+    if (p.nwpro != nullptr) rms_norm_row_wave<2048>(v, pro_w, p.eps_pro, p.unit_offset_pro);
+    // Codes, scale and correction of row `wave` of the block (rows past M hold a copy of row
+    // M - 1; rows 4-15 are never written: their outputs are never stored).
+    int32_t* const lq = reinterpret_cast<int32_t*>(lds_pool + kLdsPro);
+    float* const lsa = reinterpret_cast<float*>(lds_pool + kLdsPro + 16 * 1024);
+    int32_t* const lqc = reinterpret_cast<int32_t*>(lds_pool + kLdsPro + 16 * 1024 + 16 * 4);
+    fwht_quant_row_wave<11>(v, lane, wave, lq, lsa, lqc, p.inv_sqrt_k_pro);
+    __syncthreads();
+    load_a_lds(kb_begin, ra[0]);
+  }
 
   // Accumulators start at the correction terms, qcorr[row] + wcorr[col], so that they end
   // at 16 * acc exactly (S + qcorr + wcorr).  Only the first k part of the first K slice
@@ -546,10 +594,14 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = AccV{0, 0, 0, 0};
   } else {
     const bool first_part = (ks == 0) && (wk == 0);
-    const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
     int32_t qc[MI];
+    if constexpr (QPRO) {
+      qc[0] = reinterpret_cast<const int32_t*>(lds_pool + kLdsPro + 16 * 1024 + 16 * 4)[lane & 15];
+    } else {
+      const int32_t* qcorr = p.q + q_payload_words(p.mblocks, KB128);
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) qc[mi] = qcorr[min(mt * MI + mi, p.mblocks - 1) * 16 + (lane & 15)];
+      for (int mi = 0; mi < MI; ++mi) qc[mi] = qcorr[min(mt * MI + mi, p.mblocks - 1) * 16 + (lane & 15)];
+    }
     v4i wc[NI];
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
@@ -605,7 +657,10 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // The accumulator readout (kEpiAcc) has no row scales (p.sa may be null): it reads
     // the first M words of q instead, which always exist, and never uses the values.
     const float* sa_src = (p.sa != nullptr) ? p.sa : reinterpret_cast<const float*>(p.q);
-    e_sa = sa_src[min(m0 + r, M - 1)];
+    if constexpr (QPRO)
+      e_sa = reinterpret_cast<const float*>(lds_pool + kLdsPro + 16 * 1024)[r & 15];
+    else
+      e_sa = sa_src[min(m0 + r, M - 1)];
     const int f = (tid / 16) % (NI * NW);  // fragment of the tile: wave f / NI, ni = f % NI
     const int fn = f % NI, fw = f / NI;
     const int fcol0 = GELU ? (nt * (8 * NI * NW) + fw * (8 * NI) + (fn % (NI / 2)) * 16)
@@ -716,8 +771,11 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     // The clamped prefetches of the last step land before the LDS is reused or the wave ends.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   } else {
+  if constexpr (!QPRO) {
 #pragma unroll
-  for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
+    for (int d = 1; d < RING - 1; ++d) load(kb_begin + d, ra[d], rb[d]);
+  }
+  if constexpr (QPRO) load_a_lds(kb_begin + 1, ra[1 % RING]);
   unpack_first(ra[0], rb[0]);
   for (int i = 0; i < nkb; i += RING) {
 #pragma unroll
@@ -733,6 +791,9 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
       if constexpr (GELU) {
         if (i == 0 && j == 0) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(MI + NI) : "memory");
       }
+      // QPRO: the activation fragment two blocks ahead, from LDS (slots j, j + 1 hold this
+      // block's and the next one's).
+      if constexpr (QPRO) load_a_lds(kb_begin + i + j + 2, ra[(j + 2) % RING]);
       if (j == 0 || i + j < nkb) compute(ra[j], rb[j], ra[(j + 1) % RING], rb[(j + 1) % RING]);
     }
   }
@@ -1149,6 +1210,15 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
     case kCfg4x2K4: return launch_cfg<4, 2, 4, 4, 4, 2>(p, stream);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t launch_gemm_qpro(const GemmParams& p, hipStream_t stream) {
+  if (p.m < 1 || p.m > kQproMaxRows || p.k != 2048 || p.mtiles != 1 || p.ksplit != 1 || p.mode != kEpiFp16 ||
+      p.rope_group != 0 || p.xpro == nullptr)
+    return hipErrorInvalidValue;
+  gemm_w4a4_kernel<1, 2, 4, 4, false, 4, 2, false, false, false, true>
+      <<<dim3(static_cast<unsigned>(p.ntiles)), 256, 0, stream>>>(p);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm_gelu_quant(const GemmParams& p, int nquant, hipStream_t stream) {

@@ -215,28 +215,13 @@ __global__ __launch_bounds__(ROWS << LOGT) void fwht_quant_kernel(
     for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(h[e]);
   }
   if constexpr (NORM) {
-#pragma clang fp contract(off)
     static_assert(T == 64, "the fused RMSNorm reduces over one wave");
     // The norm weights are loaded with the row, before the sum of squares needs it.
     half8 wv[R / 8];
 #pragma unroll
     for (int c = 0; c < R / 8; ++c) wv[c] = *reinterpret_cast<const half8*>(nw + t * R + 8 * c);
     __builtin_amdgcn_sched_barrier(0);
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < R; ++j) ss = ss + v[j] * v[j];
-    ss = wave_sum_f(ss);
-    const float rr = 1.0f / __builtin_sqrtf(ss * (1.0f / K) + eps);
-#pragma unroll
-    for (int c = 0; c < R / 8; ++c) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float g = unit_offset ? 1.0f + static_cast<float>(wv[c][e]) : static_cast<float>(wv[c][e]);
-        float y = (v[8 * c + e] * rr) * g;
-        asm volatile("" : "+v"(y));  // keep the fp32 product (no v_fma_mix into fp16)
-        v[8 * c + e] = static_cast<float>(static_cast<_Float16>(y));
-      }
-    }
+    rms_norm_row_wave<K>(v, wv, eps, unit_offset);
   }
 
   if constexpr (T == 64) {

@@ -373,6 +373,33 @@ __device__ __forceinline__ void lane_stage(float (&v)[R], int lane) {
   }
 }
 
+// RMSNorm of one row held by one wave (transformers' GemmaRMSNorm, modeling_gemma.py:64-78,
+// weight wv with the (1 + w) offset when unit_offset), in place:
+//   h = fp16((x * r) * g),  r = 1 / sqrt(ss / K + eps) (correctly rounded sqrt and
+//   division),  g = unit_offset + w,
+// with ss summed per lane over its R consecutive elements in order, then over the 64 lanes
+// by the xor butterfly 32, 16, .., 1; v then holds the fp16 h as fp32 values.
+template <int K, int R>
+__device__ __forceinline__ void rms_norm_row_wave(float (&v)[R], const half8 (&wv)[R / 8], float eps,
+                                                  int unit_offset) {
+#pragma clang fp contract(off)
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < R; ++j) ss = ss + v[j] * v[j];
+  ss = wave_sum_f(ss);
+  const float rr = 1.0f / __builtin_sqrtf(ss * (1.0f / K) + eps);
+#pragma unroll
+  for (int c = 0; c < R / 8; ++c) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float g = unit_offset ? 1.0f + static_cast<float>(wv[c][e]) : static_cast<float>(wv[c][e]);
+      float y = (v[8 * c + e] * rr) * g;
+      asm volatile("" : "+v"(y));  // keep the fp32 product (no v_fma_mix into fp16)
+      v[8 * c + e] = static_cast<float>(static_cast<_Float16>(y));
+    }
+  }
+}
+
 // E3M2: the codes go out as E3M2 fragment slots (q then points at the q6 buffer; no row
 // corrections), else as INT4 words and qcorr.
 template <int LOGK, bool E3M2 = false>

@@ -79,7 +79,16 @@ struct GemmParams {
   int32_t spin_limit;    // s_sleep rounds a quant workgroup waits for one row block
   int32_t wait_extra;    // completions waited for beyond ntiles (0; tests force timeouts with 1)
   CacheWarmParams warm;  // read by the quant workgroups that find no row left
+  // Small-M prologue (launch_gemm_qpro): every workgroup quantizes the M <= kQproMaxRows fp16
+  // rows of xpro [M, 2048] itself, after the RMSNorm with weight nwpro when that is not
+  // null (eps_pro, unit_offset_pro), into LDS; q and sa are not read.
+  const _Float16* xpro;
+  const _Float16* nwpro;
+  float eps_pro;
+  int32_t unit_offset_pro;
+  float inv_sqrt_k_pro;
 };
+constexpr int kQproMaxRows = 4;
 
 // Control block of the fused gate/up + down-quant launch, in 128-byte lines so that the
 // polled words do not share one (a hot line slows every memory request near it):
@@ -233,6 +242,10 @@ hipError_t launch_quantize_e3m2(const void* x, const void* nw, float eps, int un
 // groups, optional residual or QKV attention prep) and kEpiGeluUp; p.q points at q6, the
 // groups' w at w6.
 hipError_t launch_gemm_e3m2(const GemmParams& p, int tile_cfg, hipStream_t stream);
+// 16 x 32 tiles whose four waves split K (K = 2048, 1 <= M <= kQproMaxRows, one K slice,
+// fp16 epilogue without the attention prep), the activation quant of p.xpro in every
+// workgroup's prologue.
+hipError_t launch_gemm_qpro(const GemmParams& p, hipStream_t stream);
 // Chooses the tile configuration; returns the K split used (>= 1) through *ksplit_out.
 hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream);
 // The paired gate/up GELU GEMM (7x4 tiles, no K split) with the down-projection quant of

@@ -109,6 +109,7 @@ def load_int4_gemm():
         "pi05w4a4_rmsnorm": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp]),
         "pi05w4a4_gelu_tanh_mul": (ctypes.c_int, [vp, vp, i64, vp, vp]),
         "pi05w4a4_gemm_residual": (ctypes.c_int, [vp, vp, i64, i32, vp, i32, vp, vp, vp, sz, vp]),
+        "pi05w4a4_quant_gemm_small": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, i32, vp, vp, vp, vp, vp]),
         "pi05w4a4_rmsnorm_quantize": (ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, vp]),
         "pi05w4a4_rmsnorm_quantize_warm": (
             ctypes.c_int, [vp, vp, ctypes.c_float, i32, i64, i32, vp, vp, ctypes.POINTER(vp), ctypes.POINTER(sz), i32,
@@ -729,6 +730,9 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
         return _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual, warm=warm)
     if residual is not None:  # before any launch: the kernel reads it through a raw pointer
         _check_residual(residual, x.device, (*x.shape[:-1], int(ws[0].size(0))))
+    m = x.numel() // k
+    if not gelu and k == 2048 and 1 <= m <= SMALL_M_MAX_ROWS and x.is_cuda:
+        return _run_small(x, ws, k, m, tiled, kind, norm, residual)
     # the reference quantizes before checking the weights
     q, sa = quantize(x, warm) if norm is None else rms_norm_quantize(x, *norm, warm=warm)
     conv = []
@@ -740,6 +744,55 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
     dev = x.device
     with _on_device(dev):
         return _gemm_from_q(q, sa, k, conv, tuple(x.shape[:-1]), dev, kind, gelu=gelu, residual=residual)
+
+
+# Up to this many rows (K = 2048) a call quantizes inside its GEMM launch
+# (pi05w4a4_quant_gemm_small): no activation codes in memory, one launch instead of two.
+SMALL_M_MAX_ROWS = 4
+
+
+def _run_small(x, ws, k, m, tiled, kind, norm, residual):
+    """_run for 1..SMALL_M_MAX_ROWS rows at K = 2048 (INT4 weights, fp16 outputs): the norm
+    (if any) and the activation quant run in the GEMM launch's prologue; outputs are the
+    two-launch path's bit for bit."""
+    conv = []
+    for w in ws:
+        _check_packed(w, k)
+        if tiled:
+            _check_tiled(w, k)
+        conv.append(_as_mfma(w, k, tiled))
+    x2 = x if x.is_contiguous() else x.contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    nw, eps, unit_offset = None, 0.0, False
+    if norm is not None:
+        weight, eps, unit_offset = norm
+        if not weight.is_cuda or weight.dtype != torch.float16 or weight.dim() != 1 or weight.numel() != k:
+            raise RuntimeError(f"RMSNorm weight must be a float16 CUDA/HIP tensor [{k}]")
+        nw = weight if weight.is_contiguous() else weight.contiguous()
+    dev = x2.device
+    lib = _lib if _lib is not None else load_int4_gemm()
+    outs = [torch.empty((m, int(w.size(0))), dtype=torch.float16, device=dev) for (w, _) in conv]
+    res = None
+    if residual is not None:
+        (w0, n_true), = conv
+        if n_true != int(w0.size(0)):
+            raise RuntimeError(f"residual must be [{', '.join(map(str, x.shape[:-1]))}, {n_true}] "
+                               f"with N a multiple of 16, got {tuple(residual.shape)}")
+        res = residual if residual.is_contiguous() and residual.data_ptr() % 16 == 0 else residual.contiguous().clone()
+    g = len(conv)
+    w_arr = (ctypes.c_void_p * g)(*[w.data_ptr() for (w, _) in conv])
+    y_arr = (ctypes.c_void_p * g)(*[o.data_ptr() for o in outs])
+    with _on_device(dev):
+        _check(lib.pi05w4a4_quant_gemm_small(x2.data_ptr(), _ptr(nw), float(eps), 1 if unit_offset else 0, m, k, g,
+                                             w_arr, _n_array(tuple(int(w.size(0)) for (w, _) in conv)), y_arr,
+                                             _ptr(res), _stream(dev)), f"pi05w4a4_quant_gemm_small ({kind})")
+    results = []
+    for o, (w, n_true) in zip(outs, conv):
+        if o.size(1) != n_true:
+            o = o[:, :n_true].contiguous()
+        results.append(o.view(*x.shape[:-1], n_true))
+    return results
 
 
 def _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual, warm=None):
