@@ -322,10 +322,13 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // concatenated 512-byte d4-5 parts (the last one half used when MI is odd).
   constexpr int kA6Chunks = MI + (MI + 1) / 2;
   constexpr int kA6Stage = kA6Chunks * 1024;
-  // QPRO: the block's 16 rows of codes (K = 2048: 16 fragments of 1 KB), then 16 row scales
-  // and 16 row corrections.
+  // QPRO: the block's 16 rows of codes (K = 2048: 16 fragments of 1 KB), 16 row scales, 16
+  // row corrections, then the two-wave rows' exchange (2 rows x 2 x 64 x 16 floats) and
+  // reductions (2 rows x 2 floats, 2 x 2 ints).
   constexpr int kLdsPro = kLdsA6 + (E3M2 ? 2 * kA6Stage : 0);
-  constexpr int kLdsGemm = kLdsPro + (QPRO ? 16 * 1024 + 2 * 16 * 4 : 0);
+  constexpr int kProXch = 16 * 1024 + 2 * 16 * 4;
+  constexpr int kProRed = kProXch + 2 * 2 * 64 * 16 * 4;
+  constexpr int kLdsGemm = kLdsPro + (QPRO ? kProRed + 8 * 4 : 0);
   constexpr int kLdsPool = (QFUSE && kQuantLdsBytes > kLdsGemm) ? kQuantLdsBytes : kLdsGemm;
   __shared__ __align__(16) char lds_pool[kLdsPool];
   int8_t* const fix_lds = reinterpret_cast<int8_t*>(lds_pool + kLdsFix);
@@ -347,19 +350,29 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
   // and every load of a k block shares one 32-bit lane offset.
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // QPRO: the M <= 4 rows are quantized here, by every workgroup for itself: wave w takes row
-  // min(w, M - 1) (32 consecutive elements per lane).  Its loads (and the norm weights') are
-  // issued first, so that the weight prefetches below queue behind them and their wait
-  // covers these loads only.  Without a norm the weight loads read the row again.
-  half8 pro_x[QPRO ? 4 : 1], pro_w[QPRO ? 4 : 1];
+  // QPRO: the M <= 4 rows are quantized here, by every workgroup for itself.  M <= 2: waves
+  // 2r and 2r + 1 take row min(r, M - 1), 16 elements per lane (thread 64 (w & 1) + lane:
+  // elements 16 t .. 16 t + 15, the two-wave quantizer), and each also holds the whole row
+  // in the one-wave layout (lane l: elements 32 l .. 32 l + 31) for the norm's sum of squares
+  // in the one-wave order; M = 3, 4: wave w takes row min(w, M - 1) in the one-wave layout.
+  // The loads (and the norm weights') are issued first, so that the weight prefetches below
+  // queue behind them and their wait covers these loads only.  Without a norm the weight
+  // loads read the row again.
+  half8 pro_x[QPRO ? 4 : 1], pro_w[QPRO ? 4 : 1], pro_x2[QPRO ? 2 : 1], pro_w2[QPRO ? 2 : 1];
+  const int pro_t2 = 64 * (wave & 1) + lane;
   if constexpr (QPRO) {
-    const int64_t prow = min(static_cast<int64_t>(wave), p.m - 1);
-    const _Float16* xr = p.xpro + prow * 2048 + lane * 32;
-    const _Float16* wr = (p.nwpro != nullptr ? p.nwpro : xr - lane * 32) + lane * 32;
+    const int64_t prow = min(static_cast<int64_t>(p.m <= 2 ? (wave >> 1) : wave), p.m - 1);
+    const _Float16* xrow = p.xpro + prow * 2048;
+    const _Float16* wrow = p.nwpro != nullptr ? p.nwpro : xrow;
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      pro_x[c] = *reinterpret_cast<const half8*>(xr + 8 * c);
-      pro_w[c] = *reinterpret_cast<const half8*>(wr + 8 * c);
+      pro_x[c] = *reinterpret_cast<const half8*>(xrow + lane * 32 + 8 * c);
+      pro_w[c] = *reinterpret_cast<const half8*>(wrow + lane * 32 + 8 * c);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      pro_x2[c] = *reinterpret_cast<const half8*>(xrow + pro_t2 * 16 + 8 * c);
+      pro_w2[c] = *reinterpret_cast<const half8*>(wrow + pro_t2 * 16 + 8 * c);
     }
   }
   const int wn = wave % NW;  // column block of the wave
@@ -571,13 +584,27 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
     for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(pro_x[c][e]);
-    if (p.nwpro != nullptr) rms_norm_row_wave<2048>(v, pro_w, p.eps_pro, p.unit_offset_pro);
-    // Codes, scale and correction of row `wave` of the block (rows past M hold a copy of row
-    // M - 1; rows 4-15 are never written: their outputs are never stored).
+    // Codes, scales and corrections of the block's rows (rows past M hold a copy of row
+    // M - 1; the rows after are never written: their outputs are never stored).
     int32_t* const lq = reinterpret_cast<int32_t*>(lds_pool + kLdsPro);
     float* const lsa = reinterpret_cast<float*>(lds_pool + kLdsPro + 16 * 1024);
     int32_t* const lqc = reinterpret_cast<int32_t*>(lds_pool + kLdsPro + 16 * 1024 + 16 * 4);
-    fwht_quant_row_wave<11>(v, lane, wave, lq, lsa, lqc, p.inv_sqrt_k_pro);
+    if (p.m <= 2) {  // uniform over the workgroup: every wave joins the pair quantizer's barriers
+      float v2[16];
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v2[8 * c + e] = static_cast<float>(pro_x2[c][e]);
+      if (p.nwpro != nullptr) rms_norm_apply<16>(v2, pro_w2, rms_norm_rr_wave<2048>(v, p.eps_pro), p.unit_offset_pro);
+      const int pr = wave >> 1;
+      float* const xch = reinterpret_cast<float*>(lds_pool + kLdsPro + kProXch) + pr * 2 * 64 * 16;
+      float* const redf = reinterpret_cast<float*>(lds_pool + kLdsPro + kProRed) + 2 * pr;
+      int* const redi = reinterpret_cast<int*>(lds_pool + kLdsPro + kProRed + 4 * 4) + 2 * pr;
+      fwht_quant_row_2wave<11>(v2, pro_t2, xch, redf, redi, true, pr, lq, lsa, lqc, p.inv_sqrt_k_pro);
+    } else {
+      if (p.nwpro != nullptr) rms_norm_row_wave<2048>(v, pro_w, p.eps_pro, p.unit_offset_pro);
+      fwht_quant_row_wave<11>(v, lane, wave, lq, lsa, lqc, p.inv_sqrt_k_pro);
+    }
     __syncthreads();
     load_a_lds(kb_begin, ra[0]);
   }
@@ -1216,7 +1243,9 @@ hipError_t launch_gemm_qpro(const GemmParams& p, hipStream_t stream) {
   if (p.m < 1 || p.m > kQproMaxRows || p.k != 2048 || p.mtiles != 1 || p.ksplit != 1 || p.mode != kEpiFp16 ||
       p.rope_group != 0 || p.xpro == nullptr)
     return hipErrorInvalidValue;
-  gemm_w4a4_kernel<1, 2, 4, 4, false, 4, 2, false, false, false, true>
+  // A 5-deep ring: all four k blocks of a wave's weights are requested before the prologue,
+  // so that no weight fetch waits behind the quant arithmetic.
+  gemm_w4a4_kernel<1, 2, 4, 4, false, 5, 2, false, false, false, true>
       <<<dim3(static_cast<unsigned>(p.ntiles)), 256, 0, stream>>>(p);
   return hipGetLastError();
 }

@@ -379,17 +379,22 @@ __device__ __forceinline__ void lane_stage(float (&v)[R], int lane) {
 //   division),  g = unit_offset + w,
 // with ss summed per lane over its R consecutive elements in order, then over the 64 lanes
 // by the xor butterfly 32, 16, .., 1; v then holds the fp16 h as fp32 values.
+// r of the row (the sum of squares in the order above).
 template <int K, int R>
-__device__ __forceinline__ void rms_norm_row_wave(float (&v)[R], const half8 (&wv)[R / 8], float eps,
-                                                  int unit_offset) {
+__device__ __forceinline__ float rms_norm_rr_wave(const float (&v)[R], float eps) {
 #pragma clang fp contract(off)
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < R; ++j) ss = ss + v[j] * v[j];
   ss = wave_sum_f(ss);
-  const float rr = 1.0f / __builtin_sqrtf(ss * (1.0f / K) + eps);
+  return 1.0f / __builtin_sqrtf(ss * (1.0f / K) + eps);
+}
+// h = fp16((x * r) * g) of the N values in v, elementwise (any layout of the row).
+template <int N>
+__device__ __forceinline__ void rms_norm_apply(float (&v)[N], const half8 (&wv)[N / 8], float rr, int unit_offset) {
+#pragma clang fp contract(off)
 #pragma unroll
-  for (int c = 0; c < R / 8; ++c) {
+  for (int c = 0; c < N / 8; ++c) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float g = unit_offset ? 1.0f + static_cast<float>(wv[c][e]) : static_cast<float>(wv[c][e]);
@@ -398,6 +403,11 @@ __device__ __forceinline__ void rms_norm_row_wave(float (&v)[R], const half8 (&w
       v[8 * c + e] = static_cast<float>(static_cast<_Float16>(y));
     }
   }
+}
+template <int K, int R>
+__device__ __forceinline__ void rms_norm_row_wave(float (&v)[R], const half8 (&wv)[R / 8], float eps,
+                                                  int unit_offset) {
+  rms_norm_apply<R>(v, wv, rms_norm_rr_wave<K>(v, eps), unit_offset);
 }
 
 // E3M2: the codes go out as E3M2 fragment slots (q then points at the q6 buffer; no row
