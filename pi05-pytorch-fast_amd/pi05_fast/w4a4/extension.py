@@ -291,6 +291,11 @@ def _q6_bytes(m: int, k: int) -> int:
 
 
 # ----------------------------------------------------------------------------- pieces
+# ctypes argument arrays of warm lists, by their (pointer, bytes) pairs: building ctypes
+# arrays costs several microseconds per call, a large share of an eager op call.
+_WARM_ARGS: dict[tuple, tuple] = {}
+
+
 def _warm_args(warm, who: str):
     """(pointer array, byte-size array, count) of the non-empty warm tensors, or None."""
     ws = [t for t in (warm or []) if t is not None and t.numel() > 0]
@@ -298,9 +303,15 @@ def _warm_args(warm, who: str):
         return None
     if len(ws) > 4 or any((not t.is_cuda) or (not t.is_contiguous()) for t in ws):
         raise RuntimeError(f"{who}: warm takes up to 4 contiguous CUDA/HIP tensors")
-    wp = (ctypes.c_void_p * len(ws))(*[t.data_ptr() for t in ws])
-    wb = (ctypes.c_size_t * len(ws))(*[(t.numel() * t.element_size()) // 16 * 16 for t in ws])
-    return wp, wb, len(ws)
+    key = tuple((t.data_ptr(), (t.numel() * t.element_size()) // 16 * 16) for t in ws)
+    hit = _WARM_ARGS.get(key)
+    if hit is None:
+        if len(_WARM_ARGS) > 1024:
+            _WARM_ARGS.clear()
+        wp = (ctypes.c_void_p * len(key))(*[p for p, _ in key])
+        wb = (ctypes.c_size_t * len(key))(*[b for _, b in key])
+        hit = _WARM_ARGS[key] = (wp, wb, len(key))
+    return hit
 
 
 def quantize(x: torch.Tensor, warm: list[torch.Tensor] | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -616,10 +627,27 @@ _NORM_WARM_MIN_ROWS = 256
 _GATE_UP_SELF_WARM_BYTES = 4 << 20
 
 
+_UP_SPLITS: dict[int, tuple] = {}
+
+
 def gate_up_warm_split(w_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
     """(head, tail) byte ranges of the up weight as flat views: the gate/up op's norm +
     quant launch warms the tail (at most _GATE_UP_SELF_WARM_BYTES, a multiple of 16 bytes),
-    the caller may warm the head earlier."""
+    the caller may warm the head earlier.  Cached per tensor (same storage, version and
+    split size)."""
+    key = id(w_up)
+    hit = _UP_SPLITS.get(key)
+    if hit is not None:
+        ref, ptr, version, nbytes, split = hit
+        if ref() is w_up and ptr == w_up.data_ptr() and version == w_up._version and nbytes == _GATE_UP_SELF_WARM_BYTES:
+            return split
+    split = _gate_up_split(w_up)
+    _UP_SPLITS[key] = (weakref.ref(w_up, lambda _r, key=key: _UP_SPLITS.pop(key, None)), w_up.data_ptr(),
+                       w_up._version, _GATE_UP_SELF_WARM_BYTES, split)
+    return split
+
+
+def _gate_up_split(w_up: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor | None]:
     flat = w_up.reshape(-1)
     per16 = max(1, 16 // flat.element_size())
     tail = min(flat.numel(), _GATE_UP_SELF_WARM_BYTES // flat.element_size()) // per16 * per16
