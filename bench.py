@@ -591,7 +591,7 @@ def kernel_class(name: str) -> str:
             return "down_residual"
         if (mi, ni, nwaves, kw) == (7, 4, 4, 1):
             return "gate_up"
-        if (mi, ni, nwaves, kw) == (2, 2, 4, 1):
+        if (mi, ni, nwaves, kw) in ((2, 2, 4, 1), (4, 4, 4, 4)):
             return "o_residual"
         return "gemm"
     return next((c for rx, c in _KERNEL_CLASS_RULES if re.search(rx, name)), "other")

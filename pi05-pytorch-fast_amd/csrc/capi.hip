@@ -78,6 +78,7 @@ constexpr TileCfg kCfg1x2{w4a4::kCfg1x2, 1, 2, 4, 1};
 constexpr TileCfg kCfg1x2K4{w4a4::kCfg1x2K4, 1, 2, 4, 4};
 constexpr TileCfg kCfg2x2K4{w4a4::kCfg2x2K4, 2, 2, 4, 4};
 constexpr TileCfg kCfg4x2K4{w4a4::kCfg4x2K4, 4, 2, 4, 4};
+constexpr TileCfg kCfg4x4K4{w4a4::kCfg4x4K4, 4, 4, 4, 4};
 
 struct Plan {
   TileCfg cfg;
@@ -95,14 +96,19 @@ struct Plan {
 //    - otherwise 32 x 128 tiles that keep the whole K in each wave, when they fit in two
 //      workgroups per CU (at M = 776 with weights streamed from HBM: o 7.8 us and QKV
 //      9.3 us, against 10.1 and 12.0 with 4 waves splitting K of 112 x 64 tiles, and 9.0
-//      and 10.1 with 64 x 128 tiles), else 64 x 128 tiles, else the K split.
+//      and 10.1 with 64 x 128 tiles), else 64 x 128 tiles, else the K split.  One weight
+//      (o) and the QKV + RoPE launch take 64 x 64 tiles with 4 waves splitting K instead
+//      (at M = 776, weights warm: o + residual 7.16 -> 6.87 us, QKV + RoPE 9.19 -> 8.55;
+//      the plain three-weight QKV launch measured 7.6 -> 9.3 us with them, and 32 x 128
+//      tiles with the K split 9.0 us for QKV).
 //  * M <= 64 (weight streaming): 16-, 32- or 64-row tiles of 32 columns whose four waves
 //    split K and sum their parts through LDS, so that one launch streams the weights
 //    (QKV at M = 1: 3.0 us, against 5.8 us for 16 x 128 tiles with a global K split and
 //    its reduce launch).  A global split stays for long K (down), with at least 4 k blocks
 //    per wave.  The paired gate/up GELU GEMM uses them up to M = 16 only, and 4-waves-
 //    along-N tiles with the global split above that.
-Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split) {
+Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, bool allow_split,
+               bool rope = false) {
   Plan pl{};
   const int64_t kNumCUs = w4a4::device_cu_count();
   // The GELU pairing's 16-column K-split tiles make 1024 workgroups at gate/up size, each
@@ -133,6 +139,9 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
       pl.cfg = kCfg7x4K8;
     } else if (cdiv(m, 32) * count_tiles(kCfg2x2) <= 2 * kNumCUs) {
       pl.cfg = kCfg2x2;
+      // One weight, or the attention prep's launch: 64 x 64 tiles with the K split, when
+      // they give every CU a workgroup (then no global split follows either way).
+      if ((ngroups == 1 || rope) && cdiv(m, 64) * count_tiles(kCfg4x4K4) >= kNumCUs) pl.cfg = kCfg4x4K4;
     } else if (cdiv(m, 64) * count_tiles(kCfg4x2) <= 2 * kNumCUs) {
       pl.cfg = kCfg4x2;
     } else {
@@ -202,7 +211,7 @@ int run_gemm(const int32_t* q, const float* sa, int64_t m, int32_t k, int ngroup
              const void* residual = nullptr, const QkvRope* rope = nullptr) {
   const bool gelu = mode == w4a4::kEpiGeluUp;
   // The attention prep epilogue needs the whole K in one launch: no global split for it.
-  const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc && rope == nullptr);
+  const Plan pl = make_plan(m, k, ngroups, n, gelu, mode != w4a4::kEpiAcc && rope == nullptr, rope != nullptr);
   if (pl.mtiles > 65535) return fail(PI05W4A4_EINVAL, "M too large (%lld rows)", (long long)m);
   w4a4::GemmParams p{};
   p.q = q;

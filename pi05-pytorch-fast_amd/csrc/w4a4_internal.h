@@ -186,6 +186,9 @@ enum TileCfg : int {
   kCfg1x2K4 = 7,  // MI 1: 16 x 32
   kCfg2x2K4 = 8,  // MI 2: 32 x 32
   kCfg4x2K4 = 9,  // MI 4: 64 x 32
+  // Mid-size M (the QKV + RoPE and o GEMMs at hundreds of rows): 4 waves split K of a
+  // 64 x 64 tile, so that each operand byte of the tile is loaded once per workgroup.
+  kCfg4x4K4 = 10,  // MI 4, NI 4: 64 x 64
 };
 
 

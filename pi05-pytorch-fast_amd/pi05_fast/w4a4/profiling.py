@@ -262,10 +262,10 @@ TRAFFIC_CLASSES = {
                       "fp16 out 3.18 MB"),
     "qkv": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false, false, false>", 500,
             _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560), "codes A 0.79 MB + weights 2.62 MB; fp16 q/k/v 3.97 MB"),
-    "qkv_rope": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, true, false, false, false>", 500,
+    "qkv_rope": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, true, false, false, false>", 520,
                  _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560) + 2 * _M * 256 * 2 * 2 + 2 * 832 * 256 * 2,
                  "as qkv + rotary tables 0.79 MB read + key states 0.40 MB and K/V^T 0.85 MB written"),
-    "o_residual": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false, false, false>", 400,
+    "o_residual": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, false, false, false, false>", 416,
                    _gemm_alg_bytes(_M, 2048, 2048, 2.0 * 2.0 * _M * 2048),
                    "codes A 0.79 MB + weights 2.10 MB + residual 3.18 MB; out 3.18 MB"),
     "quant_k16384": ("fwht_quant_kernel<14, 8, 1, false, false>", 776, 2.0 * _M * 16384 + _M * 16384 / 2 + 4 * _M,

@@ -173,8 +173,11 @@ def test_fused_norm_code_drift_against_eager_gemma_norm(ext, cuda, seed):
     assert frac <= 1e-4, msg
 
 
+# (776 | 520, 2048, 2048) and (776, 2048, 2000): 64 x 64 tiles whose four waves split K (the
+# last row tile partial, and at N = 2000 the last column tile a quarter used)
 @pytest.mark.parametrize("m,k,n", [(776, 2048, 2048), (776, 16384, 2048), (1, 16384, 2048), (64, 2048, 2048),
-                                   (5, 2048, 256), (30, 2048, 96), (64, 16384, 2048), (2200, 2048, 2048)])
+                                   (5, 2048, 256), (30, 2048, 96), (64, 16384, 2048), (2200, 2048, 2048),
+                                   (520, 2048, 2048), (776, 2048, 2000)])
 def test_gemm_residual_matches_oracle(ext, cuda, m, k, n):
     gen = inp.generator(m + k + n)
     x = inp.activations(gen, m, k) if k == 2048 else inp.geglu_activations(gen, m, k)
