@@ -779,8 +779,12 @@ __global__ __launch_bounds__(64 * NWAVES) __attribute__((amdgpu_waves_per_eu(WPE
           aop[mi] = e3m2_op(lo, hi.x, hi.y);
         }
         __builtin_amdgcn_sched_barrier(0);
-        load_a6(kb_begin + i + j + 1, j ^ 1);
-        load_b6(kb_begin + i + j + 1, b6[j ^ 1]);
+        // The last step requests nothing (uniform branch): every step starts with a full
+        // vmcnt(0) wait, so no wait count depends on it.
+        if (i + j + 1 < nkb) {
+          load_a6(kb_begin + i + j + 1, j ^ 1);
+          load_b6(kb_begin + i + j + 1, b6[j ^ 1]);
+        }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi) {
@@ -1237,7 +1241,16 @@ hipError_t launch_gemm(GemmParams p, int tile_cfg, hipStream_t stream) {
   switch (tile_cfg) {
     case kCfg7x4: return launch_cfg<7, 4, 4, 1>(p, stream);
     case kCfg7x4K4: return launch_cfg<7, 4, 4, 4>(p, stream);
-    case kCfg7x4K8: return launch_cfg<7, 4, 8, 8>(p, stream);
+    case kCfg7x4K8: {
+      // K = 16384 in one slice: 16 blocks per wave, the straight-line form (down + residual
+      // at 776 rows 22.1-22.2 -> 21.7 us).
+      if (p.k == 16384 && p.ksplit == 1 && p.kblocks_per_split == 128 && p.mode == kEpiFp16 && p.rope_group == 0) {
+        const dim3 grid(static_cast<unsigned>(p.ntiles) * static_cast<unsigned>(p.mtiles));
+        gemm_w4a4_kernel<7, 4, 8, 8, false, 2, 2, false, false, false, false, 16><<<grid, 512, 0, stream>>>(p);
+        return hipGetLastError();
+      }
+      return launch_cfg<7, 4, 8, 8>(p, stream);
+    }
     case kCfg7x2: return launch_cfg<7, 2, 4, 1>(p, stream);
     case kCfg4x2: return launch_cfg<4, 2, 4, 1>(p, stream);
     // 32 x 128 tiles stream the whole K per wave: a 3-deep ring hides more of the load
