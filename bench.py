@@ -576,7 +576,7 @@ def _gemm_template_args(name: str) -> list[int] | None:
 
 def kernel_class(name: str) -> str:
     """Kernel class of a profiled kernel name.  gemm_w4a4_kernel<MI, NI, NWAVES, KW, GELU,
-    RING, WPE, QKV_PREP, QFUSE, E3M2, QPRO>: the 776-token forward's GEMMs by their tile
+    RING, WPE, QKV_PREP, QFUSE, E3M2, QPRO, NKB>: the 776-token forward's GEMMs by their tile
     configuration and epilogue."""
     a = _gemm_template_args(name)
     if a is not None:

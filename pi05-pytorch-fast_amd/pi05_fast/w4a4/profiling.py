@@ -241,31 +241,31 @@ def _gemm_e3m2_bytes(m: int, k: int, n: int, out_bytes: float) -> float:
 # The kernel classes of the 776-token prefix-LM forward (one decoder layer's launches), as
 # bench.py --only-kernel names them: class -> (kernel name, workgroups, algorithmic bytes,
 # what they are).  gemm_w4a4_kernel<MI, NI, NWAVES, KW, GELU, RING, WPE, QKV_PREP, QFUSE,
-# E3M2, QPRO>, fwht_quant_kernel<LOGK, LOGT, ROWS, NORM, E3M2>.
+# E3M2, QPRO, NKB>, fwht_quant_kernel<LOGK, LOGT, ROWS, NORM, E3M2>.
 _M = 776
 TRAFFIC_CLASSES = {
-    "gate_up_gelu": ("gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, true, false>", 896,
+    "gate_up_gelu": ("gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, true, false, 0>", 896,
                      _gemm_e3m2_bytes(_M, 2048, 32768, 2.0 * _M * 16384),
                      "E3M2 codes A 1.19 MB + gate and up weights 50.33 MB + scales; fp16 h 25.43 MB"),
-    "gate_up": ("gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, true, false>", 896,
+    "gate_up": ("gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, true, false, 0>", 896,
                 _gemm_e3m2_bytes(_M, 2048, 32768, 2.0 * _M * 32768),
                 "E3M2 codes A 1.19 MB + weights 50.33 MB + scales; fp16 gate and up 50.86 MB"),
-    "gate_up_gelu_int4": ("gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, false, false>", 896,
+    "gate_up_gelu_int4": ("gemm_w4a4_kernel<7, 4, 4, 1, true, 2, 2, false, false, false, false, 0>", 896,
                           _gemm_alg_bytes(_M, 2048, 32768, 2.0 * _M * 16384),
                           "codes A 0.79 MB + gate and up weights 33.55 MB + scales/corrections; fp16 h 25.43 MB"),
-    "gate_up_int4": ("gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, false, false>", 896,
+    "gate_up_int4": ("gemm_w4a4_kernel<7, 4, 4, 1, false, 2, 2, false, false, false, false, 0>", 896,
                      _gemm_alg_bytes(_M, 2048, 32768, 2.0 * _M * 32768),
                      "codes A 0.79 MB + weights 33.55 MB + scales/corrections; fp16 gate and up 50.86 MB"),
-    "down_residual": ("gemm_w4a4_kernel<7, 4, 8, 8, false, 2, 2, false, false, false, false>", 224,
+    "down_residual": ("gemm_w4a4_kernel<7, 4, 8, 8, false, 2, 2, false, false, false, false, 16>", 224,
                       _gemm_alg_bytes(_M, 16384, 2048, 2.0 * 2.0 * _M * 2048),
                       "codes A 6.36 MB + down weights 16.78 MB + scales/corrections + fp16 residual 3.18 MB; "
                       "fp16 out 3.18 MB"),
-    "qkv": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false, false, false>", 500,
+    "qkv": ("gemm_w4a4_kernel<2, 2, 4, 1, false, 3, 2, false, false, false, false, 0>", 500,
             _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560), "codes A 0.79 MB + weights 2.62 MB; fp16 q/k/v 3.97 MB"),
-    "qkv_rope": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, true, false, false, false>", 520,
+    "qkv_rope": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, true, false, false, false, 4>", 520,
                  _gemm_alg_bytes(_M, 2048, 2560, 2.0 * _M * 2560) + 2 * _M * 256 * 2 * 2 + 2 * 832 * 256 * 2,
                  "as qkv + rotary tables 0.79 MB read + key states 0.40 MB and K/V^T 0.85 MB written"),
-    "o_residual": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, false, false, false, false>", 416,
+    "o_residual": ("gemm_w4a4_kernel<4, 4, 4, 4, false, 2, 2, false, false, false, false, 4>", 416,
                    _gemm_alg_bytes(_M, 2048, 2048, 2.0 * 2.0 * _M * 2048),
                    "codes A 0.79 MB + weights 2.10 MB + residual 3.18 MB; out 3.18 MB"),
     "quant_k16384": ("fwht_quant_kernel<14, 8, 1, false, false>", 776, 2.0 * _M * 16384 + _M * 16384 / 2 + 4 * _M,
