@@ -212,6 +212,10 @@ GEMM_SHAPES = [
     # 112 x 64 tiles with four k parts (neither narrow tile fits two per CU): the k parts'
     # reduce-scatter leaves two row blocks to three of the waves and one to the fourth
     (2200, 2048, 2048),
+    # the fixed-length K slices with a ragged last row tile: 64 x 64 tiles at K = 2048
+    # (40 rows in the last tile) and the 16-block down tiles at K = 16384 (104 rows)
+    (1000, 2048, 2048),
+    (1000, 2048, 16384),
 ]
 
 
