@@ -269,6 +269,70 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const _Float16* __restr
   if (t == 0) qcorr[row] = -8 * s16;
 }
 
+
+// K = 2048 with two waves per row, for row counts that leave most SIMDs idle: waves 2i
+// and 2i + 1 of a workgroup take row 2 blockIdx.x + i, 16 elements per lane
+// (fwht_quant_row_2wave: thread t of the pair holds elements 16 t .. 16 t + 15).  With
+// NORM both waves also load the row in the one-wave layout (lane l: elements 32 l ..
+// 32 l + 31) and take its sum of squares in the one-wave order, so that the norm, and
+// with it every code, equals fwht_quant_kernel<11, 6, 4, true>'s bit for bit.  A pair
+// past M (odd M) computes a copy of row M - 1 and stores nothing.  Workgroups past the
+// rows (launched only with warm buffers) warm the cache, as in fwht_quant_kernel.
+// Measured with the RMSNorm (µs, two-wave rows / one-wave rows): M = 1: 3.46 / 3.73, 64:
+// 3.8 / 4.2-4.3, 256: 3.9-4.0 / 4.4, 512: 4.2 / 4.45-4.5, but 640: 5.3-5.4 / 4.6 (more
+// waves than SIMDs), so the two-wave rows run up to kTwoWaveRowsMax rows.
+constexpr int64_t kTwoWaveRowsMax = 512;
+template <bool NORM>
+__global__ __launch_bounds__(256) void fwht_quant2_kernel(const _Float16* __restrict__ x, int64_t m,
+                                                          int32_t* __restrict__ q, float* __restrict__ sa,
+                                                          int32_t* __restrict__ qcorr, float inv_sqrt_k,
+                                                          const _Float16* __restrict__ nw, float eps,
+                                                          int unit_offset,
+                                                          const CacheWarmParams warm = CacheWarmParams{}) {
+  __shared__ __align__(16) float xch[2][2 * 64 * 16];
+  __shared__ float redf[2][2];
+  __shared__ int redi[2][2];
+  const int tid = threadIdx.x;
+  {
+    const int64_t row_blocks = (m + 1) / 2;
+    if (static_cast<int64_t>(blockIdx.x) >= row_blocks) {
+      cache_warm_part<256>(warm, blockIdx.x - row_blocks, gridDim.x - row_blocks, tid);
+      return;
+    }
+  }
+  const int pr = tid >> 7;
+  const int t = tid & 127;
+  const int64_t row_raw = 2 * static_cast<int64_t>(blockIdx.x) + pr;
+  const bool valid = row_raw < m;
+  const int64_t row = valid ? row_raw : m - 1;
+  const _Float16* xr = x + row * 2048;
+  float v2[16];
+  {
+    const half8 a0 = *reinterpret_cast<const half8*>(xr + 16 * t);
+    const half8 a1 = *reinterpret_cast<const half8*>(xr + 16 * t + 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v2[e] = static_cast<float>(a0[e]);
+      v2[8 + e] = static_cast<float>(a1[e]);
+    }
+  }
+  if constexpr (NORM) {
+    const int lane = tid & 63;
+    half8 xw[4], w2[2];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xw[c] = *reinterpret_cast<const half8*>(xr + 32 * lane + 8 * c);
+#pragma unroll
+    for (int c = 0; c < 2; ++c) w2[c] = *reinterpret_cast<const half8*>(nw + 16 * t + 8 * c);
+    float v[32];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[8 * c + e] = static_cast<float>(xw[c][e]);
+    rms_norm_apply<16>(v2, w2, rms_norm_rr_wave<2048>(v, eps), unit_offset);
+  }
+  fwht_quant_row_2wave<11>(v2, t, xch[pr], redf[pr], redi[pr], valid, row, q, sa, qcorr, inv_sqrt_k);
+}
+
 }  // namespace
 
 hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, float* sa,
@@ -289,6 +353,11 @@ hipError_t launch_quantize(const void* x, int64_t m, int32_t k, int32_t* q, floa
       break;
     }
     case 2048:
+      if (m <= kTwoWaveRowsMax) {
+        fwht_quant2_kernel<false><<<dim3(static_cast<unsigned>((m + 1) / 2)), 256, 0, stream>>>(
+            xh, m, q, sa, qcorr, inv_sqrt_k, nullptr, 0.0f, 0);
+        break;
+      }
       fwht_quant_kernel<11, 6, 4><<<dim3(static_cast<unsigned>((m + 3) / 4)), 256, 0, stream>>>(
           xh, m, q, sa, qcorr, inv_sqrt_k);
       break;
@@ -312,6 +381,14 @@ hipError_t launch_rmsnorm_quantize(const void* x, const void* w, float eps, int 
   // without one; none once the rows cover every CU.
   const int64_t row_blocks = (m + 3) / 4;
   const int64_t cus = device_cu_count();
+  if (m <= kTwoWaveRowsMax) {  // two waves per row, two rows per workgroup; warming as below
+    const int64_t pair_blocks = (m + 1) / 2;
+    const int64_t extra2 = (warm != nullptr && warm->nbuf > 0 && pair_blocks < cus) ? cus - pair_blocks : 0;
+    fwht_quant2_kernel<true><<<dim3(static_cast<unsigned>(pair_blocks + extra2)), 256, 0, stream>>>(
+        static_cast<const _Float16*>(x), m, q, sa, qcorr, inv_sqrt_k, static_cast<const _Float16*>(w), eps,
+        unit_offset, extra2 > 0 ? *warm : CacheWarmParams{});
+    return hipGetLastError();
+  }
   const int64_t extra = (warm != nullptr && warm->nbuf > 0 && row_blocks < cus) ? cus - row_blocks : 0;
   fwht_quant_kernel<11, 6, 4, true><<<dim3(static_cast<unsigned>(row_blocks + extra)), 256, 0, stream>>>(
       static_cast<const _Float16*>(x), m, q, sa, qcorr, inv_sqrt_k, static_cast<const _Float16*>(w),

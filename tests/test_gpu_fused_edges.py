@@ -35,7 +35,10 @@ def _codes(q: torch.Tensor, m: int, k: int) -> np.ndarray:
     return orc.unpack_nibbles(inp.to_np(codes_from_fragment_major(q.cpu(), m, k)), k)
 
 
-@pytest.mark.parametrize("m,scale,offset", [(776, 1.0, True), (1, 1.0, True), (37, 40.0, True), (64, 0.05, False)])
+# M <= 512 runs two waves per row (odd M: the last pair is a clamped copy that stores
+# nothing), M > 512 one wave per row.
+@pytest.mark.parametrize("m,scale,offset", [(776, 1.0, True), (1, 1.0, True), (37, 40.0, True), (64, 0.05, False),
+                                            (511, 1.0, True), (512, 3.0, False), (513, 1.0, True)])
 def test_rmsnorm_quantize_matches_oracle(ext, cuda, m, scale, offset):
     k = 2048
     gen = inp.generator(m)
@@ -55,7 +58,7 @@ def test_rmsnorm_quantize_matches_oracle(ext, cuda, m, scale, offset):
     assert np.array_equal(qc, -128 * q_ref[:, 1::2].astype(np.int64).sum(axis=1))
 
 
-@pytest.mark.parametrize("m", [1, 5, 776, 1100])
+@pytest.mark.parametrize("m", [1, 5, 301, 776, 1100])
 def test_rmsnorm_quantize_cache_warm_changes_nothing(ext, cuda, m):
     """The norm + quant with cache warming (a workgroup for each CU the row workgroups leave
     idle reads further buffers, here 12 MB; at M = 1100 the rows cover every CU and nothing
@@ -84,7 +87,7 @@ def test_rmsnorm_quantize_cache_warm_changes_nothing(ext, cuda, m):
         assert torch.equal(t, t0)
 
 
-@pytest.mark.parametrize("m", [1, 776])
+@pytest.mark.parametrize("m", [1, 300, 776])
 def test_rms_norm_qkv_warms_its_weights_same_outputs(ext, cuda, monkeypatch, m):
     """rms_norm_int4_gemm3 (whose norm + quant launch warms the QKV weights from 256 rows
     on: at M = 776, not at M = 1) gives the same q, k, v with warming on and off

@@ -75,7 +75,7 @@ def test_quantize_matches_golden(golden, ext, cuda, k):
 @pytest.mark.parametrize(
     "m,k,kind",
     [(776, 2048, "act"), (776, 16384, "geglu"), (640, 1024, "act"), (3, 2048, "act"), (1, 16384, "act"),
-     (33, 4096, "act")],
+     (33, 4096, "act"), (511, 2048, "act"), (513, 2048, "act")],
 )
 def test_quantize_matches_oracle(ext, cuda, m, k, kind):
     gen = inp.generator(m + k)
