@@ -94,3 +94,36 @@ def test_traffic_classes_algorithmic_bytes():
     assert c["o_residual"][2] / 1e6 == pytest.approx(9.26, abs=0.01)
     assert c["quant_k16384"][2] / 1e6 == pytest.approx(31.79, abs=0.01)
     assert c["rmsnorm_quant_k2048"][2] / 1e6 == pytest.approx(3.98, abs=0.01)
+
+
+# The forward's GEMM instances as the launchers name them (mangled, twelve template
+# arguments: <MI, NI, NWAVES, KW, GELU, RING, WPE, QKV_PREP, QFUSE, E3M2, QPRO, NKB>).
+def _mangled(args):
+    enc = "".join(f"Lb{int(a)}E" if isinstance(a, bool) else f"Li{a}E" for a in args)
+    return f"_ZN4w4a412_GLOBAL__N_116gemm_w4a4_kernelI{enc}EEvNS_10GemmParamsE"
+
+
+FORWARD_GEMMS = {
+    "gate_up_gelu": (7, 4, 4, 1, True, 2, 2, False, False, True, False, 0),
+    "down_residual": (7, 4, 8, 8, False, 2, 2, False, False, False, False, 16),
+    "qkv_rope": (4, 4, 4, 4, False, 2, 2, True, False, False, False, 4),
+    "o_residual": (4, 4, 4, 4, False, 2, 2, False, False, False, False, 4),
+}
+
+
+@pytest.mark.parametrize("cls", sorted(FORWARD_GEMMS))
+def test_forward_gemm_names_match_their_classes(cls):
+    """The profiling tables and bench.py's in-forward breakdown find each forward GEMM by
+    its name: the demangled name is the traffic class's, and bench.kernel_class maps both
+    the mangled and the demangled name to the class."""
+    import importlib.util
+    import pathlib
+
+    spec = importlib.util.spec_from_file_location("_bench", pathlib.Path(__file__).resolve().parents[1] / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+    name = _mangled(FORWARD_GEMMS[cls])
+    short = prof.short_name(name)
+    assert short == "w4a4::" + prof.TRAFFIC_CLASSES[cls][0]
+    assert bench.kernel_class(name) == cls
+    assert bench.kernel_class(short) == cls
