@@ -78,12 +78,18 @@ def load_time_weight(
     if use_mfma and on_gpu and out_features % 16 == 0:
         from pi05_fast.w4a4.extension import repack_weight, repack_weight_e3m2
 
+        w_mfma = repack_weight(w.to(device), k=in_features, tiled=False)
         # The MLP's gate/up weights (K = 2048) take the E3M2 form of the same codes, which
-        # the FP6-MFMA GEMM reads (PI05_W4A4_E3M2=0: the INT4 MFMA layout for all).
+        # the FP6-MFMA GEMM reads (PI05_W4A4_E3M2=0: the INT4 MFMA layout for all); the INT4
+        # form stays registered as its twin for calls of few rows, which run faster on it.
         if (os.environ.get("PI05_W4A4_E3M2", "1") != "0" and name.endswith((".mlp.gate_proj", ".mlp.up_proj"))
                 and in_features == 2048 and out_features % 32 == 0):
-            return repack_weight_e3m2(w.to(device), k=in_features, tiled=False), False
-        return repack_weight(w.to(device), k=in_features, tiled=False), False
+            from pi05_fast.w4a4.extension import register_int4_twin
+
+            w_e3m2 = repack_weight_e3m2(w_mfma, k=in_features, tiled=False)
+            register_int4_twin(w_e3m2, w_mfma, in_features)
+            return w_e3m2, False
+        return w_mfma, False
     gate_preshuffle = os.environ.get("PI05_W4A4_GATE_PRESHUFFLE", "1") != "0"
     row_pad_words = _row_pad_words()
     logical_words = in_features // 8
@@ -386,7 +392,12 @@ def _fused_decoder_layer_forward(
     # (the tail of the up weight is warmed by the gate/up op's own norm + quant launch)
     warm = None
     if warming:
-        warm = [attn.o_proj.packed, mlp.gate_proj.packed, ext.gate_up_warm_split(mlp.up_proj.packed)[0]]
+        # the forms the gate/up GEMM reads for this many rows (INT4 twins at few rows, whose
+        # own norm + quant launch warms nothing: the whole up weight then)
+        rows = x.numel() // x.size(-1)
+        wg, wu = ext.gemm_weights_for_rows([mlp.gate_proj.packed, mlp.up_proj.packed], mlp.gate_proj.in_features,
+                                           rows)
+        warm = [attn.o_proj.packed, wg, wu if wu is not mlp.up_proj.packed else ext.gate_up_warm_split(wu)[0]]
     wk_rope = _k_rope_weight(attn, x)
     if wk_rope is not None:
         # One KV head: RoPE and the attention's K/V layout in the QKV GEMM epilogue.

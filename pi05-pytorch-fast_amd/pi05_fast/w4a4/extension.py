@@ -469,6 +469,50 @@ _MFMA_CACHE: dict[int, tuple] = {}
 _CACHE_CLEARERS: list = []
 
 
+# INT4 MFMA-layout twins of E3M2-layout weights, registered by the loader, which converts
+# the MLP's gate/up weights to E3M2 and keeps both forms (apply.load_time_weight): calls
+# of at most E3M2_MAX_INT4_ROWS rows run the INT4 kernels on the twins, since the E3M2
+# GEMM has no small-M tiles (gate/up + GELU at 1-128 rows: 17-18 us on E3M2 weights
+# against 6-12 us on INT4 ones; from 160 rows on E3M2 is faster).  An entry lives as long
+# as its E3M2 weight and is ignored once that weight is modified in place (version or data
+# pointer moved): the call then runs on the E3M2 weight.
+E3M2_MAX_INT4_ROWS = 128
+_INT4_TWINS: dict[int, tuple] = {}
+
+
+def register_int4_twin(w_e3m2: torch.Tensor, w_int4: torch.Tensor, k: int) -> None:
+    """Record w_int4 (MFMA layout) as the INT4 form of the E3M2-layout weight w_e3m2."""
+    if not (is_e3m2_layout(w_e3m2, k) and is_mfma_layout(w_int4, k)):
+        raise RuntimeError("register_int4_twin takes an E3M2-layout weight and its MFMA-layout INT4 form")
+    if int(w_e3m2.size(0)) != int(w_int4.size(0)):
+        raise RuntimeError("the two forms of a weight must have the same N")
+    key = id(w_e3m2)
+    _INT4_TWINS[key] = (weakref.ref(w_e3m2, lambda _r, key=key: _INT4_TWINS.pop(key, None)), w_e3m2._version,
+                        w_e3m2.data_ptr(), k, w_int4)
+
+
+def int4_twin(w: torch.Tensor, k: int) -> torch.Tensor | None:
+    """The registered INT4 form of the E3M2-layout weight w, or None."""
+    hit = _INT4_TWINS.get(id(w))
+    if hit is None:
+        return None
+    ref, version, ptr, hk, twin = hit
+    if ref() is not w or version != w._version or ptr != w.data_ptr() or hk != k:
+        return None
+    return twin
+
+
+def gemm_weights_for_rows(ws: list[torch.Tensor], k: int, m: int) -> list[torch.Tensor]:
+    """The tensors a call of m rows on the weights ws reads: the INT4 twins of E3M2-layout
+    weights at m <= E3M2_MAX_INT4_ROWS when every weight has one, else ws (for cache
+    warming lists)."""
+    if m <= E3M2_MAX_INT4_ROWS and ws and all(is_e3m2_layout(w, k) for w in ws):
+        twins = [int4_twin(w, k) for w in ws]
+        if all(t is not None for t in twins):
+            return twins
+    return list(ws)
+
+
 def clear_weight_caches() -> None:
     """Drop every derived copy of a weight that the ops keep (the repacked L1/L2/L3
     weights and the RoPE-pair K weights of fused decoder layers), so that the next call
@@ -754,6 +798,10 @@ def _run(x: torch.Tensor, ws: list[torch.Tensor], tiled: bool, kind: str, gelu: 
          norm=None, residual=None, warm=None):
     k = _check_x(x)
     n_e3m2 = sum(1 for w in ws if is_e3m2_layout(w, k))
+    if n_e3m2 == len(ws) and x.numel() // k <= E3M2_MAX_INT4_ROWS:
+        twins = gemm_weights_for_rows(ws, k, x.numel() // k)
+        if twins[0] is not ws[0]:  # small M on INT4 twins
+            ws, n_e3m2 = twins, 0
     if n_e3m2:
         return _run_e3m2(x, ws, k, n_e3m2, kind, gelu, norm, residual, warm=warm)
     if residual is not None:  # before any launch: the kernel reads it through a raw pointer

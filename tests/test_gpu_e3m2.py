@@ -243,3 +243,42 @@ def test_forward_e3m2_equals_int4(cuda, monkeypatch):
         del model
     torch.cuda.synchronize()
     assert _same_f16(outs[1], outs[0])
+
+
+@pytest.mark.parametrize("m", [1, 64, 128, 129, 776])
+def test_gate_up_loaded_weights_run_int4_twins_at_few_rows(ext, cuda, monkeypatch, m):
+    """The loader gives the MLP's gate/up weights the E3M2 form and registers their INT4
+    form as its twin: calls of at most E3M2_MAX_INT4_ROWS rows run the INT4 kernels on the
+    twins, larger ones the E3M2 kernels; the fp16 outputs equal the INT4-only weights' bit
+    for bit either way (plain pair and GELU-tanh*up)."""
+    from pi05_fast.w4a4 import apply
+
+    k, n = 2048, 1024
+    gen = inp.generator(7100 + m)
+    x = inp.activations(gen, m, k).to(cuda)
+    wg_ref, wu_ref = inp.packed_weight(gen, n, k), inp.packed_weight(gen, n, k)
+    wg, _ = apply.load_time_weight(wg_ref, "model.layers.0.mlp.gate_proj", k, n, cuda)
+    wu, _ = apply.load_time_weight(wu_ref, "model.layers.0.mlp.up_proj", k, n, cuda)
+    assert ext.is_e3m2_layout(wg, k) and ext.is_e3m2_layout(wu, k)
+    assert ext.is_mfma_layout(ext.int4_twin(wg, k), k) and ext.is_mfma_layout(ext.int4_twin(wu, k), k)
+    wg4, wu4 = ext.repack_weight(wg_ref.to(cuda)), ext.repack_weight(wu_ref.to(cuda))
+    calls = {"e3m2": 0}
+    real = ext._run_e3m2
+
+    def counting(*a, **kw):
+        calls["e3m2"] += 1
+        return real(*a, **kw)
+
+    monkeypatch.setattr(ext, "_run_e3m2", counting)
+    y = ext.int4_gemm2_gelu(x, wg, wu)
+    g, u = ext.int4_gemm2(x, wg, wu)
+    y_ref = ext.int4_gemm2_gelu(x, wg4, wu4)
+    g_ref, u_ref = ext.int4_gemm2(x, wg4, wu4)
+    torch.cuda.synchronize()
+    assert _same_f16(y, y_ref) and _same_f16(g, g_ref) and _same_f16(u, u_ref)
+    assert calls["e3m2"] == (0 if m <= ext.E3M2_MAX_INT4_ROWS else 2)
+    # an in-place write to the E3M2 weight retires its twin: the call runs on E3M2 weights
+    wg.add_(0)
+    calls["e3m2"] = 0
+    ext.int4_gemm2_gelu(x, wg, wu)
+    assert calls["e3m2"] == 1

@@ -843,3 +843,33 @@ def test_e3m2_abi_validation_without_gpu(lib):
     assert b"K = 2048" in lib.pi05w4a4_last_error()
     assert lib.pi05w4a4_repack_weight_e3m2(16, 64, 2048, 16, None) != 0  # in place
     assert lib.pi05w4a4_gemm_e3m2(16, 16, 0, 2048, 2, w, n3, y, 0, None) == 0  # M = 0: nothing to do
+
+
+def test_int4_twin_registry():
+    """register_int4_twin / int4_twin / gemm_weights_for_rows on CPU tensors of the two
+    layouts' shapes: the twin is served while its E3M2 weight is unchanged, for at most
+    E3M2_MAX_INT4_ROWS rows; an in-place write or a freed weight retires it."""
+    import gc
+
+    from pi05_fast.w4a4 import extension as ext
+
+    k, n = 2048, 64
+    w6 = torch.zeros(n, 3 * k // 16 + ext.E3M2_MARKER_WORDS, dtype=torch.int32)
+    w4 = torch.zeros(n, k // 8 + ext.MFMA_MARKER_WORDS, dtype=torch.int32)
+    assert ext.int4_twin(w6, k) is None
+    ext.register_int4_twin(w6, w4, k)
+    assert ext.int4_twin(w6, k) is w4
+    assert ext.int4_twin(w6, 1024) is None
+    rows = ext.E3M2_MAX_INT4_ROWS
+    assert ext.gemm_weights_for_rows([w6], k, rows)[0] is w4
+    assert ext.gemm_weights_for_rows([w6], k, rows + 1)[0] is w6
+    other = torch.zeros_like(w6)  # no twin: the call keeps its E3M2 weights
+    assert ext.gemm_weights_for_rows([w6, other], k, 1)[1] is other
+    with pytest.raises(RuntimeError):
+        ext.register_int4_twin(w4, w6, k)
+    w6.add_(1)
+    assert ext.int4_twin(w6, k) is None
+    key = id(w6)
+    del w6
+    gc.collect()
+    assert key not in ext._INT4_TWINS
