@@ -150,6 +150,15 @@ Plan make_plan(int64_t m, int32_t k, int ngroups, const int32_t* n, bool gelu, b
     pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
     pl.ntiles = count_tiles(pl.cfg);
   }
+  // The QKV + RoPE launch keeps the 64 x 64 K-split tiles at large M too: the attention
+  // prep epilogue of its K and V tiles runs long on 112-row tiles (batch 8 x 776 tokens:
+  // forward 14.36-14.38 -> 14.24-14.25 ms; the plain o GEMM measured slower on them there,
+  // 25.6 -> 39.7 us, and keeps 112 x 256 tiles).
+  if (rope && pl.cfg.id == w4a4::kCfg7x4 && cdiv(m, 64) * count_tiles(kCfg4x4K4) >= kNumCUs) {
+    pl.cfg = kCfg4x4K4;
+    pl.mtiles = cdiv(m, 16 * pl.cfg.mi);
+    pl.ntiles = count_tiles(pl.cfg);
+  }
   const int nkb = w4a4::kblocks128(k);
   int ks = 1;
   if (allow_split) {

@@ -45,9 +45,9 @@ def _rope_tables(gen, b, s, cuda):
     return emb.cos().half().to(cuda), emb.sin().half().to(cuda)
 
 
-# Tile layouts reached (capi.hip make_plan, N = 2560, 256 CUs): 7x4 at 8 x 776 (M = 6208);
-# 7x4K4 (four waves split K, reduce-scatter before the RoPE / V^T epilogue) at 3 x 776;
-# 4x4K4 (64 x 64, four waves split K) at 1 x 776; 4x2 at 2 x 776, 1 x 1000 and 1 x 1024;
+# Tile layouts reached (capi.hip make_plan, N = 2560, 256 CUs): 7x4K4 (four waves split K,
+# reduce-scatter before the RoPE / V^T epilogue) at 3 x 776; 4x4K4 (64 x 64, four waves
+# split K) at 1 x 776 and 8 x 776 (M = 6208); 4x2 at 2 x 776, 1 x 1000 and 1 x 1024;
 # 2x2 at 3 x 24 and 2 x 40; the small-M K-split tiles 1x2K4 at 1 x 8, 2x2K4 at 1 x 24 and
 # 4 x 8, 4x2K4 at 1 x 64.
 CASES = [(1, 776), (2, 776), (8, 776), (3, 776), (1, 8), (1, 24), (4, 8), (3, 24), (1, 64), (2, 40), (1, 1000),
