@@ -475,7 +475,9 @@ _CACHE_CLEARERS: list = []
 # GEMM has no small-M tiles (gate/up + GELU at 1-128 rows: 17-18 us on E3M2 weights
 # against 6-12 us on INT4 ones; from 160 rows on E3M2 is faster).  An entry lives as long
 # as its E3M2 weight and is ignored once that weight is modified in place (version or data
-# pointer moved): the call then runs on the E3M2 weight.
+# pointer moved): the call then runs on the E3M2 weight.  A write through ``w.data`` moves
+# neither: clear_weight_caches() then drops every twin (and the calls run on the E3M2
+# weights, correct and slower at few rows).
 E3M2_MAX_INT4_ROWS = 128
 _INT4_TWINS: dict[int, tuple] = {}
 
@@ -515,10 +517,13 @@ def gemm_weights_for_rows(ws: list[torch.Tensor], k: int, m: int) -> list[torch.
 
 def clear_weight_caches() -> None:
     """Drop every derived copy of a weight that the ops keep (the repacked L1/L2/L3
-    weights and the RoPE-pair K weights of fused decoder layers), so that the next call
-    rebuilds them from the current weights.  Needed after writing a weight in place
-    through ``.data`` (which bypasses the version counter the caches check)."""
+    weights, the RoPE-pair K weights of fused decoder layers and the INT4 twins of E3M2
+    weights), so that the next call rebuilds them from the current weights (a twin is not
+    rebuilt: calls on its E3M2 weight run the E3M2 kernels).  Needed after writing a
+    weight in place through ``.data`` (which bypasses the version counter the caches
+    check)."""
     _MFMA_CACHE.clear()
+    _INT4_TWINS.clear()
     for fn in _CACHE_CLEARERS:
         fn()
 

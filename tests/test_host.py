@@ -867,6 +867,11 @@ def test_int4_twin_registry():
     assert ext.gemm_weights_for_rows([w6, other], k, 1)[1] is other
     with pytest.raises(RuntimeError):
         ext.register_int4_twin(w4, w6, k)
+    w6b = torch.zeros_like(w6)  # clear_weight_caches() drops the twins too
+    ext.register_int4_twin(w6b, w4, k)
+    ext.clear_weight_caches()
+    assert ext.int4_twin(w6b, k) is None
+    ext.register_int4_twin(w6, w4, k)
     w6.add_(1)
     assert ext.int4_twin(w6, k) is None
     key = id(w6)
